@@ -1,0 +1,242 @@
+/*
+ * parakeet_paged.h -- C ABI of the MI355X (gfx950) paged KV-cache hot path for
+ * cache-aware FastConformer streaming.
+ *
+ * Every entry point takes plain pointers, sizes and element strides; no torch
+ * types cross this boundary.  Device pointers are raw HIP device addresses
+ * (a torch tensor's data_ptr()), `stream` is a hipStream_t (torch's
+ * current_stream().cuda_stream).  Calls return PK_OK (0) or a negative PK_ERR_*
+ * code; pk_last_error() then holds a message for the calling thread.  No C++
+ * exception crosses the ABI.  The library never allocates device memory and keeps
+ * no device pointer past a call.
+ *
+ * Paged layout shared by the kernels (pk_paged_layout):
+ *   k_pool, v_pool : [num_layers][num_pages][page_size][d_model] of `dtype`
+ *   rows           : int32 [batch][rows_stride], one row per stream of the batch:
+ *                    rows[b][0]     = frames appended to stream b before this step (A)
+ *                    rows[b][1 + r] = page id held in ring entry r, -1 if none,
+ *                                     r in [0, max_pages)
+ *   Frame position p of a stream (its p-th appended frame) lives in page
+ *   rows[b][1 + (p / page_size) % max_pages] at row p % page_size.
+ * The dense window a kernel sees for stream b after appending this step's
+ * `chunk` frames is positions [A + chunk - window, A + chunk); positions < 0
+ * read as zeros (the reference zeroes a slot before use).
+ */
+#ifndef PARAKEET_PAGED_H
+#define PARAKEET_PAGED_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PK_ABI_VERSION 1
+
+enum pk_dtype { PK_DTYPE_F32 = 0, PK_DTYPE_F16 = 1, PK_DTYPE_BF16 = 2 };
+
+#define PK_OK 0
+#define PK_ERR_INVALID (-1)     /* bad argument: shape, stride, pointer, range */
+#define PK_ERR_UNSUPPORTED (-2) /* valid but not built: e.g. head_dim not 64/128 */
+#define PK_ERR_EXHAUSTED (-3)   /* page pool has no page for a reserved slot */
+#define PK_ERR_HIP (-4)         /* a HIP runtime call failed */
+#define PK_ERR_STATE (-5)       /* call out of order: e.g. a slot twice in one step */
+
+typedef struct pk_paged_layout {
+  void* k_pool;
+  void* v_pool;
+  int32_t num_layers;
+  int32_t num_pages;
+  int32_t page_size; /* frames per page, power of two */
+  int32_t d_model;
+  const int32_t* rows;
+  int32_t rows_stride; /* int32 elements between consecutive rows */
+  int32_t max_pages;   /* ring entries per stream */
+} pk_paged_layout;
+
+/* ---------------------------------------------------------------------------
+ * pk_kv_append -- write this step's `chunk` new K and V frames of every stream
+ * into its pages at positions [A, A + chunk).
+ * Replaces ModelCache.update_attn_cache, the tail write
+ *   parakeet/modules/cache.py:43-44  (attn_k[:, l, left:].copy_(key), same for V)
+ * and, together with the host page pool, the window shift cache.py:37-42.
+ * key/value: [batch][chunk][d_model] with element strides (stride_b, stride_t),
+ * last dimension contiguous (the views qkv.chunk(3) makes, attention.py:94-95).
+ */
+typedef struct pk_kv_append_args {
+  int32_t dtype;
+  int32_t device;
+  pk_paged_layout pages;
+  int32_t layer;
+  int32_t batch;
+  int32_t chunk;
+  const void* key;
+  int64_t key_stride_b;
+  int64_t key_stride_t;
+  const void* value;
+  int64_t value_stride_b;
+  int64_t value_stride_t;
+} pk_kv_append_args;
+int pk_kv_append(const pk_kv_append_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * pk_kv_gather -- materialise the dense window [batch][window][d_model] of K
+ * and V from the pages, positions [A + end_offset - window, A + end_offset),
+ * zero for positions < 0.  Bit-exact copy of what the reference returns from
+ *   parakeet/modules/cache.py:45  (attn_k[:, l], attn_v[:, l])
+ * after update_attn_cache when end_offset == chunk.
+ */
+typedef struct pk_kv_gather_args {
+  int32_t dtype;
+  int32_t device;
+  pk_paged_layout pages;
+  int32_t layer;
+  int32_t batch;
+  int32_t window;
+  int32_t end_offset;
+  void* out_k;
+  int64_t out_k_stride_b;
+  int64_t out_k_stride_t;
+  void* out_v;
+  int64_t out_v_stride_b;
+  int64_t out_v_stride_t;
+} pk_kv_gather_args;
+int pk_kv_gather(const pk_kv_gather_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * pk_paged_relpos_attn -- fused page append + relative-position multi-head
+ * attention (Transformer-XL form with pos_bias_u / pos_bias_v) over each
+ * stream's window read straight from its pages.
+ * Replaces parakeet/modules/attention.py:97-121 (ConformerAttention.forward from
+ * update_attn_cache through sdpa_attention_forward, incl. rel_shift :79-83,
+ * masked_fill :115 and SDPA :9-20); the qkv / linear_pos / linear_out GEMMs stay
+ * with the caller.
+ * For query i (0..chunk-1) and window key j (0..window-1, window = left + chunk):
+ *   s = ((q_i + u_h).k_j + (q_i + v_h).pos[j + chunk - 1 - i]) / sqrt(head_dim)
+ *   s = (q_i + u_h).k_j / sqrt(head_dim) - 1e5          where mask[b,h,i,j] != 0
+ *   out_i = sum_j softmax_j(s) v_j            (fp32 accumulation)
+ * Keys j >= left are this step's frames, read from key/value; keys j < left come
+ * from the pages.  With append != 0 the new frames are also written to the pages
+ * (pk_kv_append fused).  left == 0 with k_pool == NULL attends over the chunk only
+ * (cache=None in the reference).
+ * query/key/value: [batch][chunk][num_heads*head_dim], strides (b, t), last dim
+ * contiguous.  pos: [pos_rows][num_heads*head_dim], row stride pos_stride; needs
+ * pos_rows >= window + chunk - 1.  bias_u/bias_v: [num_heads][head_dim]
+ * contiguous.  mask: uint8/bool [batch][heads][chunk][window] with element
+ * strides (b, h, t) and unit stride along window (mask_stride_h 0 broadcasts a
+ * [batch][chunk][window] mask), or NULL for no mask.  out: [batch][chunk][d_model].
+ * All floating tensors share `dtype`.  head_dim must be 64 or 128.
+ * start_event/stop_event: optional hipEvent_t pair timing this kernel alone.
+ */
+typedef struct pk_attn_args {
+  int32_t dtype;
+  int32_t device;
+  pk_paged_layout pages;
+  int32_t layer;
+  int32_t batch;
+  int32_t chunk;
+  int32_t num_heads;
+  int32_t head_dim;
+  int32_t left;
+  int32_t append;
+  const void* query;
+  int64_t query_stride_b;
+  int64_t query_stride_t;
+  const void* key;
+  int64_t key_stride_b;
+  int64_t key_stride_t;
+  const void* value;
+  int64_t value_stride_b;
+  int64_t value_stride_t;
+  const void* pos;
+  int64_t pos_stride;
+  int32_t pos_rows;
+  const void* bias_u;
+  const void* bias_v;
+  const uint8_t* mask;
+  int64_t mask_stride_b;
+  int64_t mask_stride_h;
+  int64_t mask_stride_t;
+  void* out;
+  int64_t out_stride_b;
+  int64_t out_stride_t;
+  int32_t rows_per_lane; /* tuning: key rows per lane per tile, 0 = automatic */
+  void* start_event;
+  void* stop_event;
+} pk_attn_args;
+int pk_paged_relpos_attn(const pk_attn_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * pk_streaming_mask -- device-side construction of the streaming attention and
+ * padding masks for a batch, bit-exact with the reference's per-stream loop
+ *   parakeet/modules/encoder.py:167-227 (ConformerEncoder._create_streaming_masks)
+ * att_mask: uint8 [batch][chunk][left + chunk] (1 = masked); pad_mask: uint8
+ * [batch][chunk] (1 = padded query).  processed_frames, cache_lengths, lengths:
+ * int64 [batch] contiguous device arrays; lengths may be NULL, then every
+ * stream uses length_scalar.  chunk_size is att_context_size[1] + 1 and
+ * left_chunks = left / chunk_size.  Requires 0 <= cache_lengths <= left (the
+ * reference clamps it, encoder.py:260).
+ */
+typedef struct pk_mask_args {
+  int32_t device;
+  int32_t batch;
+  int32_t chunk;
+  int32_t left;
+  int32_t chunk_size;
+  const int64_t* processed_frames;
+  const int64_t* cache_lengths;
+  const int64_t* lengths;
+  int64_t length_scalar;
+  uint8_t* att_mask;
+  uint8_t* pad_mask;
+} pk_mask_args;
+int pk_streaming_mask(const pk_mask_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Host page pool: FIFO free-page queue and per-slot page rings.  Thread safe
+ * (one internal mutex, the counterpart of Scheduler._state_lock,
+ * parakeet/engine/scheduler.py:26,94-97,103-104).  Host memory only.
+ *
+ * pk_pool_create   -- replaces the slot-pool construction
+ *                     parakeet/engine/scheduler.py:68-84 and the dense buffers of
+ *                     ModelCache.__init__ parakeet/modules/cache.py:8-34.  Pages are
+ *                     handed out in `page_order` (NULL: 0..num_pages-1), freed pages
+ *                     go to the back (deque discipline of scheduler.py:84,97,104).
+ *                     Requires num_pages >= num_slots * max_pages, so every slot's
+ *                     window can always be held (no allocation can fail mid-step).
+ * pk_pool_advance  -- opens one step for `n` slots: frees the pages that fell out of
+ *                     each window (sliding-window eviction, the shift of
+ *                     cache.py:37-42), allocates pages for positions [A, A+chunk),
+ *                     writes rows_out[b] = {A, ring[0..max_pages-1]} and advances A by
+ *                     chunk.  Slots are processed in the given order.  Replaces the
+ *                     per-step batch gather of Scheduler.pack_states
+ *                     scheduler.py:128-170 (a block-table row replaces the dense
+ *                     state copy).
+ * pk_pool_reset_slot / pk_pool_reset_all -- free every page of a slot and set A = 0:
+ *                     replaces ModelCache.reset_slot / reset cache.py:55-63 as used
+ *                     by Scheduler._reset_state scheduler.py:86-91.
+ * pk_pool_slot_info, pk_pool_free_list, pk_pool_free_pages -- inspection for
+ *                     parity tests (free queue in FIFO order).
+ */
+typedef struct pk_pool pk_pool;
+int pk_pool_create(int32_t num_pages, int32_t num_slots, int32_t page_size, int32_t left,
+                   int32_t chunk, const int32_t* page_order, pk_pool** out);
+void pk_pool_destroy(pk_pool* pool);
+int pk_pool_max_pages(const pk_pool* pool);
+int pk_pool_advance(pk_pool* pool, int32_t n, const int32_t* slots, int32_t* rows_out,
+                    int32_t rows_stride);
+int pk_pool_reset_slot(pk_pool* pool, int32_t slot);
+int pk_pool_reset_all(pk_pool* pool);
+int pk_pool_free_pages(const pk_pool* pool);
+int pk_pool_slot_info(const pk_pool* pool, int32_t slot, int64_t* appended, int32_t* ring_out);
+int pk_pool_free_list(const pk_pool* pool, int32_t* out, int32_t capacity);
+
+/* Message for the last failed call on this thread ("" if none). */
+const char* pk_last_error(void);
+int pk_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PARAKEET_PAGED_H */

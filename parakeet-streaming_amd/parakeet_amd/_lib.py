@@ -1,0 +1,196 @@
+"""ctypes binding of ``libparakeet_paged.so`` (declared in ``include/parakeet_paged.h``).
+
+The library is built in-tree by ``parakeet-streaming_amd/build.py``.  Loading it
+never touches the GPU; the kernels run only when a launch entry point is called.
+There is no fallback: if the library is missing, :func:`lib` raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from ctypes import POINTER, c_char_p, c_int, c_int32, c_int64, c_void_p
+from pathlib import Path
+
+LIB_NAME = "libparakeet_paged.so"
+LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
+
+ABI_VERSION = 1
+
+DTYPE_F32 = 0
+DTYPE_F16 = 1
+DTYPE_BF16 = 2
+
+PK_OK = 0
+PK_ERR_INVALID = -1
+PK_ERR_UNSUPPORTED = -2
+PK_ERR_EXHAUSTED = -3
+PK_ERR_HIP = -4
+PK_ERR_STATE = -5
+
+
+class PagedLayout(ctypes.Structure):
+    _fields_ = [
+        ("k_pool", c_void_p),
+        ("v_pool", c_void_p),
+        ("num_layers", c_int32),
+        ("num_pages", c_int32),
+        ("page_size", c_int32),
+        ("d_model", c_int32),
+        ("rows", c_void_p),
+        ("rows_stride", c_int32),
+        ("max_pages", c_int32),
+    ]
+
+
+class KvAppendArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", c_int32),
+        ("device", c_int32),
+        ("pages", PagedLayout),
+        ("layer", c_int32),
+        ("batch", c_int32),
+        ("chunk", c_int32),
+        ("key", c_void_p),
+        ("key_stride_b", c_int64),
+        ("key_stride_t", c_int64),
+        ("value", c_void_p),
+        ("value_stride_b", c_int64),
+        ("value_stride_t", c_int64),
+    ]
+
+
+class KvGatherArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", c_int32),
+        ("device", c_int32),
+        ("pages", PagedLayout),
+        ("layer", c_int32),
+        ("batch", c_int32),
+        ("window", c_int32),
+        ("end_offset", c_int32),
+        ("out_k", c_void_p),
+        ("out_k_stride_b", c_int64),
+        ("out_k_stride_t", c_int64),
+        ("out_v", c_void_p),
+        ("out_v_stride_b", c_int64),
+        ("out_v_stride_t", c_int64),
+    ]
+
+
+class AttnArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", c_int32),
+        ("device", c_int32),
+        ("pages", PagedLayout),
+        ("layer", c_int32),
+        ("batch", c_int32),
+        ("chunk", c_int32),
+        ("num_heads", c_int32),
+        ("head_dim", c_int32),
+        ("left", c_int32),
+        ("append", c_int32),
+        ("query", c_void_p),
+        ("query_stride_b", c_int64),
+        ("query_stride_t", c_int64),
+        ("key", c_void_p),
+        ("key_stride_b", c_int64),
+        ("key_stride_t", c_int64),
+        ("value", c_void_p),
+        ("value_stride_b", c_int64),
+        ("value_stride_t", c_int64),
+        ("pos", c_void_p),
+        ("pos_stride", c_int64),
+        ("pos_rows", c_int32),
+        ("bias_u", c_void_p),
+        ("bias_v", c_void_p),
+        ("mask", c_void_p),
+        ("mask_stride_b", c_int64),
+        ("mask_stride_h", c_int64),
+        ("mask_stride_t", c_int64),
+        ("out", c_void_p),
+        ("out_stride_b", c_int64),
+        ("out_stride_t", c_int64),
+        ("rows_per_lane", c_int32),
+        ("start_event", c_void_p),
+        ("stop_event", c_void_p),
+    ]
+
+
+class MaskArgs(ctypes.Structure):
+    _fields_ = [
+        ("device", c_int32),
+        ("batch", c_int32),
+        ("chunk", c_int32),
+        ("left", c_int32),
+        ("chunk_size", c_int32),
+        ("processed_frames", c_void_p),
+        ("cache_lengths", c_void_p),
+        ("lengths", c_void_p),
+        ("length_scalar", c_int64),
+        ("att_mask", c_void_p),
+        ("pad_mask", c_void_p),
+    ]
+
+
+# name -> (restype, argtypes); exactly the functions include/parakeet_paged.h declares
+SIGNATURES = {
+    "pk_kv_append": (c_int, [POINTER(KvAppendArgs), c_void_p]),
+    "pk_kv_gather": (c_int, [POINTER(KvGatherArgs), c_void_p]),
+    "pk_paged_relpos_attn": (c_int, [POINTER(AttnArgs), c_void_p]),
+    "pk_streaming_mask": (c_int, [POINTER(MaskArgs), c_void_p]),
+    "pk_pool_create": (
+        c_int,
+        [c_int32, c_int32, c_int32, c_int32, c_int32, POINTER(c_int32), POINTER(c_void_p)],
+    ),
+    "pk_pool_destroy": (None, [c_void_p]),
+    "pk_pool_max_pages": (c_int, [c_void_p]),
+    "pk_pool_advance": (c_int, [c_void_p, c_int32, POINTER(c_int32), POINTER(c_int32), c_int32]),
+    "pk_pool_reset_slot": (c_int, [c_void_p, c_int32]),
+    "pk_pool_reset_all": (c_int, [c_void_p]),
+    "pk_pool_free_pages": (c_int, [c_void_p]),
+    "pk_pool_slot_info": (c_int, [c_void_p, c_int32, POINTER(c_int64), POINTER(c_int32)]),
+    "pk_pool_free_list": (c_int, [c_void_p, POINTER(c_int32), c_int32]),
+    "pk_last_error": (c_char_p, []),
+    "pk_abi_version": (c_int, []),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def lib() -> ctypes.CDLL:
+    """Loads the library once; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(
+                    f"{LIB_PATH} is missing: build it with parakeet-streaming_amd/build.py "
+                    "(the paged KV-cache path has no non-HIP fallback)"
+                )
+            handle = ctypes.CDLL(str(LIB_PATH))
+            for name, (restype, argtypes) in SIGNATURES.items():
+                fn = getattr(handle, name)
+                fn.restype = restype
+                fn.argtypes = argtypes
+            version = handle.pk_abi_version()
+            if version != ABI_VERSION:
+                raise RuntimeError(f"{LIB_PATH}: ABI version {version}, expected {ABI_VERSION}")
+            _lib = handle
+    return _lib
+
+
+def last_error() -> str:
+    msg = lib().pk_last_error()
+    return msg.decode("utf-8", "replace") if msg else ""
+
+
+def check(rc: int, what: str) -> int:
+    """Raises RuntimeError for a negative return code (the reference raises
+    RuntimeError for unusable state, parakeet/engine/scheduler.py:112,132)."""
+    if rc < 0:
+        raise RuntimeError(f"{what} failed ({rc}): {last_error()}")
+    return rc

@@ -1,0 +1,12 @@
+from .attention import ConformerAttention, PositionalEncoding
+from .cache import ModelCache, StreamingState
+from .encoder import ConformerEncoder, ConformerLayer
+
+__all__ = [
+    "ConformerAttention",
+    "PositionalEncoding",
+    "ModelCache",
+    "StreamingState",
+    "ConformerEncoder",
+    "ConformerLayer",
+]

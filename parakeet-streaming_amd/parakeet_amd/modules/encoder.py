@@ -1,0 +1,235 @@
+"""Drop-in for the streaming parts of ``parakeet.modules.encoder``
+(parakeet/modules/encoder.py).
+
+* ``init_streaming_state`` builds the paged :class:`ModelCache`
+  (encoder.py:140-165);
+* ``_create_streaming_masks`` is one HIP launch for the whole batch instead of
+  a per-stream Python loop with two device->host syncs per stream
+  (encoder.py:167-227);
+* ``forward`` keeps the layer loop and the state advance (encoder.py:229-267);
+  the attention of every layer runs on the paged cache.
+
+The feed-forward, layer-norm and convolution blocks are plain torch modules with
+the reference's parameter names (encoder.py:11-81, convolution.py:8-52,107-162,
+feedforward.py:4-26); the convolution subsampling front end (``pre_encode``) is
+not part of this package.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import Tensor, nn
+from torch.nn import functional as F
+
+from .. import ops
+from .attention import ConformerAttention, PositionalEncoding
+from .cache import ModelCache, StreamingState
+
+
+class ConformerFeedForward(nn.Module):
+    def __init__(self, hidden_size: int, d_ff: int, dropout: float, use_bias: bool = True):
+        super().__init__()
+        self.d_model = hidden_size
+        self.d_ff = d_ff
+        self.use_bias = use_bias
+        self.linear1 = nn.Linear(hidden_size, d_ff, bias=use_bias)
+        self.activation = nn.SiLU()
+        self.linear2 = nn.Linear(d_ff, hidden_size, bias=use_bias)
+        self.dropout = nn.Dropout(dropout)
+
+    def forward(self, x: Tensor) -> Tensor:
+        return self.linear2(self.dropout(self.activation(self.linear1(x))))
+
+
+class CausalConv1d(nn.Conv1d):
+    """Depthwise conv whose left context comes from a per-stream cache of
+    kernel_size-1 frames (parakeet/modules/convolution.py:8-52)."""
+
+    def __init__(self, in_channels, out_channels, kernel_size, stride=1, padding=(0, 0), dilation=1, groups=1, bias=True):
+        self._left_padding = padding[0]
+        self._right_padding = padding[1]
+        super().__init__(in_channels, out_channels, kernel_size, stride=stride, padding=0, dilation=dilation, groups=groups, bias=bias)
+
+    def forward(self, x: Tensor, cache: Tensor | None = None):
+        B, C, _ = x.shape
+        if cache is None:
+            cache = torch.zeros(B, C, self.kernel_size[0] - 1, device=x.device, dtype=x.dtype)
+        x = torch.cat([cache, F.pad(x, pad=(0, self._right_padding))], dim=-1)
+        next_cache = x[:, :, -cache.size(-1) :]
+        return super().forward(x), next_cache
+
+
+class ConformerConvolution(nn.Module):
+    def __init__(self, hidden_size, kernel_size, use_bias=False):
+        super().__init__()
+        self.d_model = hidden_size
+        self.kernel_size = kernel_size
+        self.pointwise_conv1 = nn.Conv1d(hidden_size, hidden_size * 2, kernel_size=1, bias=use_bias)
+        self.depthwise_conv = CausalConv1d(
+            hidden_size, hidden_size, kernel_size, groups=hidden_size, padding=(kernel_size - 1, 0), bias=use_bias
+        )
+        self.batch_norm = nn.LayerNorm(hidden_size)
+        self.activation = nn.SiLU()
+        self.pointwise_conv2 = nn.Conv1d(hidden_size, hidden_size, kernel_size=1, bias=use_bias)
+
+    def forward(self, x: Tensor, pad_mask: Tensor, cache: Tensor | None = None):
+        x = F.glu(self.pointwise_conv1(x.transpose(1, 2)), dim=1)
+        x = x.masked_fill(pad_mask.unsqueeze(1), 0.0)
+        x, cache = self.depthwise_conv(x, cache=cache)
+        x = self.batch_norm(x.transpose(1, 2)).transpose(1, 2)
+        x = self.pointwise_conv2(self.activation(x))
+        return x.transpose(1, 2), cache
+
+
+class ConformerLayer(nn.Module):
+    """FF/2 -> rel-pos MHA -> conv -> FF/2 -> LN (parakeet/modules/encoder.py:11-81)."""
+
+    def __init__(self, layer_idx, hidden_size, d_ff, num_heads, dropout, conv_kernel_size, use_bias):
+        super().__init__()
+        self.layer_idx = layer_idx
+        self.hidden_size = hidden_size
+        self.norm_feed_forward1 = nn.LayerNorm(hidden_size)
+        self.feed_forward1 = ConformerFeedForward(hidden_size, d_ff, dropout, use_bias)
+        self.norm_conv = nn.LayerNorm(hidden_size)
+        self.conv = ConformerConvolution(hidden_size, conv_kernel_size)
+        self.norm_self_att = nn.LayerNorm(hidden_size)
+        self.self_attn = ConformerAttention(layer_idx=layer_idx, hidden_size=hidden_size, num_heads=num_heads, use_bias=use_bias)
+        self.norm_feed_forward2 = nn.LayerNorm(hidden_size)
+        self.feed_forward2 = ConformerFeedForward(hidden_size, d_ff, dropout, use_bias)
+        self.norm_out = nn.LayerNorm(hidden_size)
+
+    def forward(self, x: Tensor, pos_emb: Tensor, pad_mask: Tensor, attn_mask: Tensor, cache: ModelCache):
+        residual = x
+        residual = residual + 0.5 * self.feed_forward1(self.norm_feed_forward1(residual))
+        residual = residual + self.self_attn(self.norm_self_att(residual), pos_emb, attn_mask=attn_mask, cache=cache)
+        conv_out, conv_cache = self.conv(
+            self.norm_conv(residual), pad_mask=pad_mask, cache=cache.get_conv_cache(self.layer_idx)
+        )
+        cache.update_conv_cache(self.layer_idx, conv_cache)
+        residual = residual + conv_out
+        residual = residual + 0.5 * self.feed_forward2(self.norm_feed_forward2(residual))
+        return self.norm_out(residual)
+
+
+class ConformerEncoder(nn.Module):
+    """Streaming FastConformer encoder stack on the paged cache
+    (parakeet/modules/encoder.py:84-267); same constructor arguments."""
+
+    def __init__(
+        self,
+        feat_in: int,
+        hidden_size,
+        ff_expansion_factor: int,
+        num_layers: int,
+        num_heads: int,
+        subsampling_factor: int,
+        pos_emb_max_len: int,
+        conv_kernel_size: int,
+        att_context_size,
+        subsampling_conv_channels: int,
+        use_bias: bool,
+        pre_encode_cache_size: list | tuple = (0, 9),
+        drop_extra_pre_encoded: int = 2,
+        page_size: int = 16,
+    ):
+        super().__init__()
+        self.embed_dim = hidden_size
+        self.feat_in = feat_in
+        self.subsampling_factor = subsampling_factor
+        self.pre_encode = None
+        self.pos_enc = PositionalEncoding(hidden_size=hidden_size, dropout_rate_emb=0.0, max_len=pos_emb_max_len, dropout=0.0)
+        self.layers = nn.ModuleList(
+            ConformerLayer(i, hidden_size, hidden_size * ff_expansion_factor, num_heads, 0.0, conv_kernel_size, use_bias)
+            for i in range(num_layers)
+        )
+        self.pos_enc.extend_pe(pos_emb_max_len, device=next(self.parameters()).device)
+        self.att_context_size = list(att_context_size)
+        self.conv_kernel_size = conv_kernel_size
+        self.pre_encode_cache_size = pre_encode_cache_size
+        self.drop_extra_pre_encoded = drop_extra_pre_encoded
+        self.page_size = page_size
+
+    def init_streaming_state(
+        self,
+        batch_size: int = 1,
+        device: torch.device | None = None,
+        dtype: torch.dtype | None = None,
+        **cache_kwargs,
+    ) -> StreamingState:
+        if device is None:
+            device = next(self.parameters()).device
+        if dtype is None:
+            dtype = next(self.parameters()).dtype
+        cache_kwargs.setdefault("page_size", self.page_size)
+        cache = ModelCache(
+            num_layers=len(self.layers),
+            attn_context_size=self.att_context_size,
+            embed_dim=self.embed_dim,
+            conv_kernel_size=self.conv_kernel_size,
+            batch_size=batch_size,
+            device=device,
+            dtype=dtype,
+            **cache_kwargs,
+        )
+        return StreamingState(
+            cache=cache,
+            processed_frames=torch.zeros(batch_size, dtype=torch.int64, device=device),
+            cache_lengths=torch.zeros(batch_size, dtype=torch.int64, device=device),
+        )
+
+    def _create_streaming_masks(
+        self,
+        current_len: int,
+        cache_lengths: Tensor,
+        processed_frames: Tensor,
+        device: torch.device,
+        lengths: Tensor | int,
+    ):
+        """(pad_mask [B, T], att_mask [B, T, left+T]) from one kernel launch."""
+        batch = cache_lengths.shape[0]
+
+        def as_state(v):
+            if isinstance(v, Tensor):
+                return v.to(device=device, dtype=torch.int64).contiguous()
+            return torch.full((batch,), int(v), dtype=torch.int64, device=device)
+
+        if lengths is None:
+            raise ValueError("lengths is required (the reference compares against it, encoder.py:204)")
+        lengths = as_state(lengths) if isinstance(lengths, Tensor) else int(lengths)
+        return ops.streaming_mask(
+            as_state(processed_frames),
+            as_state(cache_lengths),
+            lengths,
+            chunk=current_len,
+            left=self.att_context_size[0],
+            chunk_size=self.att_context_size[1] + 1,
+        )
+
+    def forward(self, x: Tensor, state: StreamingState, length: Tensor | None = None, bypass_pre_encode: bool = False):
+        cache_lengths = state.cache_lengths
+        if not isinstance(cache_lengths, Tensor):
+            cache_lengths = torch.full((x.size(0),), int(cache_lengths), dtype=torch.int64, device=x.device)
+        processed = state.processed_frames
+        if not isinstance(processed, Tensor):
+            processed = torch.full((x.size(0),), int(processed), dtype=torch.int64, device=x.device)
+        x, pos_emb = self.pos_enc(x, cache_len=self.att_context_size[0])
+        pad_mask, att_mask = self._create_streaming_masks(
+            current_len=x.size(1),
+            cache_lengths=cache_lengths,
+            processed_frames=processed,
+            device=x.device,
+            lengths=length,
+        )
+        for layer in self.layers:
+            x = layer(x, pos_emb=pos_emb, pad_mask=pad_mask, attn_mask=att_mask, cache=state.cache)
+        if isinstance(length, Tensor):
+            state.processed_frames.add_(length)
+            state.cache_lengths.add_(length)
+            state.cache_lengths.clamp_(max=self.att_context_size[0])
+        else:
+            state.processed_frames += x.size(1)
+            state.cache_lengths = min(int(state.cache_lengths) + x.size(1), self.att_context_size[0])
+        return x.transpose(1, 2), state
+
+
+__all__ = ["ConformerEncoder", "ConformerLayer", "ConformerConvolution", "ConformerFeedForward", "CausalConv1d"]

@@ -1,0 +1,283 @@
+"""Tensor-level entry points of the paged K/V-cache hot path.
+
+Each function checks shapes, dtypes, devices and strides on the host, then makes
+one call into ``libparakeet_paged.so`` on torch's current HIP stream.  Nothing
+here computes on the CPU: without the library or a HIP device the call raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from ._lib import AttnArgs, KvAppendArgs, KvGatherArgs, MaskArgs, PagedLayout, check, lib
+
+_DTYPES = {
+    torch.float32: _lib.DTYPE_F32,
+    torch.float16: _lib.DTYPE_F16,
+    torch.bfloat16: _lib.DTYPE_BF16,
+}
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPES[dtype]
+    except KeyError:
+        raise TypeError(f"paged K/V cache supports float32/float16/bfloat16, got {dtype}") from None
+
+
+def _require_device(*tensors: torch.Tensor) -> torch.device:
+    dev = tensors[0].device
+    if dev.type != "cuda":
+        raise RuntimeError(
+            f"paged K/V cache kernels run on a HIP device; got a tensor on {dev} "
+            "(there is no CPU implementation)"
+        )
+    for t in tensors[1:]:
+        if t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+def _stream(dev: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _event_handle(ev) -> int:
+    """hipEvent_t of a torch.cuda.Event (recorded once, so it exists) or a raw handle."""
+    handle = getattr(ev, "cuda_event", ev)
+    if not handle:
+        raise ValueError("timing event has no handle yet: record it once before use")
+    return int(handle)
+
+
+def _rows3(t: torch.Tensor, name: str, B: int, T: int, D: int, dtype: torch.dtype) -> None:
+    if t.dim() != 3 or tuple(t.shape) != (B, T, D):
+        raise ValueError(f"{name}: expected shape {(B, T, D)}, got {tuple(t.shape)}")
+    if t.dtype != dtype:
+        raise TypeError(f"{name}: dtype {t.dtype} != {dtype}")
+    if t.stride(2) != 1:
+        raise ValueError(f"{name}: last dimension must be contiguous")
+
+
+@dataclass
+class PagedKV:
+    """Device view of a batch's pages: pools [Ly, num_pages, P, D] and the
+    per-stream rows {A, ring[max_pages]} (int32 [B, 1 + max_pages])."""
+
+    k_pool: torch.Tensor
+    v_pool: torch.Tensor
+    rows: torch.Tensor
+    max_pages: int
+
+    def layout(self) -> PagedLayout:
+        kp, vp, rows = self.k_pool, self.v_pool, self.rows
+        if kp.shape != vp.shape or kp.dim() != 4 or kp.dtype != vp.dtype:
+            raise ValueError("k_pool and v_pool must be matching [Ly, num_pages, P, D] tensors")
+        if not (kp.is_contiguous() and vp.is_contiguous()):
+            raise ValueError("page pools must be contiguous")
+        if rows.dtype != torch.int32 or rows.dim() != 2 or rows.stride(1) != 1:
+            raise ValueError("rows must be int32 [B, 1 + max_pages] with unit inner stride")
+        if rows.shape[1] < 1 + self.max_pages:
+            raise ValueError(f"rows has {rows.shape[1]} columns, needs {1 + self.max_pages}")
+        L = PagedLayout()
+        L.k_pool = kp.data_ptr()
+        L.v_pool = vp.data_ptr()
+        L.num_layers, L.num_pages, L.page_size, L.d_model = (int(s) for s in kp.shape)
+        L.rows = rows.data_ptr()
+        L.rows_stride = rows.stride(0)
+        L.max_pages = self.max_pages
+        return L
+
+
+def kv_append(pages: PagedKV, layer: int, key: torch.Tensor, value: torch.Tensor) -> None:
+    """Writes key/value [B, T, D] into the pages at positions [A, A+T) of each
+    row (parakeet/modules/cache.py:43-44)."""
+    B, T, D = key.shape
+    _rows3(key, "key", B, T, D, pages.k_pool.dtype)
+    _rows3(value, "value", B, T, D, pages.k_pool.dtype)
+    if pages.rows.shape[0] < B:
+        raise ValueError(f"rows covers {pages.rows.shape[0]} streams, batch is {B}")
+    dev = _require_device(key, value, pages.k_pool, pages.v_pool, pages.rows)
+    a = KvAppendArgs()
+    a.dtype = dtype_code(key.dtype)
+    a.device = dev.index if dev.index is not None else torch.cuda.current_device()
+    a.pages = pages.layout()
+    a.layer, a.batch, a.chunk = int(layer), B, T
+    a.key, a.key_stride_b, a.key_stride_t = key.data_ptr(), key.stride(0), key.stride(1)
+    a.value, a.value_stride_b, a.value_stride_t = value.data_ptr(), value.stride(0), value.stride(1)
+    check(lib().pk_kv_append(ctypes.byref(a), _stream(dev)), "pk_kv_append")
+
+
+def kv_gather(
+    pages: PagedKV,
+    layer: int,
+    batch: int,
+    window: int,
+    end_offset: int,
+    out_k: torch.Tensor | None = None,
+    out_v: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Dense window [B, window, D] of positions [A + end_offset - window,
+    A + end_offset), zeros before position 0 (parakeet/modules/cache.py:45)."""
+    kp = pages.k_pool
+    D = kp.shape[3]
+    if out_k is None:
+        out_k = torch.empty((batch, window, D), dtype=kp.dtype, device=kp.device)
+    if out_v is None:
+        out_v = torch.empty((batch, window, D), dtype=kp.dtype, device=kp.device)
+    _rows3(out_k, "out_k", batch, window, D, kp.dtype)
+    _rows3(out_v, "out_v", batch, window, D, kp.dtype)
+    if pages.rows.shape[0] < batch:
+        raise ValueError(f"rows covers {pages.rows.shape[0]} streams, batch is {batch}")
+    dev = _require_device(out_k, out_v, kp, pages.v_pool, pages.rows)
+    a = KvGatherArgs()
+    a.dtype = dtype_code(kp.dtype)
+    a.device = dev.index if dev.index is not None else torch.cuda.current_device()
+    a.pages = pages.layout()
+    a.layer, a.batch, a.window, a.end_offset = int(layer), int(batch), int(window), int(end_offset)
+    a.out_k, a.out_k_stride_b, a.out_k_stride_t = out_k.data_ptr(), out_k.stride(0), out_k.stride(1)
+    a.out_v, a.out_v_stride_b, a.out_v_stride_t = out_v.data_ptr(), out_v.stride(0), out_v.stride(1)
+    check(lib().pk_kv_gather(ctypes.byref(a), _stream(dev)), "pk_kv_gather")
+    return out_k, out_v
+
+
+def _mask_strides(mask: torch.Tensor, B: int, H: int, T: int, Lk: int) -> tuple[torch.Tensor, int, int, int]:
+    if mask.dtype not in (torch.bool, torch.uint8):
+        raise TypeError(f"mask must be bool or uint8, got {mask.dtype}")
+    if mask.dim() == 3:
+        mask = mask.unsqueeze(1)
+    if mask.dim() != 4:
+        raise ValueError(f"mask must be [B, T, L] or [B, H, T, L], got {tuple(mask.shape)}")
+    mb, mh, mt, ml = mask.shape
+    if mb != B or mt != T or ml != Lk or mh not in (1, H):
+        raise ValueError(f"mask shape {tuple(mask.shape)} does not broadcast to {(B, H, T, Lk)}")
+    if mask.stride(3) != 1:
+        mask = mask.contiguous()
+    sh = 0 if mh == 1 else mask.stride(1)
+    return mask, mask.stride(0), sh, mask.stride(2)
+
+
+def paged_relpos_attn(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    pos: torch.Tensor,
+    bias_u: torch.Tensor,
+    bias_v: torch.Tensor,
+    mask: torch.Tensor | None,
+    *,
+    num_heads: int,
+    left: int,
+    pages: PagedKV | None = None,
+    layer: int = 0,
+    append: bool = True,
+    out: torch.Tensor | None = None,
+    rows_per_lane: int = 0,
+    start_event=None,
+    stop_event=None,
+) -> torch.Tensor:
+    """Relative-position MHA of the chunk's queries over each stream's window
+    (``left`` cached frames from ``pages`` + this chunk's frames), appending the
+    chunk's K/V to the pages when ``append``.  Restates
+    parakeet/modules/attention.py:97-121; returns [B, T, D] before linear_out.
+
+    query/key/value: [B, T, D] (views of the qkv projection are fine);
+    pos: [>= L + T - 1, D] (linear_pos of the sinusoid slice, batch dim dropped);
+    bias_u/bias_v: [H, dk]; mask: [B, T, L] / [B, 1|H, T, L] bool, True = masked.
+    """
+    B, T, D = query.shape
+    dt = query.dtype
+    _rows3(query, "query", B, T, D, dt)
+    _rows3(key, "key", B, T, D, dt)
+    _rows3(value, "value", B, T, D, dt)
+    H = int(num_heads)
+    if D % H != 0:
+        raise ValueError(f"d_model {D} not divisible by {H} heads")
+    dk = D // H
+    Lk = int(left) + T
+    if pos.dim() != 2 or pos.shape[1] != D or pos.stride(1) != 1 or pos.dtype != dt:
+        raise ValueError(f"pos must be [rows, {D}] of {dt} with unit inner stride, got {tuple(pos.shape)} {pos.dtype}")
+    for name, bias in (("bias_u", bias_u), ("bias_v", bias_v)):
+        if tuple(bias.shape) != (H, dk) or bias.dtype != dt or not bias.is_contiguous():
+            raise ValueError(f"{name} must be contiguous [{H}, {dk}] of {dt}")
+    tensors = [query, key, value, pos, bias_u, bias_v]
+    if pages is not None:
+        if pages.k_pool.dtype != dt:
+            raise TypeError(f"pages dtype {pages.k_pool.dtype} != {dt}")
+        if pages.rows.shape[0] < B:
+            raise ValueError(f"rows covers {pages.rows.shape[0]} streams, batch is {B}")
+        tensors += [pages.k_pool, pages.v_pool, pages.rows]
+    elif left != 0 or append:
+        raise ValueError("left > 0 or append needs pages")
+    dev = _require_device(*tensors)
+    if out is None:
+        out = torch.empty((B, T, D), dtype=dt, device=dev)
+    _rows3(out, "out", B, T, D, dt)
+
+    a = AttnArgs()
+    a.dtype = dtype_code(dt)
+    a.device = dev.index if dev.index is not None else torch.cuda.current_device()
+    if pages is not None:
+        a.pages = pages.layout()
+    a.layer, a.batch, a.chunk = int(layer), B, T
+    a.num_heads, a.head_dim, a.left, a.append = H, dk, int(left), 1 if append else 0
+    a.query, a.query_stride_b, a.query_stride_t = query.data_ptr(), query.stride(0), query.stride(1)
+    a.key, a.key_stride_b, a.key_stride_t = key.data_ptr(), key.stride(0), key.stride(1)
+    a.value, a.value_stride_b, a.value_stride_t = value.data_ptr(), value.stride(0), value.stride(1)
+    a.pos, a.pos_stride, a.pos_rows = pos.data_ptr(), pos.stride(0), pos.shape[0]
+    a.bias_u, a.bias_v = bias_u.data_ptr(), bias_v.data_ptr()
+    if mask is not None:
+        mask, sb, sh, st = _mask_strides(mask, B, H, T, Lk)
+        if mask.device != dev:
+            raise ValueError("mask on a different device")
+        a.mask, a.mask_stride_b, a.mask_stride_h, a.mask_stride_t = mask.data_ptr(), sb, sh, st
+    a.out, a.out_stride_b, a.out_stride_t = out.data_ptr(), out.stride(0), out.stride(1)
+    a.rows_per_lane = int(rows_per_lane)
+    if start_event is not None:
+        a.start_event = _event_handle(start_event)
+    if stop_event is not None:
+        a.stop_event = _event_handle(stop_event)
+    check(lib().pk_paged_relpos_attn(ctypes.byref(a), _stream(dev)), "pk_paged_relpos_attn")
+    return out
+
+
+def streaming_mask(
+    processed_frames: torch.Tensor,
+    cache_lengths: torch.Tensor,
+    lengths: torch.Tensor | int,
+    *,
+    chunk: int,
+    left: int,
+    chunk_size: int,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """(pad_mask [B, T], att_mask [B, T, left + T]) bool, as
+    ConformerEncoder._create_streaming_masks (parakeet/modules/encoder.py:167-227)."""
+    B = int(cache_lengths.shape[0])
+    tensors = [processed_frames, cache_lengths]
+    for name, t in (("processed_frames", processed_frames), ("cache_lengths", cache_lengths)):
+        if t.dtype != torch.int64 or t.shape != (B,) or not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous int64 [{B}]")
+    if isinstance(lengths, torch.Tensor):
+        if lengths.dtype != torch.int64 or lengths.shape != (B,) or not lengths.is_contiguous():
+            raise ValueError(f"lengths must be contiguous int64 [{B}]")
+        tensors.append(lengths)
+    dev = _require_device(*tensors)
+    att = torch.empty((B, chunk, left + chunk), dtype=torch.bool, device=dev)
+    pad = torch.empty((B, chunk), dtype=torch.bool, device=dev)
+    a = MaskArgs()
+    a.device = dev.index if dev.index is not None else torch.cuda.current_device()
+    a.batch, a.chunk, a.left, a.chunk_size = B, int(chunk), int(left), int(chunk_size)
+    a.processed_frames = processed_frames.data_ptr()
+    a.cache_lengths = cache_lengths.data_ptr()
+    if isinstance(lengths, torch.Tensor):
+        a.lengths = lengths.data_ptr()
+    else:
+        a.length_scalar = int(lengths)
+    a.att_mask = att.data_ptr()
+    a.pad_mask = pad.data_ptr()
+    check(lib().pk_streaming_mask(ctypes.byref(a), _stream(dev)), "pk_streaming_mask")
+    return pad, att

@@ -1,0 +1,79 @@
+"""The C-ABI library loads without a GPU, exports every function that
+include/parakeet_paged.h declares, and the ctypes structures match the header's
+field order.  No kernel is launched here."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from parakeet_amd import _lib
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "parakeet_paged.h"
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = re.findall(r"^\s*(?:const\s+)?[\w]+\s*\*?\s*(pk_\w+)\s*\(", text, flags=re.M)
+    return sorted(set(names))
+
+
+def _struct_fields(name):
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    m = re.search(r"typedef struct %s \{(.*?)\} %s;" % (name, name), text, flags=re.S)
+    assert m, name
+    fields = []
+    for line in m.group(1).split(";"):
+        line = line.strip()
+        if not line:
+            continue
+        fields.append(line.split()[-1].lstrip("*"))
+    return fields
+
+
+def test_library_loads_and_versions():
+    lib = _lib.lib()
+    assert lib.pk_abi_version() == _lib.ABI_VERSION
+    assert _lib.last_error() == ""
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    declared = _declared_functions()
+    assert len(declared) >= 15, declared
+    lib = _lib.lib()
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in the header but not exported"
+    assert sorted(_lib.SIGNATURES) == declared
+
+
+@pytest.mark.parametrize(
+    "cname,pyclass",
+    [
+        ("pk_paged_layout", _lib.PagedLayout),
+        ("pk_kv_append_args", _lib.KvAppendArgs),
+        ("pk_kv_gather_args", _lib.KvGatherArgs),
+        ("pk_attn_args", _lib.AttnArgs),
+        ("pk_mask_args", _lib.MaskArgs),
+    ],
+)
+def test_struct_layout_matches_header(cname, pyclass):
+    assert [f[0] for f in pyclass._fields_] == _struct_fields(cname)
+
+
+def test_null_args_rejected_without_gpu():
+    lib = _lib.lib()
+    assert lib.pk_paged_relpos_attn(None, None) == _lib.PK_ERR_INVALID
+    assert "NULL" in _lib.last_error()
+    assert lib.pk_kv_append(None, None) == _lib.PK_ERR_INVALID
+    assert lib.pk_kv_gather(None, None) == _lib.PK_ERR_INVALID
+    assert lib.pk_streaming_mask(None, None) == _lib.PK_ERR_INVALID
+
+
+def test_mask_args_validated_before_launch():
+    a = _lib.MaskArgs()
+    a.batch, a.chunk, a.left, a.chunk_size = 2, 0, 70, 2
+    assert _lib.lib().pk_streaming_mask(ctypes.byref(a), None) == _lib.PK_ERR_INVALID
+    a.chunk = 2
+    assert _lib.lib().pk_streaming_mask(ctypes.byref(a), None) == _lib.PK_ERR_INVALID  # NULL state

@@ -1,0 +1,139 @@
+"""GPU parity: the fused append + paged rel-pos attention kernel against the
+oracle (parakeet/modules/attention.py:94-121 restated in float64 numpy) on the
+same seeded inputs, step after step with eviction.
+
+Tolerance (max-abs over valid query rows, outputs of magnitude ~1):
+  fp32 1e-4, fp16 2e-3, bf16 1e-2  -- the fp16/bf16 bounds are the ones the
+  hot path is specified to; the reference itself discards padded query rows
+  (parakeet/engine/model_runner.py:297), so rows with i >= length are not
+  compared.  The oracle sees the same dtype-rounded inputs upcast to float64.
+The pages the kernel appends are checked bit-exact against the dense window.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from _scenario import PagedScenario, to_np64
+from oracle import attention as oa
+from oracle import masks as om
+from parakeet_amd import ops, synth
+
+TOL = {torch.float32: 1e-4, torch.float16: 2e-3, torch.bfloat16: 1e-2}
+
+
+def _relpos(sc, H, seed):
+    shape = synth.Shape("t", sc.Ly, sc.D, H, left=sc.left, right=sc.right, page_size=sc.P, dtype=sc.dtype)
+    return synth.relpos_inputs(shape, sc.device, seed=seed)
+
+
+def _run(cuda, dtype, B, H, dk, left, right, P, steps, mask_kind="engine", shuffle=False, seed=0, rows_per_lane=0, layers=2):
+    print(f"\n[attn] dtype={dtype} B={B} H={H} dk={dk} left={left} right={right} P={P} mask={mask_kind} nr={rows_per_lane}", flush=True)
+    D = H * dk
+    sc = PagedScenario(cuda, dtype, B=B, layers=layers, d_model=D, left=left, right=right, page_size=P, seed=seed, shuffle=shuffle)
+    pos, bu, bv = _relpos(sc, H, seed)
+    rng = np.random.default_rng(seed)
+    T, L = sc.T, sc.L
+    proc = np.zeros(B, dtype=np.int64)
+    worst = 0.0
+    for step in range(steps):
+        sc.open_step()
+        cl = np.minimum(proc, left)
+        if mask_kind == "engine":
+            lengths = np.full(B, T)
+        else:
+            lengths = rng.integers(1, T + 1, size=B)
+        _, mask_np = om.create_streaming_masks(T, cl, proc, lengths, (left, right))
+        if mask_kind == "random":
+            mask_np = mask_np | (rng.random(mask_np.shape) < 0.2)
+            mask_np[:, :, left:] = False  # keep this chunk's frames visible
+        mask = torch.from_numpy(mask_np).to(cuda)
+        for layer in range(sc.Ly):
+            x, (q, k, v) = sc.frames()
+            out = ops.paged_relpos_attn(
+                q, k, v, pos, bu, bv, mask, num_heads=H, left=left, pages=sc.pages, layer=layer,
+                append=True, rows_per_lane=rows_per_lane,
+            )
+            dk_win, dv_win = sc.dense_update(layer, k, v)
+            ref = oa.relpos_attention(to_np64(q), dk_win, dv_win, to_np64(pos), to_np64(bu), to_np64(bv), mask_np, H)
+            got = to_np64(out)
+            valid = np.arange(T)[None, :] < lengths[:, None]
+            err = np.abs(got - ref)[valid]
+            worst = max(worst, float(err.max()))
+            assert err.max() <= TOL[dtype], f"step {step} layer {layer}: max abs err {err.max():.3e}"
+            # the fused append wrote exactly this step's frames
+            gk, gv = ops.kv_gather(sc.pages, layer, B, L, T)
+            assert torch.equal(gk.cpu(), torch.from_numpy(np.ascontiguousarray(dk_win)).to(dtype))
+            assert torch.equal(gv.cpu(), torch.from_numpy(np.ascontiguousarray(dv_win)).to(dtype))
+        proc += lengths
+    torch.cuda.synchronize()
+    print(f"  worst max-abs error {worst:.3e}", flush=True)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("H,dk", [(8, 64), (8, 128)])
+def test_engine_shape(cuda, dtype, H, dk):
+    _run(cuda, dtype, B=3, H=H, dk=dk, left=70, right=1, P=16, steps=40)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_large_chunk_t14(cuda, dtype):
+    # the real large model's att_context_size (70, 13): T = 14 straddles pages
+    _run(cuda, dtype, B=2, H=8, dk=128, left=70, right=13, P=16, steps=10)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("right", [0, 2, 3])
+def test_other_chunks(cuda, right):
+    _run(cuda, torch.float16, B=3, H=4, dk=64, left=20, right=right, P=8, steps=12, mask_kind="ragged")
+
+
+@pytest.mark.gpu
+def test_random_masks_and_ragged_lengths(cuda):
+    _run(cuda, torch.bfloat16, B=4, H=8, dk=64, left=70, right=1, P=16, steps=20, mask_kind="random", shuffle=True)
+
+
+@pytest.mark.gpu
+def test_long_window_multi_tile(cuda):
+    # left context long enough that the window needs several tiles
+    _run(cuda, torch.float16, B=2, H=8, dk=64, left=600, right=1, P=16, steps=6, layers=1)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("nr", [2, 3, 4, 6])
+def test_every_row_tiling(cuda, nr):
+    _run(cuda, torch.bfloat16, B=2, H=8, dk=128, left=70, right=1, P=16, steps=8, rows_per_lane=nr, layers=1)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_no_cache_mode(cuda, dtype):
+    """cache=None in the reference: keys are this chunk's frames only."""
+    B, H, dk, T = 3, 8, 64, 5
+    D = H * dk
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(B, T, 3 * D, generator=g).to(dtype).to(cuda)
+    q, k, v = x.chunk(3, dim=-1)
+    pos = (torch.randn(2 * T - 1 + 6, D, generator=g) * 0.3).to(dtype).to(cuda)
+    bu = (torch.randn(H, dk, generator=g) * 0.02).to(dtype).to(cuda)
+    bv = (torch.randn(H, dk, generator=g) * 0.02).to(dtype).to(cuda)
+    mask = torch.zeros(B, T, T, dtype=torch.bool)
+    mask[1, 0, 3:] = True
+    out = ops.paged_relpos_attn(q, k, v, pos, bu, bv, mask.to(cuda), num_heads=H, left=0, pages=None, append=False)
+    ref = oa.relpos_attention(to_np64(q), to_np64(k), to_np64(v), to_np64(pos), to_np64(bu), to_np64(bv), mask.numpy(), H)
+    assert np.abs(to_np64(out) - ref).max() <= TOL[dtype]
+
+
+@pytest.mark.gpu
+def test_bad_shapes_raise(cuda):
+    sc = PagedScenario(cuda, torch.float16, B=2, layers=1, d_model=128, left=6, right=1, page_size=4)
+    sc.open_step()
+    pos, bu, bv = _relpos(sc, 2, 0)
+    _, (q, k, v) = sc.frames()
+    with pytest.raises(RuntimeError, match="pos has"):
+        ops.paged_relpos_attn(q, k, v, pos[:3], bu, bv, None, num_heads=2, left=6, pages=sc.pages)
+    with pytest.raises(RuntimeError, match="head_dim"):
+        ops.paged_relpos_attn(q, k, v, pos, bu.reshape(4, 32), bv.reshape(4, 32), None, num_heads=4, left=6, pages=sc.pages)
+    torch.cuda.synchronize()
