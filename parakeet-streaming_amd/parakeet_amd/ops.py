@@ -79,16 +79,20 @@ class PagedKV:
             raise ValueError("k_pool and v_pool must be matching [Ly, num_pages, P, D] tensors")
         if not (kp.is_contiguous() and vp.is_contiguous()):
             raise ValueError("page pools must be contiguous")
-        if rows.dtype != torch.int32 or rows.dim() != 2 or rows.stride(1) != 1:
-            raise ValueError("rows must be int32 [B, 1 + max_pages] with unit inner stride")
+        if rows.dtype != torch.int32 or rows.dim() != 2:
+            raise ValueError("rows must be int32 [B, 1 + max_pages]")
         if rows.shape[1] < 1 + self.max_pages:
             raise ValueError(f"rows has {rows.shape[1]} columns, needs {1 + self.max_pages}")
+        # an empty batch reads no row; torch gives empty tensors arbitrary strides
+        empty = rows.shape[0] == 0
+        if not empty and rows.stride(1) != 1:
+            raise ValueError("rows must have unit inner stride")
         L = PagedLayout()
         L.k_pool = kp.data_ptr()
         L.v_pool = vp.data_ptr()
         L.num_layers, L.num_pages, L.page_size, L.d_model = (int(s) for s in kp.shape)
         L.rows = rows.data_ptr()
-        L.rows_stride = rows.stride(0)
+        L.rows_stride = 1 + self.max_pages if empty else rows.stride(0)
         L.max_pages = self.max_pages
         return L
 
