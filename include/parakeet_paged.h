@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define PK_ABI_VERSION 1
+#define PK_ABI_VERSION 2
 
 enum pk_dtype { PK_DTYPE_F32 = 0, PK_DTYPE_F16 = 1, PK_DTYPE_BF16 = 2 };
 
@@ -122,9 +122,20 @@ int pk_kv_gather(const pk_kv_gather_args* args, void* stream);
  * query/key/value: [batch][chunk][num_heads*head_dim], strides (b, t), last dim
  * contiguous.  pos: [pos_rows][num_heads*head_dim], row stride pos_stride; needs
  * pos_rows >= window + chunk - 1.  bias_u/bias_v: [num_heads][head_dim]
- * contiguous.  mask: uint8/bool [batch][heads][chunk][window] with element
- * strides (b, h, t) and unit stride along window (mask_stride_h 0 broadcasts a
- * [batch][chunk][window] mask), or NULL for no mask.  out: [batch][chunk][d_model].
+ * contiguous.  out: [batch][chunk][d_model].
+ * The mask comes from one of three sources:
+ *   mask != NULL   uint8/bool [batch][heads][chunk][window] with element strides
+ *                  (b, h, t) and unit stride along window (mask_stride_h 0
+ *                  broadcasts a [batch][chunk][window] mask), 1 = masked -- the
+ *                  attn_mask argument of ConformerAttention.forward;
+ *   mask == NULL and processed_frames != NULL
+ *                  the streaming mask of ConformerEncoder._create_streaming_masks
+ *                  (parakeet/modules/encoder.py:167-227) evaluated per score from
+ *                  processed_frames / cache_lengths / lengths (int64 [batch], lengths
+ *                  NULL -> length_scalar for every stream) and chunk_size
+ *                  (att_context_size[1] + 1); bit-identical to pk_streaming_mask for
+ *                  0 <= cache_lengths <= left and processed_frames < 2^31;
+ *   both NULL      no mask.
  * All floating tensors share `dtype`.  head_dim must be 64 or 128.
  * start_event/stop_event: optional hipEvent_t pair timing this kernel alone.
  */
@@ -157,6 +168,11 @@ typedef struct pk_attn_args {
   int64_t mask_stride_b;
   int64_t mask_stride_h;
   int64_t mask_stride_t;
+  const int64_t* processed_frames;
+  const int64_t* cache_lengths;
+  const int64_t* lengths;
+  int64_t length_scalar;
+  int32_t chunk_size;
   void* out;
   int64_t out_stride_b;
   int64_t out_stride_t;

@@ -16,6 +16,7 @@
 #include <hip/hip_ext.h>
 
 #include <cstdint>
+#include <type_traits>
 
 #include "pk_common.h"
 
@@ -172,12 +173,14 @@ struct PagesK {
   int32_t D;
 };
 
-// Element offset of frame `pos` (>= 0) of stream `ring` in a layer's pool slab,
-// or -1 when the ring holds no valid page for it.
+// Element offset of frame `pos` (0 <= pos < 2^31, the int32 range of the
+// rows' frame counter) of stream `ring` in a layer's pool slab, or -1 when the
+// ring holds no valid page for it.  32-bit index arithmetic.
 __device__ static inline int64_t page_offset(const PagesK& pg, const int32_t* ring, int64_t pos) {
-  const int32_t page = ring[(int32_t)((pos >> pg.page_shift) % pg.max_pages)];
+  const uint32_t p32 = (uint32_t)pos;
+  const int32_t page = ring[(p32 >> pg.page_shift) % (uint32_t)pg.max_pages];
   if (page < 0 || page >= pg.num_pages) return -1;
-  return (int64_t)page * pg.page_elems + (pos & ((1 << pg.page_shift) - 1)) * (int64_t)pg.D;
+  return (int64_t)page * pg.page_elems + (int64_t)(p32 & ((1u << pg.page_shift) - 1u)) * pg.D;
 }
 
 // ---------------------------------------------------------------------------
@@ -199,21 +202,69 @@ struct AttnK {
   const ST* bv;
   const uint8_t* mask;
   int64_t m_sb, m_sh, m_st;
+  const int64_t* st_proc;  // state-derived mask (mask == nullptr)
+  const int64_t* st_cl;
+  const int64_t* st_len;
+  int64_t len_scalar;
+  int32_t chunk_size, left_chunks;
   ST* out;
   int64_t o_sb, o_st;
-  int32_t T, H, left, Lk, append, tiles;
+  int32_t B, T, H, left, Lk, append, tiles;
   float scale;  // log2(e) / sqrt(head_dim)
 };
 
-// One workgroup per (stream b, head h, query group of TQ queries); W waves.
-// Wave w of tile t owns the contiguous window rows jb = (t*W + w)*BLK ...
-// jb + BLK - 1; inside the wave, lane group rl (G lanes) owns rows
-// jb + n*RLW + rl, n < NR.  Each wave computes its own (q+v).pos terms for the
-// BLK + TQ - 1 position rows its keys need into a wave-private LDS strip, so no
-// workgroup barrier stalls the K/V loads in flight; the only barrier is the
-// final cross-wave softmax combine.
+// Streaming-mask state of one stream (encoder.py:186-212), 32-bit.  The key and
+// query chunk indices are floor((key_start + x) / C) = ks_q + (ks_r + x) / C with
+// key_start = ks_q * C + ks_r, so only small non-negative values are divided.
+struct StreamMask {
+  int cl, len, offset, ks_q, ks_r, C, left_chunks;
+
+  __device__ inline void set(int64_t pr, int64_t c, int64_t n, int left, int C_, int lc) {
+    n = n < -1 ? -1 : (n > 0x7fffffff ? 0x7fffffff : n);
+    const int64_t ks = pr - c > 0 ? pr - c : 0;  // encoder.py:189
+    cl = (int)c;
+    len = (int)n;
+    offset = left - cl;  // encoder.py:214
+    C = C_;
+    left_chunks = lc;
+    ks_q = (int)((uint32_t)ks / (uint32_t)C);
+    ks_r = (int)ks - ks_q * C;
+  }
+  __device__ inline void load(const int64_t* proc, const int64_t* cl64, const int64_t* lens,
+                              int64_t len_scalar, int b, int left, int C_, int lc) {
+    set(proc[b], cl64[b], lens ? lens[b] : len_scalar, left, C_, lc);
+  }
+  // chunk index of query i (its frame is key_start + cl + i)
+  __device__ inline int query_chunk(int i) const {
+    return ks_q + (int)((uint32_t)(ks_r + cl + i) / (uint32_t)C);
+  }
+  // true where the reference's att_mask is set (encoder.py:199-225)
+  __device__ inline bool masked(int i, int qchunk, int j) const {
+    if (j < offset || i >= len) return true;
+    const int kidx = j - offset;
+    const int kc = ks_q + (int)((uint32_t)(ks_r + kidx) / (uint32_t)C);
+    const int diff = qchunk - kc;
+    const bool allowed = diff >= 0 && diff <= left_chunks;
+    const bool valid_k = kidx < cl || kidx - cl < len;
+    return !(allowed && valid_k);
+  }
+};
+
+// One single-wave workgroup per (stream b, head h, query group of TQ queries).
+// Lane group rl (G lanes, VEC columns each) owns window rows jb + n*RLW + rl,
+// n < NR, of every tile of BLK = RLW*NR rows.  Per tile:
+//   1. the position rows of the tile (L2-resident, shared by all streams) are
+//      loaded in the same round trip as the stream's page header, the queries
+//      and the biases, and reduced to the (q+v).pos terms in a wave-private LDS
+//      strip before any K/V load is issued (vector loads complete in issue
+//      order, so position loads queued behind K/V would wait for all of them);
+//   2. page ids come from the ring held one entry per lane (ds_bpermute), and
+//      all NR K rows and NR V rows of the lane are issued back to back;
+//   3. scores, an online softmax over the lane group's rows and the value sum.
+// The lane groups are combined with cross-lane shuffles at the end: no
+// workgroup barrier, and one wave holds the whole window of its head in flight.
 template <typename ST, int DK, int TQ, int NR>
-__global__ void __launch_bounds__(512) relpos_attn_kernel(const AttnK<ST> p) {
+__global__ void __launch_bounds__(64) relpos_attn_kernel(const AttnK<ST> p) {
   constexpr int VEC = Tr<ST>::VEC;
   constexpr int G = DK / VEC;
   static_assert(G >= 1 && 64 % G == 0, "head_dim / VEC must divide 64");
@@ -224,10 +275,10 @@ __global__ void __launch_bounds__(512) relpos_attn_kernel(const AttnK<ST> p) {
   constexpr float NEG = -1e30f;
   constexpr float MASKED = -1e5f * 1.4426950408889634f;  // -1e5 in log2 units
 
-  extern __shared__ float smem[];
-  const int W = blockDim.x >> 6;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  __shared__ float cbuf[TQ][NP * RLW];  // (q+v).pos terms of the tile
+  __shared__ uint8_t mbuf[TQ][BLK];     // mask bytes of the tile (pointer mask)
+
+  const int lane = threadIdx.x;
   const int g = lane % G;
   const int rl = lane / G;
   const int b = blockIdx.x / p.H;
@@ -235,37 +286,36 @@ __global__ void __launch_bounds__(512) relpos_attn_kernel(const AttnK<ST> p) {
   const int i0 = blockIdx.y * TQ;
   const int nq = min(TQ, p.T - i0);
   const int col = h * DK + g * VEC;
-  float* cbuf = smem + wave * (TQ * CROWS);
 
-  int64_t A = 0;
+  // page header of the stream: frames appended before this step and the ring,
+  // one ring entry per lane
+  int A = 0;
+  int ring_lane = -1;
   const int32_t* ring = nullptr;
+  const int M = p.pg.max_pages;
   if (p.pg.rows) {
     const int32_t* row = p.pg.rows + (int64_t)b * p.pg.rows_stride;
     A = row[0];
     ring = row + 1;
+    ring_lane = ring[min(lane, M - 1)];
+  }
+  const int mask_mode = p.mask ? 1 : (p.st_proc ? 2 : 0);
+  StreamMask sm{};
+  int qchunk[TQ];
+  if (mask_mode == 2) {
+    sm.load(p.st_proc, p.st_cl, p.st_len, p.len_scalar, b, p.left, p.chunk_size, p.left_chunks);
+#pragma unroll
+    for (int ii = 0; ii < TQ; ++ii) qchunk[ii] = sm.query_chunk(i0 + ii);
   }
 
-  float qu[TQ][VEC], qv[TQ][VEC];
-  {
-    float bu[VEC], bv[VEC];
-    Tr<ST>::unpack(ld16(p.bu + col), bu);
-    Tr<ST>::unpack(ld16(p.bv + col), bv);
+  u32x4 qraw[TQ];
 #pragma unroll
-    for (int ii = 0; ii < TQ; ++ii) {
-      float qf[VEC];
-      if (ii < nq) {
-        Tr<ST>::unpack(ld16(p.q + b * p.q_sb + (int64_t)(i0 + ii) * p.q_st + col), qf);
-      } else {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) qf[e] = 0.f;
-      }
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        qu[ii][e] = qf[e] + bu[e];
-        qv[ii][e] = qf[e] + bv[e];
-      }
-    }
+  for (int ii = 0; ii < TQ; ++ii) {
+    const int ic = min(i0 + ii, p.T - 1);
+    qraw[ii] = ld16(p.q + b * p.q_sb + (int64_t)ic * p.q_st + col);
   }
+  const u32x4 buraw = ld16(p.bu + col);
+  const u32x4 bvraw = ld16(p.bv + col);
 
   float m[TQ], l[TQ], acc[TQ][VEC];
 #pragma unroll
@@ -276,80 +326,101 @@ __global__ void __launch_bounds__(512) relpos_attn_kernel(const AttnK<ST> p) {
     for (int e = 0; e < VEC; ++e) acc[ii][e] = 0.f;
   }
 
-  for (int tile = 0; tile < p.tiles; ++tile) {
-    const int jb = (tile * W + wave) * BLK;
-    if (jb >= p.Lk) break;  // uniform per wave
+  const uint32_t pmask = (1u << p.pg.page_shift) - 1u;
+  const ST* kn_b = p.kn + b * p.k_sb;
+  const ST* vn_b = p.vn + b * p.v_sb;
 
-    // position-table rows rb .. rb + CROWS - 1 (L2-resident, shared by all streams)
+  for (int tile = 0; tile < p.tiles; ++tile) {
+    const int jb = tile * BLK;
+
+    // (1) position rows rb .. rb + CROWS - 1 and mask bytes of the tile
     const int rb = jb + p.T - i0 - TQ;
     u32x4 pr[NP];
 #pragma unroll
     for (int k = 0; k < NP; ++k) {
-      const int mm = rl + k * RLW;
-      const int r = rb + mm;
-      if (mm < CROWS && r >= 0 && r < p.pos_rows)
-        pr[k] = ld16(p.pos + r * p.pos_sr + col);
-      else
-        pr[k] = u32x4{0u, 0u, 0u, 0u};
+      const int r = min(max(rb + rl + k * RLW, 0), p.pos_rows - 1);
+      pr[k] = ld16(p.pos + r * p.pos_sr + col);
     }
-    // mask bytes
-    uint8_t mk[NR][TQ];
-#pragma unroll
-    for (int n = 0; n < NR; ++n) {
-      const int j = jb + n * RLW + rl;
-#pragma unroll
-      for (int ii = 0; ii < TQ; ++ii)
-        mk[n][ii] = (p.mask && j < p.Lk && ii < nq)
-                        ? p.mask[b * p.m_sb + h * p.m_sh + (int64_t)(i0 + ii) * p.m_st + j]
-                        : (uint8_t)0;
+    if (mask_mode == 1) {
+      for (int x = lane; x < TQ * BLK; x += 64) {
+        const int ii = x / BLK;
+        const int jj = x - ii * BLK;
+        const int ic = min(i0 + ii, p.T - 1);
+        const int jcl = min(jb + jj, p.Lk - 1);
+        mbuf[ii][jj] = p.mask[b * p.m_sb + h * p.m_sh + (int64_t)ic * p.m_st + jcl];
+      }
     }
-    // K/V rows: this step's frames from the projection output, older ones from pages
-    u32x4 kr[NR], vr[NR];
+    float qu[TQ][VEC];
+    {
+      float bu[VEC], bv[VEC];
+      Tr<ST>::unpack(buraw, bu);
+      Tr<ST>::unpack(bvraw, bv);
+      float qv[TQ][VEC];
 #pragma unroll
-    for (int n = 0; n < NR; ++n) {
-      const int j = jb + n * RLW + rl;
-      kr[n] = u32x4{0u, 0u, 0u, 0u};
-      vr[n] = u32x4{0u, 0u, 0u, 0u};
-      if (j < p.Lk) {
-        if (j >= p.left) {
-          const int t = j - p.left;
-          kr[n] = ld16(p.kn + b * p.k_sb + (int64_t)t * p.k_st + col);
-          vr[n] = ld16(p.vn + b * p.v_sb + (int64_t)t * p.v_st + col);
-        } else {
-          const int64_t pos = A - p.left + j;
-          if (pos >= 0) {
-            const int64_t off = page_offset(p.pg, ring, pos);
-            if (off >= 0) {
-              kr[n] = ld16_stream(p.kp + off + col);
-              vr[n] = ld16_stream(p.vp + off + col);
-            }
-          }
+      for (int ii = 0; ii < TQ; ++ii) {
+        float qf[VEC];
+        Tr<ST>::unpack(qraw[ii], qf);
+        const bool live = ii < nq;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float x = live ? qf[e] : 0.f;
+          qu[ii][e] = x + bu[e];
+          qv[ii][e] = x + bv[e];
+        }
+      }
+      // bd terms cbuf[ii][mm] = (q_ii + v) . pos[rb + mm]
+#pragma unroll
+      for (int k = 0; k < NP; ++k) {
+        float pf[VEC];
+        Tr<ST>::unpack(pr[k], pf);
+        const int mm = rl + k * RLW;
+        const int r = rb + mm;
+        const bool live = r >= 0 && r < p.pos_rows;
+#pragma unroll
+        for (int ii = 0; ii < TQ; ++ii) {
+          float d = 0.f;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) d = fmaf(qv[ii][e], pf[e], d);
+          d = group_sum<G>(d);
+          if (g == 0) cbuf[ii][mm] = live ? d : 0.f;
         }
       }
     }
 
-    // bd terms c[ii][mm] = (q_ii + v) . pos[rb + mm], into this wave's LDS strip
+    // (2) page ids and K/V rows: this step's frames from the projection
+    //     output, older ones from the pages
+    u32x4 kr[NR], vr[NR];
+    bool ok[NR];
 #pragma unroll
-    for (int k = 0; k < NP; ++k) {
-      float pf[VEC];
-      Tr<ST>::unpack(pr[k], pf);
-      const int mm = rl + k * RLW;
-#pragma unroll
-      for (int ii = 0; ii < TQ; ++ii) {
-        float d = 0.f;
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) d = fmaf(qv[ii][e], pf[e], d);
-        d = group_sum<G>(d);
-        if (g == 0 && mm < CROWS) cbuf[ii * CROWS + mm] = d;
+    for (int n = 0; n < NR; ++n) {
+      const int j = jb + n * RLW + rl;
+      const int jc = min(j, p.Lk - 1);
+      const int pos = A - p.left + jc;
+      const bool fresh = jc >= p.left;
+      int page = -1;
+      if (ring) {
+        const uint32_t ridx = ((uint32_t)max(pos, 0) >> p.pg.page_shift) % (uint32_t)M;
+        page = __shfl(ring_lane, (int)ridx);
       }
+      const bool paged_ok = pos >= 0 && page >= 0 && page < p.pg.num_pages;
+      ok[n] = j < p.Lk && (fresh || paged_ok);
+      const int t = fresh ? jc - p.left : 0;
+      const int64_t poff = (int64_t)(paged_ok ? page : 0) * p.pg.page_elems +
+                           (int64_t)((uint32_t)max(pos, 0) & pmask) * p.pg.D;
+      const bool from_new = fresh || !paged_ok;
+      const ST* ka = from_new ? kn_b + (int64_t)t * p.k_st : p.kp + poff;
+      const ST* va = from_new ? vn_b + (int64_t)t * p.v_st : p.vp + poff;
+      kr[n] = ld16(ka + col);
+      vr[n] = ld16(va + col);
     }
     wave_lds_sync();
 
-    // scores in log2 units
+    // (3) scores in log2 units
     float s[TQ][NR];
 #pragma unroll
     for (int n = 0; n < NR; ++n) {
       const int j = jb + n * RLW + rl;
+      const int jc = min(j, p.Lk - 1);
       float kf[VEC];
       Tr<ST>::unpack(kr[n], kf);
 #pragma unroll
@@ -358,18 +429,20 @@ __global__ void __launch_bounds__(512) relpos_attn_kernel(const AttnK<ST> p) {
 #pragma unroll
         for (int e = 0; e < VEC; ++e) ac = fmaf(qu[ii][e], kf[e], ac);
         ac = group_sum<G>(ac);
-        float sc = NEG;
-        if (j < p.Lk && ii < nq) {
-          if (mk[n][ii])
-            sc = fmaf(ac, p.scale, MASKED);
-          else
-            sc = (ac + cbuf[ii * CROWS + n * RLW + rl + TQ - 1 - ii]) * p.scale;
-        }
-        s[ii][n] = sc;
+        if (!ok[n]) ac = 0.f;  // a key outside the stream's history reads as zeros
+        bool msk = false;
+        if (mask_mode == 1) msk = mbuf[ii][n * RLW + rl] != 0;
+        if (mask_mode == 2) msk = sm.masked(i0 + ii, qchunk[ii], jc);
+        float sc;
+        if (msk)
+          sc = fmaf(ac, p.scale, MASKED);
+        else
+          sc = (ac + cbuf[ii][n * RLW + rl + TQ - 1 - ii]) * p.scale;
+        s[ii][n] = (j < p.Lk && ii < nq) ? sc : NEG;
       }
     }
 
-    // online softmax update over this lane group's rows
+    // online softmax over the lane group's rows, then the value sum
 #pragma unroll
     for (int ii = 0; ii < TQ; ++ii) {
       float tmax = NEG;
@@ -386,6 +459,10 @@ __global__ void __launch_bounds__(512) relpos_attn_kernel(const AttnK<ST> p) {
     for (int n = 0; n < NR; ++n) {
       float vf[VEC];
       Tr<ST>::unpack(vr[n], vf);
+      if (!ok[n]) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) vf[e] = 0.f;
+      }
 #pragma unroll
       for (int ii = 0; ii < TQ; ++ii) {
         const float e = s[ii][n] > 0.5f * NEG ? __builtin_amdgcn_exp2f(s[ii][n] - m[ii]) : 0.f;
@@ -409,10 +486,10 @@ __global__ void __launch_bounds__(512) relpos_attn_kernel(const AttnK<ST> p) {
         }
       }
     }
-    wave_lds_sync();  // the next tile rewrites cbuf
+    wave_lds_sync();  // the next tile rewrites cbuf / mbuf
   }
 
-  // combine the RLW lane groups of the wave
+  // combine the RLW lane groups and write [b, i, h*DK + ...]
 #pragma unroll
   for (int ii = 0; ii < TQ; ++ii) {
 #pragma unroll
@@ -431,42 +508,432 @@ __global__ void __launch_bounds__(512) relpos_attn_kernel(const AttnK<ST> p) {
       m[ii] = mx;
     }
   }
-
-  // combine the W waves through LDS and write [b, i, h*DK ...]
-  float* comb = smem + W * TQ * CROWS;  // [W][TQ][2 + DK]
   if (rl == 0) {
 #pragma unroll
     for (int ii = 0; ii < TQ; ++ii) {
-      float* c = comb + (wave * TQ + ii) * (2 + DK);
-      if (g == 0) {
-        c[0] = m[ii];
-        c[1] = l[ii];
-      }
+      if (ii >= nq) continue;
+      const float inv = l[ii] > 0.f ? 1.f / l[ii] : 0.f;
+      float o[VEC];
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) c[2 + g * VEC + e] = acc[ii][e];
+      for (int e = 0; e < VEC; ++e) o[e] = acc[ii][e] * inv;
+      st16(p.out + b * p.o_sb + (int64_t)(i0 + ii) * p.o_st + col, Tr<ST>::pack(o));
     }
   }
-  __syncthreads();
-  for (int idx = threadIdx.x; idx < TQ * G; idx += blockDim.x) {
-    const int ii = idx / G;
-    const int gg = idx - ii * G;
-    if (ii >= nq) continue;
-    float mx = NEG;
-    for (int w = 0; w < W; ++w) mx = fmaxf(mx, comb[(w * TQ + ii) * (2 + DK)]);
-    float L = 0.f, o[VEC];
+}
+
+// ---------------------------------------------------------------------------
+// fused append + paged relative-position attention on the matrix cores
+// (fp16 / bf16)
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// v_mfma_f32_16x16x32_{bf16,f16}: lane l holds A[l%16][8*(l/16)+e],
+// B[8*(l/16)+e][l%16] (e < 8) and D[4*(l/16)+i][l%16] (i < 4).
+template <typename ST>
+struct Mma;
+
+template <>
+struct Mma<bf16_t> {
+  __device__ static inline f32x4_t run(const u32x4 a, const u32x4 b, const f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  }
+  // x rounded to the operand type: bit pattern, and its value back in fp32
+  __device__ static inline uint32_t round(float x, float* back) {
+    const uint32_t bits = f32_to_bf16_bits(x);
+    *back = __uint_as_float(bits << 16);
+    return bits;
+  }
+};
+
+template <>
+struct Mma<_Float16> {
+  __device__ static inline f32x4_t run(const u32x4 a, const u32x4 b, const f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+  __device__ static inline uint32_t round(float x, float* back) {
+    const _Float16 hv = (_Float16)x;
+    *back = (float)hv;
+    return (uint32_t)__builtin_bit_cast(uint16_t, hv);
+  }
+};
+
+// Max over the 16 lanes of each DPP row.
+__device__ static inline float row16_max(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  v = fmaxf(v, dpp_f<0x141>(v));
+  v = fmaxf(v, dpp_f<0x140>(v));
+  return v;
+}
+
+__device__ static inline float lane0(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
+}
+
+// Workgroup of NW = 4 * SPLIT waves: four streams of one head h and one query
+// pair, each stream's head split over SPLIT = head_dim / 64 waves of 64
+// columns.  Per key tile of KT = 16*NT window rows:
+//   * the tile's position rows of head h (shared by every stream) are staged
+//     once per workgroup in LDS, rows padded by 16 bytes so the 16 lanes of an
+//     MFMA operand read hit distinct banks;
+//   * the MFMA A operand holds, in rows 0..7, (q+u) and (q+v) of both queries,
+//     each split into a high and a low 16-bit part (x = hi + lo to ~2^-17), so
+//     the 16-bit operands lose nothing against the fp32 query + bias sums;
+//   * B operands are the stream's K rows (straight from its pages, 16 keys per
+//     MFMA) and the staged position rows; D rows 0..3 give (q+u).k, rows 4..7
+//     (q+v).pos, each as hi + lo, over the wave's 64 columns;
+//   * the partial dot products of the SPLIT waves of a stream meet in LDS; each
+//     wave then runs the same softmax and sums the values of its own columns on
+//     the VALU (lane = 8 columns of every RLW-th key).
+// Every load that does not depend on the page table (header, stream state,
+// queries, biases, position rows, mask bytes) is issued in one round trip; the
+// K and V rows of the whole tile follow back to back.
+template <typename ST, int DK, int NT, int MODE>
+__global__ void __launch_bounds__(256 * (DK / 64)) relpos_attn_mfma_kernel(const AttnK<ST> p) {
+  constexpr int SPLIT = DK / 64;
+  constexpr int NW = 4 * SPLIT;
+  constexpr int NTH = 64 * NW;
+  constexpr int TQ = 2;
+  constexpr int KS = 2;            // k-steps of 32 columns per wave
+  constexpr int KT = 16 * NT;      // keys per tile
+  constexpr int NPT = (KT + TQ - 1 + 15) / 16;  // position-row tiles
+  constexpr int PROWS = 16 * NPT;
+  constexpr int PSTRIDE = DK * 2 + 16;          // bytes per staged position row
+  constexpr int CHR = DK / 8;                   // 16-byte chunks per staged row
+  constexpr int PCH = (PROWS * CHR + NTH - 1) / NTH;  // staged chunks per thread
+  constexpr int VEC = 8;
+  constexpr int G = 64 / VEC;   // lanes per key row in the value sum
+  constexpr int RLW = 64 / G;   // key rows per value load
+  constexpr int NV = KT / RLW;  // value rows per lane per tile
+  constexpr float NEG = -1e30f;
+  constexpr float MASKED = -1e5f * 1.4426950408889634f;
+
+  __shared__ __attribute__((aligned(16))) uint8_t pos_lds[PROWS * PSTRIDE];
+  __shared__ float bd_lds[NW][TQ][PROWS];
+  __shared__ float ac_lds[NW][TQ][KT];
+  __shared__ __attribute__((aligned(8))) float p_lds[NW][KT][TQ];
+
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int q16 = lane & 15;
+  const int kg = lane >> 4;
+  const int sw = wave / SPLIT;   // stream slot in the workgroup
+  const int hf = wave % SPLIT;   // 64-column part of the head
+  const int w0 = sw * SPLIT;     // first wave of this stream
+  const int h = blockIdx.y;
+  const int i0 = blockIdx.z * TQ;
+  const int nq = min(TQ, p.T - i0);
+  const int b_raw = blockIdx.x * 4 + sw;
+  const bool active = b_raw < p.B;  // uniform per wave
+  const int b = active ? b_raw : p.B - 1;
+  const int hcol = h * DK + hf * 64;  // first column of the wave
+  const int M = p.pg.max_pages;
+  constexpr int mask_mode = MODE;  // 0 none, 1 mask bytes, 2 stream state
+
+  // ---------------- prologue: every load independent of the page table
+  int A = 0, ring_lane = -1;
+  if (p.pg.rows) {
+    const int32_t* row = p.pg.rows + (int64_t)b * p.pg.rows_stride;
+    A = row[0];
+    ring_lane = row[1 + min(lane, M - 1)];
+  }
+  int64_t st_pr = 0, st_cl = 0, st_n = p.len_scalar;
+  if (mask_mode == 2) {
+    st_pr = p.st_proc[b];
+    st_cl = p.st_cl[b];
+    if (p.st_len) st_n = p.st_len[b];
+  }
+  // A operand source: row m = q16 is (q+u)_hi, (q+u)_lo, (q+v)_hi, (q+v)_lo of
+  // query m & 1 for m < 8, zero above; element e of k-step ks is column
+  // kg*16 + ks*8 + e of the wave's 64
+  const int a_ii = q16 & 1;
+  const int a_kind = q16 >> 1;  // 0 u-hi, 1 u-lo, 2 v-hi, 3 v-lo, >= 4 zero
+  u32x4 qraw[KS], braw[KS];
+  {
+    const int ic = min(i0 + a_ii, p.T - 1);
+    const ST* qrow = p.q + b * p.q_sb + (int64_t)ic * p.q_st + hcol + kg * 16;
+    const ST* brow = (a_kind < 2 ? p.bu : p.bv) + hcol + kg * 16;
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) o[e] = 0.f;
-    for (int w = 0; w < W; ++w) {
-      const float* c = comb + (w * TQ + ii) * (2 + DK);
-      const float f = __builtin_amdgcn_exp2f(c[0] - mx);
-      L = fmaf(c[1], f, L);
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) o[e] = fmaf(c[2 + gg * VEC + e], f, o[e]);
+    for (int ks = 0; ks < KS; ++ks) {
+      qraw[ks] = ld16(qrow + ks * 8);
+      braw[ks] = ld16(brow + ks * 8);
     }
-    const float inv = L > 0.f ? 1.f / L : 0.f;
+  }
+  u32x4 pst[PCH];
+  uint8_t mk[NT][TQ];
+  auto load_tile_shared = [&](int jb) {
+    const int rb = jb + p.T - i0 - TQ;
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) o[e] *= inv;
-    st16(p.out + b * p.o_sb + (int64_t)(i0 + ii) * p.o_st + h * DK + gg * VEC, Tr<ST>::pack(o));
+    for (int c = 0; c < PCH; ++c) {
+      const int idx = min((int)threadIdx.x + c * NTH, PROWS * CHR - 1);
+      const int r = idx / CHR;
+      const int ch = idx - r * CHR;
+      const int rc = min(max(rb + r, 0), p.pos_rows - 1);
+      pst[c] = ld16(p.pos + rc * p.pos_sr + h * DK + ch * 8);
+    }
+    if (mask_mode == 1) {
+#pragma unroll
+      for (int kt = 0; kt < NT; ++kt)
+#pragma unroll
+        for (int ii = 0; ii < TQ; ++ii) {
+          const int ic = min(i0 + ii, p.T - 1);
+          const int jc = min(jb + 16 * kt + q16, p.Lk - 1);
+          mk[kt][ii] = p.mask[b * p.m_sb + h * p.m_sh + (int64_t)ic * p.m_st + jc];
+        }
+    }
+  };
+  load_tile_shared(0);
+
+  // ---------------- A operand (hi / lo split of the fp32 sums)
+  u32x4 aop[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    float qf[8], bf[8];
+    Tr<ST>::unpack(qraw[ks], qf);
+    Tr<ST>::unpack(braw[ks], bf);
+    uint32_t bits[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x = (a_ii < nq ? qf[e] : 0.f) + bf[e];
+      float hi, dummy;
+      const uint32_t hb = Mma<ST>::round(x, &hi);
+      const uint32_t lb = Mma<ST>::round(x - hi, &dummy);
+      bits[e] = a_kind >= 4 ? 0u : ((a_kind & 1) ? lb : hb);
+    }
+    aop[ks] = u32x4{bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16),
+                    bits[4] | (bits[5] << 16), bits[6] | (bits[7] << 16)};
+  }
+  StreamMask sm{};
+  int qchunk[TQ];
+  if (mask_mode == 2) {
+    sm.set(st_pr, st_cl, st_n, p.left, p.chunk_size, p.left_chunks);
+#pragma unroll
+    for (int ii = 0; ii < TQ; ++ii) qchunk[ii] = sm.query_chunk(i0 + ii);
+  }
+
+  // value-sum accumulators: lane = columns g*8 .. g*8+7 of keys rl (mod RLW)
+  const int g = lane % G;
+  const int rl = lane / G;
+  float acc[TQ][VEC];
+  float m_run[TQ], l_run[TQ];
+#pragma unroll
+  for (int ii = 0; ii < TQ; ++ii) {
+    m_run[ii] = NEG;
+    l_run[ii] = 0.f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[ii][e] = 0.f;
+  }
+  const ST* kn_b = p.kn + b * p.k_sb;
+  const ST* vn_b = p.vn + b * p.v_sb;
+  const bool paged = p.pg.rows != nullptr;
+
+  for (int tile = 0; tile < p.tiles; ++tile) {
+    const int jb = tile * KT;
+
+    // ---- stage the position rows of the tile
+    {
+      const int rb = jb + p.T - i0 - TQ;
+#pragma unroll
+      for (int c = 0; c < PCH; ++c) {
+        const int idx = threadIdx.x + c * NTH;
+        if (idx < PROWS * CHR) {
+          const int r = idx / CHR;
+          const int ch = idx - r * CHR;
+          const bool in = rb + r >= 0 && rb + r < p.pos_rows;
+          *reinterpret_cast<u32x4*>(pos_lds + r * PSTRIDE + ch * 16) =
+              in ? pst[c] : u32x4{0u, 0u, 0u, 0u};
+        }
+      }
+    }
+    uint8_t mkt[NT][TQ];
+#pragma unroll
+    for (int kt = 0; kt < NT; ++kt)
+#pragma unroll
+      for (int ii = 0; ii < TQ; ++ii) mkt[kt][ii] = mask_mode == 1 ? mk[kt][ii] : (uint8_t)0;
+
+    // ---- K rows (MFMA B layout: lane = key q16, columns kg*16 ..) and V rows
+    //      (lane = columns g*8 .., key rl mod RLW): every page lookup first,
+    //      then all loads back to back
+    int kpos[NT], vpos[NV], kpage[NT], vpage[NV];
+#pragma unroll
+    for (int kt = 0; kt < NT; ++kt) {
+      kpos[kt] = A - p.left + min(jb + 16 * kt + q16, p.Lk - 1);
+      kpage[kt] = paged ? __shfl(ring_lane, (int)((((uint32_t)max(kpos[kt], 0)) >> p.pg.page_shift) %
+                                                  (uint32_t)M))
+                        : -1;
+    }
+#pragma unroll
+    for (int n = 0; n < NV; ++n) {
+      vpos[n] = A - p.left + min(jb + n * RLW + rl, p.Lk - 1);
+      vpage[n] = paged ? __shfl(ring_lane, (int)((((uint32_t)max(vpos[n], 0)) >> p.pg.page_shift) %
+                                                 (uint32_t)M))
+                       : -1;
+    }
+    u32x4 kr[NT][KS], vr[NV];
+    bool okk[NT], okv[NV];
+    const uint32_t pmask = (1u << p.pg.page_shift) - 1u;
+#pragma unroll
+    for (int kt = 0; kt < NT; ++kt) {
+      const int j = jb + 16 * kt + q16;
+      const int jc = min(j, p.Lk - 1);
+      const bool fresh = jc >= p.left;
+      const bool pok = kpos[kt] >= 0 && kpage[kt] >= 0 && kpage[kt] < p.pg.num_pages;
+      okk[kt] = j < p.Lk && (fresh || pok);
+      const ST* ka = (fresh || !pok)
+                         ? kn_b + (int64_t)(fresh ? jc - p.left : 0) * p.k_st
+                         : p.kp + (int64_t)kpage[kt] * p.pg.page_elems +
+                               (int64_t)((uint32_t)kpos[kt] & pmask) * p.pg.D;
+      ka += hcol + kg * 16;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kr[kt][ks] = ld16(ka + ks * 8);
+    }
+#pragma unroll
+    for (int n = 0; n < NV; ++n) {
+      const int j = jb + n * RLW + rl;
+      const int jc = min(j, p.Lk - 1);
+      const bool fresh = jc >= p.left;
+      const bool pok = vpos[n] >= 0 && vpage[n] >= 0 && vpage[n] < p.pg.num_pages;
+      okv[n] = j < p.Lk && (fresh || pok);
+      const ST* va = (fresh || !pok)
+                         ? vn_b + (int64_t)(fresh ? jc - p.left : 0) * p.v_st
+                         : p.vp + (int64_t)vpage[n] * p.pg.page_elems +
+                               (int64_t)((uint32_t)vpos[n] & pmask) * p.pg.D;
+      vr[n] = ld16(va + hcol + g * VEC);
+    }
+    if (tile + 1 < p.tiles) load_tile_shared(jb + KT);  // prefetch behind K/V
+    __syncthreads();  // position rows staged
+
+    // ---- (q+v).pos over the wave's columns: D rows 4..7 (lanes 16..31)
+#pragma unroll
+    for (int pt = 0; pt < NPT; ++pt) {
+      f32x4_t d = {0.f, 0.f, 0.f, 0.f};
+      const uint8_t* src = pos_lds + (pt * 16 + q16) * PSTRIDE + (hf * 64 + kg * 16) * 2;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        d = Mma<ST>::run(aop[ks], *reinterpret_cast<const u32x4*>(src + ks * 16), d);
+      if (kg == 1) {
+        bd_lds[wave][0][pt * 16 + q16] = d[0] + d[2];
+        bd_lds[wave][1][pt * 16 + q16] = d[1] + d[3];
+      }
+    }
+    // ---- (q+u).k over the wave's columns: D rows 0..3 (lanes 0..15)
+#pragma unroll
+    for (int kt = 0; kt < NT; ++kt) {
+      f32x4_t d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) d = Mma<ST>::run(aop[ks], kr[kt][ks], d);
+      if (kg == 0) {
+        ac_lds[wave][0][16 * kt + q16] = d[0] + d[2];
+        ac_lds[wave][1][16 * kt + q16] = d[1] + d[3];
+      }
+    }
+    __syncthreads();  // partial dot products of the stream's waves in LDS
+
+    // ---- scores (lanes 0..15 hold key 16*kt + q16), softmax over the tile
+    float s[NT][TQ];
+#pragma unroll
+    for (int kt = 0; kt < NT; ++kt) {
+      const int j = jb + 16 * kt + q16;
+      const int jc = min(j, p.Lk - 1);
+#pragma unroll
+      for (int ii = 0; ii < TQ; ++ii) {
+        float ac = 0.f, bd = 0.f;
+#pragma unroll
+        for (int x = 0; x < SPLIT; ++x) {
+          ac += ac_lds[w0 + x][ii][16 * kt + q16];
+          bd += bd_lds[w0 + x][ii][16 * kt + q16 + TQ - 1 - ii];
+        }
+        if (!okk[kt]) ac = 0.f;  // a key outside the stream's history reads as zeros
+        bool msk = false;
+        if (mask_mode == 1) msk = mkt[kt][ii] != 0;
+        if (mask_mode == 2) msk = sm.masked(i0 + ii, qchunk[ii], jc);
+        const float sc = msk ? fmaf(ac, p.scale, MASKED) : (ac + bd) * p.scale;
+        s[kt][ii] = (kg == 0 && j < p.Lk && ii < nq) ? sc : NEG;
+      }
+    }
+#pragma unroll
+    for (int ii = 0; ii < TQ; ++ii) {
+      float tmax = NEG;
+#pragma unroll
+      for (int kt = 0; kt < NT; ++kt) tmax = fmaxf(tmax, s[kt][ii]);
+      const float mnew = fmaxf(m_run[ii], lane0(row16_max(tmax)));
+      const float corr = __builtin_amdgcn_exp2f(m_run[ii] - mnew);
+      m_run[ii] = mnew;
+      float lsum = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < NT; ++kt) {
+        const float e = s[kt][ii] > 0.5f * NEG ? __builtin_amdgcn_exp2f(s[kt][ii] - mnew) : 0.f;
+        lsum += e;
+        if (kg == 0) p_lds[wave][16 * kt + q16][ii] = e;
+      }
+      l_run[ii] = l_run[ii] * corr + lane0(group_sum<16>(lsum));
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc[ii][e] *= corr;
+    }
+    wave_lds_sync();
+
+    // ---- value sum over the wave's columns
+#pragma unroll
+    for (int n = 0; n < NV; ++n) {
+      const float2 pp = *reinterpret_cast<const float2*>(&p_lds[wave][n * RLW + rl][0]);
+      float vf[VEC];
+      Tr<ST>::unpack(vr[n], vf);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float x = okv[n] ? vf[e] : 0.f;
+        acc[0][e] = fmaf(pp.x, x, acc[0][e]);
+        acc[1][e] = fmaf(pp.y, x, acc[1][e]);
+      }
+    }
+
+    // ---- append this step's frames to the pages (query group 0 only); the
+    //      page ids were looked up above, outside any divergent branch
+    if (p.append && blockIdx.z == 0 && active) {
+#pragma unroll
+      for (int kt = 0; kt < NT; ++kt) {
+        const int j = jb + 16 * kt + q16;
+        const bool pok = kpage[kt] >= 0 && kpage[kt] < p.pg.num_pages;
+        if (j < p.Lk && j >= p.left && pok) {
+          ST* dst = p.kp + (int64_t)kpage[kt] * p.pg.page_elems +
+                    (int64_t)((uint32_t)kpos[kt] & pmask) * p.pg.D + hcol + kg * 16;
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks) st16(dst + ks * 8, kr[kt][ks]);
+        }
+      }
+#pragma unroll
+      for (int n = 0; n < NV; ++n) {
+        const int j = jb + n * RLW + rl;
+        const bool pok = vpage[n] >= 0 && vpage[n] < p.pg.num_pages;
+        if (j < p.Lk && j >= p.left && pok)
+          st16(p.vp + (int64_t)vpage[n] * p.pg.page_elems +
+                   (int64_t)((uint32_t)vpos[n] & pmask) * p.pg.D + hcol + g * VEC,
+               vr[n]);
+      }
+    }
+    __syncthreads();  // the next tile restages pos_lds and rewrites bd / ac / p
+  }
+
+  // ---- combine the RLW key groups (same running max everywhere) and write
+#pragma unroll
+  for (int ii = 0; ii < TQ; ++ii)
+#pragma unroll
+    for (int off = G; off < 64; off <<= 1)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc[ii][e] += __shfl_xor(acc[ii][e], off);
+  if (active && rl == 0) {
+#pragma unroll
+    for (int ii = 0; ii < TQ; ++ii) {
+      if (ii >= nq) continue;
+      const float inv = l_run[ii] > 0.f ? 1.f / l_run[ii] : 0.f;
+      float o[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) o[e] = acc[ii][e] * inv;
+      st16(p.out + b * p.o_sb + (int64_t)(i0 + ii) * p.o_st + hcol + g * VEC, Tr<ST>::pack(o));
+    }
   }
 }
 
@@ -659,79 +1126,89 @@ unsigned grid_for(int64_t total, int block) {
 // ---- attention dispatch
 
 template <typename ST, int DK, int TQ, int NR>
-int launch_attn_t(const pk_attn_args* a, const AttnK<ST>& k, int W, hipStream_t s) {
-  constexpr int VEC = Tr<ST>::VEC;
-  constexpr int G = DK / VEC;
-  constexpr int RLW = 64 / G;
-  constexpr int CROWS = RLW * NR + TQ - 1;
+int launch_attn_t(const pk_attn_args* a, const AttnK<ST>& k, hipStream_t s) {
   dim3 grid((unsigned)(a->batch * a->num_heads), (unsigned)((a->chunk + TQ - 1) / TQ));
-  dim3 block((unsigned)(64 * W));
-  const size_t smem = sizeof(float) * ((size_t)W * TQ * CROWS + (size_t)W * TQ * (2 + DK));
+  dim3 block(64u);
   if (a->start_event || a->stop_event) {
-    hipExtLaunchKernelGGL(relpos_attn_kernel<ST, DK, TQ, NR>, grid, block, (uint32_t)smem, s,
+    hipExtLaunchKernelGGL(relpos_attn_kernel<ST, DK, TQ, NR>, grid, block, 0u, s,
                           (hipEvent_t)a->start_event, (hipEvent_t)a->stop_event, 0u, k);
   } else {
-    hipLaunchKernelGGL((relpos_attn_kernel<ST, DK, TQ, NR>), grid, block, smem, s, k);
+    hipLaunchKernelGGL((relpos_attn_kernel<ST, DK, TQ, NR>), grid, block, 0, s, k);
   }
   return check_launch("pk_paged_relpos_attn");
 }
 
+// Rows per lane a kernel is built for.
+constexpr int kRowsPerLane[4] = {4, 9, 12, 18};
+
 template <typename ST, int DK, int TQ>
-int launch_attn_nr(const pk_attn_args* a, const AttnK<ST>& k, int NR, int W, hipStream_t s) {
+int launch_attn_nr(const pk_attn_args* a, const AttnK<ST>& k, int NR, hipStream_t s) {
   switch (NR) {
-    case 2: return launch_attn_t<ST, DK, TQ, 2>(a, k, W, s);
-    case 3: return launch_attn_t<ST, DK, TQ, 3>(a, k, W, s);
-    case 4: return launch_attn_t<ST, DK, TQ, 4>(a, k, W, s);
-    case 6: return launch_attn_t<ST, DK, TQ, 6>(a, k, W, s);
+    case 4: return launch_attn_t<ST, DK, TQ, 4>(a, k, s);
+    case 9: return launch_attn_t<ST, DK, TQ, 9>(a, k, s);
+    case 12: return launch_attn_t<ST, DK, TQ, 12>(a, k, s);
+    case 18: return launch_attn_t<ST, DK, TQ, 18>(a, k, s);
     default: return fail(PK_ERR_UNSUPPORTED, "pk_paged_relpos_attn: rows_per_lane %d not built", NR);
   }
 }
 
 template <typename ST, int DK>
-int launch_attn_tq(const pk_attn_args* a, const AttnK<ST>& k, int TQ, int NR, int W,
-                   hipStream_t s) {
+int launch_attn_tq(const pk_attn_args* a, const AttnK<ST>& k, int TQ, int NR, hipStream_t s) {
   switch (TQ) {
-    case 1: return launch_attn_nr<ST, DK, 1>(a, k, NR, W, s);
-    case 2: return launch_attn_nr<ST, DK, 2>(a, k, NR, W, s);
-    case 4: return launch_attn_nr<ST, DK, 4>(a, k, NR, W, s);
+    case 1: return launch_attn_nr<ST, DK, 1>(a, k, NR, s);
+    case 2: return launch_attn_nr<ST, DK, 2>(a, k, NR, s);
     default: return fail(PK_ERR_UNSUPPORTED, "pk_paged_relpos_attn: query group %d not built", TQ);
   }
 }
 
-// Queries per workgroup: 1, 2 or 4 for chunks up to 4 frames, else groups of 2.
-int pick_tq(int T) {
-  if (T <= 1) return 1;
-  if (T == 2) return 2;
-  if (T <= 4) return 4;
-  return 2;
-}
+// Queries per workgroup: one chunk frame alone, otherwise groups of two.
+int pick_tq(int T) { return T <= 1 ? 1 : 2; }
 
-// Rows per lane NR and waves per workgroup W for a window of Lk keys: prefer a
-// single tile, then the least padding, then NR close to 4.
-void pick_tiling(int Lk, int rlw, int hint, int* NR, int* W, int* tiles) {
-  static const int cand[4] = {2, 3, 4, 6};
-  int best_nr = 0, best_w = 0, best_t = 0;
+// Rows per lane NR for a window of Lk keys with rlw rows per wave load: the
+// fewest tiles, then the least padding (hint > 0 forces NR).
+void pick_tiling(int Lk, int rlw, int hint, int* NR, int* tiles) {
+  int best_nr = 0, best_t = 0;
   long best_score = -1;
-  for (int c : cand) {
+  for (int c : kRowsPerLane) {
     if (hint > 0 && c != hint) continue;
-    const int per_wave = rlw * c;
-    int w = (Lk + per_wave - 1) / per_wave;
-    if (w > 8) w = 8;
-    if (w < 1) w = 1;
-    const int t = (Lk + w * per_wave - 1) / (w * per_wave);
-    const int waste = t * w * per_wave - Lk;
-    const int dist = c > 4 ? c - 4 : 4 - c;
-    const long score = (long)t * 1000000L + (long)waste * 100L + dist;
+    const int per_tile = rlw * c;
+    const int t = (Lk + per_tile - 1) / per_tile;
+    const int waste = t * per_tile - Lk;
+    const long score = (long)t * 1000000L + waste;
     if (best_score < 0 || score < best_score) {
       best_score = score;
       best_nr = c;
-      best_w = w;
       best_t = t;
     }
   }
   *NR = best_nr;
-  *W = best_w;
   *tiles = best_t;
+}
+
+// Matrix-core path (fp16 / bf16): workgroups of 4 streams x one head x one
+// pair of queries, key tiles of 16 * kMfmaTiles rows.
+constexpr int kMfmaTiles = 5;
+
+template <typename ST, int DK, int MODE>
+int launch_attn_mfma_mode(const pk_attn_args* a, const AttnK<ST>& k, hipStream_t s) {
+  dim3 grid((unsigned)((a->batch + 3) / 4), (unsigned)a->num_heads, (unsigned)((a->chunk + 1) / 2));
+  dim3 block(256u * (DK / 64));
+  if (a->start_event || a->stop_event) {
+    hipExtLaunchKernelGGL(relpos_attn_mfma_kernel<ST, DK, kMfmaTiles, MODE>, grid, block, 0u, s,
+                          (hipEvent_t)a->start_event, (hipEvent_t)a->stop_event, 0u, k);
+  } else {
+    hipLaunchKernelGGL((relpos_attn_mfma_kernel<ST, DK, kMfmaTiles, MODE>), grid, block, 0, s, k);
+  }
+  return check_launch("pk_paged_relpos_attn");
+}
+
+template <typename ST, int DK>
+int launch_attn_mfma(const pk_attn_args* a, AttnK<ST>& k, hipStream_t s) {
+  constexpr int KT = 16 * kMfmaTiles;
+  k.tiles = (k.Lk + KT - 1) / KT;
+  if (k.mask) return launch_attn_mfma_mode<ST, DK, 1>(a, k, s);
+  if (k.st_proc) return launch_attn_mfma_mode<ST, DK, 2>(a, k, s);
+  return launch_attn_mfma_mode<ST, DK, 0>(a, k, s);
 }
 
 template <typename ST>
@@ -783,6 +1260,9 @@ int attn_typed(const pk_attn_args* a, hipStream_t s) {
     if (a->pages.d_model != D)
       return fail(PK_ERR_INVALID, "%s: pages.d_model %d != heads*head_dim %d", what,
                   a->pages.d_model, D);
+    if (a->pages.max_pages > 64)
+      return fail(PK_ERR_UNSUPPORTED, "%s: max_pages %d > 64 (window longer than 64 pages)", what,
+                  a->pages.max_pages);
     const int64_t lo = layer_offset(a->pages, a->layer);
     k.kp = static_cast<ST*>(a->pages.k_pool) + lo;
     k.vp = static_cast<ST*>(a->pages.v_pool) + lo;
@@ -796,9 +1276,23 @@ int attn_typed(const pk_attn_args* a, hipStream_t s) {
   k.m_sb = a->mask_stride_b;
   k.m_sh = a->mask_stride_h;
   k.m_st = a->mask_stride_t;
+  if (!a->mask && a->processed_frames) {
+    if (!a->cache_lengths)
+      return fail(PK_ERR_INVALID, "%s: processed_frames needs cache_lengths", what);
+    if (a->chunk_size <= 0)
+      return fail(PK_ERR_INVALID, "%s: chunk_size %d must be > 0 for the streaming mask", what,
+                  a->chunk_size);
+    k.st_proc = a->processed_frames;
+    k.st_cl = a->cache_lengths;
+    k.st_len = a->lengths;
+    k.len_scalar = a->length_scalar;
+    k.chunk_size = a->chunk_size;
+    k.left_chunks = a->left / a->chunk_size;
+  }
   k.out = static_cast<ST*>(a->out);
   k.o_sb = a->out_stride_b;
   k.o_st = a->out_stride_t;
+  k.B = a->batch;
   k.T = a->chunk;
   k.H = a->num_heads;
   k.left = a->left;
@@ -806,17 +1300,25 @@ int attn_typed(const pk_attn_args* a, hipStream_t s) {
   k.append = a->append ? 1 : 0;
   k.scale = 1.4426950408889634f / sqrtf((float)DK);
 
+  if (a->num_heads > 65535 || a->chunk > 2 * 65535)
+    return fail(PK_ERR_INVALID, "%s: num_heads or chunk exceeds the launch grid", what);
+  if constexpr (!std::is_same<ST, float>::value) {
+    if (a->rows_per_lane == 0) {
+      if (DK == 64) return launch_attn_mfma<ST, 64>(a, k, s);
+      return launch_attn_mfma<ST, 128>(a, k, s);
+    }
+  }
   const int G = DK / VEC;
   const int rlw = 64 / G;
   const int TQ = pick_tq(a->chunk);
-  int NR = 0, W = 0, tiles = 0;
-  pick_tiling(Lk, rlw, a->rows_per_lane, &NR, &W, &tiles);
+  int NR = 0, tiles = 0;
+  pick_tiling(Lk, rlw, a->rows_per_lane, &NR, &tiles);
   if (NR == 0)
-    return fail(PK_ERR_UNSUPPORTED, "%s: rows_per_lane %d not built (2, 3, 4, 6)", what,
+    return fail(PK_ERR_UNSUPPORTED, "%s: rows_per_lane %d not built (4, 9, 12, 18)", what,
                 a->rows_per_lane);
   k.tiles = tiles;
-  if (DK == 64) return launch_attn_tq<ST, 64>(a, k, TQ, NR, W, s);
-  return launch_attn_tq<ST, 128>(a, k, TQ, NR, W, s);
+  if (DK == 64) return launch_attn_tq<ST, 64>(a, k, TQ, NR, s);
+  return launch_attn_tq<ST, 128>(a, k, TQ, NR, s);
 }
 
 template <typename ST>

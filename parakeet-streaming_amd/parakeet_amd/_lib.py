@@ -15,7 +15,7 @@ from pathlib import Path
 LIB_NAME = "libparakeet_paged.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -108,6 +108,11 @@ class AttnArgs(ctypes.Structure):
         ("mask_stride_b", c_int64),
         ("mask_stride_h", c_int64),
         ("mask_stride_t", c_int64),
+        ("processed_frames", c_void_p),
+        ("cache_lengths", c_void_p),
+        ("lengths", c_void_p),
+        ("length_scalar", c_int64),
+        ("chunk_size", c_int32),
         ("out", c_void_p),
         ("out_stride_b", c_int64),
         ("out_stride_t", c_int64),

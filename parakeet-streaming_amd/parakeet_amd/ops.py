@@ -165,6 +165,33 @@ def _mask_strides(mask: torch.Tensor, B: int, H: int, T: int, Lk: int) -> tuple[
     return mask, mask.stride(0), sh, mask.stride(2)
 
 
+@dataclass
+class StreamMaskState:
+    """Per-stream streaming state from which the attention kernel evaluates the
+    streaming mask of ConformerEncoder._create_streaming_masks
+    (parakeet/modules/encoder.py:167-227) score by score, instead of reading a
+    materialised [B, T, L] mask.  processed_frames / cache_lengths: int64 [B] on
+    the device; lengths: int64 [B] or one int for every stream; chunk_size:
+    att_context_size[1] + 1.  Needs 0 <= cache_lengths <= left and
+    processed_frames < 2**31."""
+
+    processed_frames: torch.Tensor
+    cache_lengths: torch.Tensor
+    lengths: torch.Tensor | int
+    chunk_size: int
+
+    def check(self, B: int, dev: torch.device) -> None:
+        for name, t in (("processed_frames", self.processed_frames), ("cache_lengths", self.cache_lengths)):
+            if t.dtype != torch.int64 or tuple(t.shape) != (B,) or not t.is_contiguous() or t.device != dev:
+                raise ValueError(f"{name} must be contiguous int64 [{B}] on {dev}")
+        if isinstance(self.lengths, torch.Tensor):
+            t = self.lengths
+            if t.dtype != torch.int64 or tuple(t.shape) != (B,) or not t.is_contiguous() or t.device != dev:
+                raise ValueError(f"lengths must be contiguous int64 [{B}] on {dev}")
+        if int(self.chunk_size) <= 0:
+            raise ValueError("chunk_size must be > 0")
+
+
 def paged_relpos_attn(
     query: torch.Tensor,
     key: torch.Tensor,
@@ -181,6 +208,7 @@ def paged_relpos_attn(
     append: bool = True,
     out: torch.Tensor | None = None,
     rows_per_lane: int = 0,
+    mask_state: StreamMaskState | None = None,
     start_event=None,
     stop_event=None,
 ) -> torch.Tensor:
@@ -192,6 +220,8 @@ def paged_relpos_attn(
     query/key/value: [B, T, D] (views of the qkv projection are fine);
     pos: [>= L + T - 1, D] (linear_pos of the sinusoid slice, batch dim dropped);
     bias_u/bias_v: [H, dk]; mask: [B, T, L] / [B, 1|H, T, L] bool, True = masked.
+    With ``mask`` None and ``mask_state`` given, the kernel evaluates the
+    streaming mask from the stream state instead.
     """
     B, T, D = query.shape
     dt = query.dtype
@@ -239,6 +269,15 @@ def paged_relpos_attn(
         if mask.device != dev:
             raise ValueError("mask on a different device")
         a.mask, a.mask_stride_b, a.mask_stride_h, a.mask_stride_t = mask.data_ptr(), sb, sh, st
+    elif mask_state is not None:
+        mask_state.check(B, dev)
+        a.processed_frames = mask_state.processed_frames.data_ptr()
+        a.cache_lengths = mask_state.cache_lengths.data_ptr()
+        if isinstance(mask_state.lengths, torch.Tensor):
+            a.lengths = mask_state.lengths.data_ptr()
+        else:
+            a.length_scalar = int(mask_state.lengths)
+        a.chunk_size = int(mask_state.chunk_size)
     a.out, a.out_stride_b, a.out_stride_t = out.data_ptr(), out.stride(0), out.stride(1)
     a.rows_per_lane = int(rows_per_lane)
     if start_event is not None:

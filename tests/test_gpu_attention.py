@@ -39,7 +39,7 @@ def _run(cuda, dtype, B, H, dk, left, right, P, steps, mask_kind="engine", shuff
     for step in range(steps):
         sc.open_step()
         cl = np.minimum(proc, left)
-        if mask_kind == "engine":
+        if mask_kind in ("engine", "state"):
             lengths = np.full(B, T)
         else:
             lengths = rng.integers(1, T + 1, size=B)
@@ -48,11 +48,19 @@ def _run(cuda, dtype, B, H, dk, left, right, P, steps, mask_kind="engine", shuff
             mask_np = mask_np | (rng.random(mask_np.shape) < 0.2)
             mask_np[:, :, left:] = False  # keep this chunk's frames visible
         mask = torch.from_numpy(mask_np).to(cuda)
+        state = None
+        if mask_kind.startswith("state"):
+            # the kernel evaluates the streaming mask from the stream state
+            mask = None
+            state = ops.StreamMaskState(
+                torch.from_numpy(proc.copy()).to(cuda), torch.from_numpy(cl.astype(np.int64)).to(cuda),
+                torch.from_numpy(lengths.astype(np.int64)).to(cuda), right + 1,
+            )
         for layer in range(sc.Ly):
             x, (q, k, v) = sc.frames()
             out = ops.paged_relpos_attn(
                 q, k, v, pos, bu, bv, mask, num_heads=H, left=left, pages=sc.pages, layer=layer,
-                append=True, rows_per_lane=rows_per_lane,
+                append=True, rows_per_lane=rows_per_lane, mask_state=state,
             )
             dk_win, dv_win = sc.dense_update(layer, k, v)
             ref = oa.relpos_attention(to_np64(q), dk_win, dv_win, to_np64(pos), to_np64(bu), to_np64(bv), mask_np, H)
@@ -91,6 +99,17 @@ def test_other_chunks(cuda, right):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("dtype,kind", [(torch.bfloat16, "state"), (torch.float16, "state-ragged"), (torch.float32, "state")])
+def test_state_mask_stepped(cuda, dtype, kind):
+    _run(cuda, dtype, B=3, H=8, dk=128, left=70, right=1, P=16, steps=40, mask_kind=kind)
+
+
+@pytest.mark.gpu
+def test_state_mask_t14(cuda):
+    _run(cuda, torch.bfloat16, B=2, H=8, dk=128, left=70, right=13, P=16, steps=10, mask_kind="state-ragged")
+
+
+@pytest.mark.gpu
 def test_random_masks_and_ragged_lengths(cuda):
     _run(cuda, torch.bfloat16, B=4, H=8, dk=64, left=70, right=1, P=16, steps=20, mask_kind="random", shuffle=True)
 
@@ -102,7 +121,7 @@ def test_long_window_multi_tile(cuda):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("nr", [2, 3, 4, 6])
+@pytest.mark.parametrize("nr", [4, 9, 12, 18])
 def test_every_row_tiling(cuda, nr):
     _run(cuda, torch.bfloat16, B=2, H=8, dk=128, left=70, right=1, P=16, steps=8, rows_per_lane=nr, layers=1)
 
@@ -136,4 +155,58 @@ def test_bad_shapes_raise(cuda):
         ops.paged_relpos_attn(q, k, v, pos[:3], bu, bv, None, num_heads=2, left=6, pages=sc.pages)
     with pytest.raises(RuntimeError, match="head_dim"):
         ops.paged_relpos_attn(q, k, v, pos, bu.reshape(4, 32), bv.reshape(4, 32), None, num_heads=4, left=6, pages=sc.pages)
+    torch.cuda.synchronize()
+
+
+def _mask_grid(left, T):
+    cases = []
+    for proc in range(0, 3 * (left + T) + 1):
+        for cl in sorted({0, min(proc, left), min(proc, left) // 2}):
+            for n in range(0, T + 1):
+                cases.append((proc, cl, n))
+    return cases
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("left,right,dtype", [(70, 1, torch.bfloat16), (70, 13, torch.float16), (9, 2, torch.float32), (5, 0, torch.float16)])
+def test_state_mask_identical_to_mask_tensor(cuda, left, right, dtype):
+    """The streaming mask evaluated in the kernel from (processed_frames,
+    cache_lengths, lengths) gives bit-identical outputs to the same kernel fed
+    the oracle's mask tensor (encoder.py:167-227), over a grid of stream states
+    with ragged lengths."""
+    print(f"\n[state-mask] left={left} right={right} dtype={dtype}", flush=True)
+    T = right + 1
+    L = left + T
+    H, dk = 2, 64
+    D = H * dk
+    cases = _mask_grid(left, T)
+    B = len(cases)
+    proc = np.array([c[0] for c in cases], dtype=np.int64)
+    cl = np.array([c[1] for c in cases], dtype=np.int64)
+    n = np.array([c[2] for c in cases], dtype=np.int64)
+    P = 16
+    M = (L + P - 2) // P + 1
+    g = torch.Generator().manual_seed(11)
+    kp = torch.randn(1, B * M, P, D, generator=g).to(dtype).to(cuda)
+    vp = torch.randn(1, B * M, P, D, generator=g).to(dtype).to(cuda)
+    rows = np.zeros((B, 1 + M), dtype=np.int32)
+    rows[:, 0] = 1000
+    rows[:, 1:] = np.arange(B * M, dtype=np.int32).reshape(B, M)
+    pages = ops.PagedKV(kp, vp, torch.from_numpy(rows).to(cuda), M)
+    x = torch.randn(B, T, 3 * D, generator=g).to(dtype).to(cuda)
+    q, k, v = x.chunk(3, dim=-1)
+    pos = (torch.randn(L + T - 1, D, generator=g) * 0.5).to(dtype).to(cuda)
+    bu = (torch.randn(H, dk, generator=g) * 0.02).to(dtype).to(cuda)
+    bv = (torch.randn(H, dk, generator=g) * 0.02).to(dtype).to(cuda)
+    _, mask_np = om.create_streaming_masks(T, cl, proc, n, (left, right))
+    out_m = ops.paged_relpos_attn(q, k, v, pos, bu, bv, torch.from_numpy(mask_np).to(cuda), num_heads=H, left=left, pages=pages, append=False)
+    st = ops.StreamMaskState(torch.from_numpy(proc).to(cuda), torch.from_numpy(cl).to(cuda), torch.from_numpy(n).to(cuda), right + 1)
+    out_s = ops.paged_relpos_attn(q, k, v, pos, bu, bv, None, num_heads=H, left=left, pages=pages, append=False, mask_state=st)
+    assert torch.equal(out_m, out_s)
+    # scalar length form
+    st1 = ops.StreamMaskState(st.processed_frames, st.cache_lengths, T, right + 1)
+    _, mask1 = om.create_streaming_masks(T, cl, proc, T, (left, right))
+    out_m1 = ops.paged_relpos_attn(q, k, v, pos, bu, bv, torch.from_numpy(mask1).to(cuda), num_heads=H, left=left, pages=pages, append=False)
+    out_s1 = ops.paged_relpos_attn(q, k, v, pos, bu, bv, None, num_heads=H, left=left, pages=pages, append=False, mask_state=st1)
+    assert torch.equal(out_m1, out_s1)
     torch.cuda.synchronize()
