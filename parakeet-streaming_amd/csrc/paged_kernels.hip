@@ -207,6 +207,7 @@ struct AttnK {
   const int64_t* st_len;
   int64_t len_scalar;
   int32_t chunk_size, left_chunks;
+  uint32_t c_magic;
   ST* out;
   int64_t o_sb, o_st;
   int32_t B, T, H, left, Lk, append, tiles;
@@ -218,8 +219,14 @@ struct AttnK {
 // key_start = ks_q * C + ks_r, so only small non-negative values are divided.
 struct StreamMask {
   int cl, len, offset, ks_q, ks_r, C, left_chunks;
+  uint32_t magic;  // floor(2^32 / C) + 1 for C >= 2: x / C == umulhi(x, magic), x < 2^32 / C
+                   // (the small per-score arguments, bounded on the host)
 
-  __device__ inline void set(int64_t pr, int64_t c, int64_t n, int left, int C_, int lc) {
+  __device__ inline int div_c(uint32_t x) const {
+    return C == 1 ? (int)x : (int)__umulhi(x, magic);
+  }
+  __device__ inline void set(int64_t pr, int64_t c, int64_t n, int left, int C_, int lc,
+                             uint32_t magic_) {
     n = n < -1 ? -1 : (n > 0x7fffffff ? 0x7fffffff : n);
     const int64_t ks = pr - c > 0 ? pr - c : 0;  // encoder.py:189
     cl = (int)c;
@@ -227,22 +234,17 @@ struct StreamMask {
     offset = left - cl;  // encoder.py:214
     C = C_;
     left_chunks = lc;
-    ks_q = (int)((uint32_t)ks / (uint32_t)C);
+    magic = magic_;
+    ks_q = (int)((uint32_t)ks / (uint32_t)C);  // once per stream: exact for any ks < 2^32
     ks_r = (int)ks - ks_q * C;
   }
-  __device__ inline void load(const int64_t* proc, const int64_t* cl64, const int64_t* lens,
-                              int64_t len_scalar, int b, int left, int C_, int lc) {
-    set(proc[b], cl64[b], lens ? lens[b] : len_scalar, left, C_, lc);
-  }
   // chunk index of query i (its frame is key_start + cl + i)
-  __device__ inline int query_chunk(int i) const {
-    return ks_q + (int)((uint32_t)(ks_r + cl + i) / (uint32_t)C);
-  }
+  __device__ inline int query_chunk(int i) const { return ks_q + div_c((uint32_t)(ks_r + cl + i)); }
   // true where the reference's att_mask is set (encoder.py:199-225)
   __device__ inline bool masked(int i, int qchunk, int j) const {
     if (j < offset || i >= len) return true;
     const int kidx = j - offset;
-    const int kc = ks_q + (int)((uint32_t)(ks_r + kidx) / (uint32_t)C);
+    const int kc = ks_q + div_c((uint32_t)(ks_r + kidx));
     const int diff = qchunk - kc;
     const bool allowed = diff >= 0 && diff <= left_chunks;
     const bool valid_k = kidx < cl || kidx - cl < len;
@@ -303,7 +305,8 @@ __global__ void __launch_bounds__(64) relpos_attn_kernel(const AttnK<ST> p) {
   StreamMask sm{};
   int qchunk[TQ];
   if (mask_mode == 2) {
-    sm.load(p.st_proc, p.st_cl, p.st_len, p.len_scalar, b, p.left, p.chunk_size, p.left_chunks);
+    sm.set(p.st_proc[b], p.st_cl[b], p.st_len ? p.st_len[b] : p.len_scalar, p.left, p.chunk_size,
+           p.left_chunks, p.c_magic);
 #pragma unroll
     for (int ii = 0; ii < TQ; ++ii) qchunk[ii] = sm.query_chunk(i0 + ii);
   }
@@ -525,128 +528,155 @@ __global__ void __launch_bounds__(64) relpos_attn_kernel(const AttnK<ST> p) {
 // fused append + paged relative-position attention on the matrix cores
 // (fp16 / bf16)
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
 
-// v_mfma_f32_16x16x32_{bf16,f16}: lane l holds A[l%16][8*(l/16)+e],
-// B[8*(l/16)+e][l%16] (e < 8) and D[4*(l/16)+i][l%16] (i < 4).
+// 16-bit operand type of the matrix-core path, with the two MFMA shapes used:
+//   16x16x32: lane l holds A[l%16][8*(l/16)+e], B[8*(l/16)+e][l%16], e < 8
+//   16x16x16: lane l holds A[l%16][4*(l/16)+e], B[4*(l/16)+e][l%16], e < 4
+//   both:     lane l holds D[4*(l/16)+i][l%16], i < 4
 template <typename ST>
 struct Mma;
 
 template <>
 struct Mma<bf16_t> {
-  __device__ static inline f32x4_t run(const u32x4 a, const u32x4 b, const f32x4_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  typedef __bf16 H;
+  typedef __bf16 H8 __attribute__((ext_vector_type(8)));
+  typedef __bf16 H4 __attribute__((ext_vector_type(4)));
+  __device__ static inline f32x4_t k32(const u32x4 a, const u32x4 b, const f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(H8, a),
+                                                   __builtin_bit_cast(H8, b), c, 0, 0, 0);
   }
-  // x rounded to the operand type: bit pattern, and its value back in fp32
-  __device__ static inline uint32_t round(float x, float* back) {
-    const uint32_t bits = f32_to_bf16_bits(x);
-    *back = __uint_as_float(bits << 16);
-    return bits;
+  __device__ static inline f32x4_t k16(const i16x4_t a, const i16x4_t b, const f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
   }
 };
 
 template <>
 struct Mma<_Float16> {
-  __device__ static inline f32x4_t run(const u32x4 a, const u32x4 b, const f32x4_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
-                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  typedef _Float16 H;
+  typedef _Float16 H8 __attribute__((ext_vector_type(8)));
+  typedef _Float16 H4 __attribute__((ext_vector_type(4)));
+  __device__ static inline f32x4_t k32(const u32x4 a, const u32x4 b, const f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(H8, a),
+                                                  __builtin_bit_cast(H8, b), c, 0, 0, 0);
   }
-  __device__ static inline uint32_t round(float x, float* back) {
-    const _Float16 hv = (_Float16)x;
-    *back = (float)hv;
-    return (uint32_t)__builtin_bit_cast(uint16_t, hv);
+  __device__ static inline f32x4_t k16(const i16x4_t a, const i16x4_t b, const f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(H4, a),
+                                                 __builtin_bit_cast(H4, b), c, 0, 0, 0);
   }
 };
 
-// Max over the 16 lanes of each DPP row.
-__device__ static inline float row16_max(float v) {
-  v = fmaxf(v, dpp_f<0xB1>(v));
-  v = fmaxf(v, dpp_f<0x4E>(v));
-  v = fmaxf(v, dpp_f<0x141>(v));
-  v = fmaxf(v, dpp_f<0x140>(v));
-  return v;
+// x = hi + lo with hi, lo in the 16-bit operand type (x to ~2^-17 for bf16,
+// ~2^-22 for fp16): the high or the low part of each element.
+template <typename ST, int N, typename V>
+__device__ static inline V split16(const float* x, bool low) {
+  typedef typename Mma<ST>::H H;
+  typedef H HN __attribute__((ext_vector_type(N)));
+  HN out;
+#pragma unroll
+  for (int e = 0; e < N; ++e) {
+    const H hi = (H)x[e];
+    out[e] = low ? (H)(x[e] - (float)hi) : hi;
+  }
+  return __builtin_bit_cast(V, out);
 }
 
 __device__ static inline float lane0(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
 }
 
-// Workgroup of NW = 4 * SPLIT waves: four streams of one head h and one query
-// pair, each stream's head split over SPLIT = head_dim / 64 waves of 64
-// columns.  Per key tile of KT = 16*NT window rows:
-//   * the tile's position rows of head h (shared by every stream) are staged
-//     once per workgroup in LDS, rows padded by 16 bytes so the 16 lanes of an
+// Max / sum over all 64 lanes, result in every lane.
+__device__ static inline float wave_max(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  v = fmaxf(v, dpp_f<0x141>(v));
+  v = fmaxf(v, dpp_f<0x140>(v));
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return lane0(v);
+}
+__device__ static inline float wave_sum(float v) { return lane0(group_sum<64>(v)); }
+
+// Workgroup of 4 waves: 4 / SPLIT streams of one head h and one query pair,
+// each stream's head split over SPLIT = head_dim / 64 waves of 64 columns.
+// Per key tile of KT = 16*NT window rows:
+//   * the tile's position rows of head h (shared by the workgroup's streams)
+//     are staged once in LDS, rows padded by 16 bytes so the 16 lanes of an
 //     MFMA operand read hit distinct banks;
-//   * the MFMA A operand holds, in rows 0..7, (q+u) and (q+v) of both queries,
-//     each split into a high and a low 16-bit part (x = hi + lo to ~2^-17), so
-//     the 16-bit operands lose nothing against the fp32 query + bias sums;
-//   * B operands are the stream's K rows (straight from its pages, 16 keys per
-//     MFMA) and the staged position rows; D rows 0..3 give (q+u).k, rows 4..7
-//     (q+v).pos, each as hi + lo, over the wave's 64 columns;
-//   * the partial dot products of the SPLIT waves of a stream meet in LDS; each
-//     wave then runs the same softmax and sums the values of its own columns on
-//     the VALU (lane = 8 columns of every RLW-th key).
+//   * (q+u).k and (q+v).pos on 16x16x32 MFMAs: A rows 0..7 hold (q+u) and
+//     (q+v) of both queries split into high and low 16-bit parts, so the
+//     16-bit operands lose nothing against the fp32 query + bias sums; B is a
+//     tile of 16 K rows straight from the pages (lane = key, 16 columns) or of
+//     16 staged position rows; the SPLIT waves' partial sums meet in LDS;
+//   * scores and the online softmax spread over the 64 lanes (key = lane,
+//     lane + 64, ...);
+//   * P.V on 16x16x16 MFMAs: A = the probabilities (high and low 16-bit
+//     parts), B = 16 V rows x
+//     16 columns transposed on the way out of LDS by ds_read_b64_tr_b16 (the
+//     wave writes its V tile row-major, 16 rows at a time, and each 16-lane
+//     group reads 4 rows x 16 columns back transposed).
 // Every load that does not depend on the page table (header, stream state,
 // queries, biases, position rows, mask bytes) is issued in one round trip; the
-// K and V rows of the whole tile follow back to back.
-template <typename ST, int DK, int NT, int MODE>
-__global__ void __launch_bounds__(256 * (DK / 64)) relpos_attn_mfma_kernel(const AttnK<ST> p) {
+// K and V rows of the whole tile follow back to back.  Per-stream values live
+// in scalar registers; the ring position of the window's first page is found
+// once per wave, so a row's page needs no division.
+template <typename ST, int DK, int NT, int MODE, bool MULTI>
+__global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p) {
   constexpr int SPLIT = DK / 64;
-  constexpr int NW = 4 * SPLIT;
+  constexpr int NW = 4;
+  constexpr int SPW = NW / SPLIT;  // streams per workgroup
   constexpr int NTH = 64 * NW;
   constexpr int TQ = 2;
-  constexpr int KS = 2;            // k-steps of 32 columns per wave
-  constexpr int KT = 16 * NT;      // keys per tile
+  constexpr int KS = 2;          // 16x16x32 k-steps over the wave's 64 columns
+  constexpr int KT = 16 * NT;    // keys per tile
   constexpr int NPT = (KT + TQ - 1 + 15) / 16;  // position-row tiles
   constexpr int PROWS = 16 * NPT;
   constexpr int PSTRIDE = DK * 2 + 16;          // bytes per staged position row
   constexpr int CHR = DK / 8;                   // 16-byte chunks per staged row
   constexpr int PCH = (PROWS * CHR + NTH - 1) / NTH;  // staged chunks per thread
-  constexpr int VEC = 8;
-  constexpr int G = 64 / VEC;   // lanes per key row in the value sum
-  constexpr int RLW = 64 / G;   // key rows per value load
-  constexpr int NV = KT / RLW;  // value rows per lane per tile
+  constexpr int VSTRIDE = 64 * 2 + 16;          // bytes per staged V row
+  constexpr int SK = (KT + 63) / 64;            // scores per lane per query
   constexpr float NEG = -1e30f;
-  constexpr float MASKED = -1e5f * 1.4426950408889634f;
+  constexpr float MASKED = -1e5f * 1.4426950408889634f;  // -1e5 in log2 units
+  constexpr int mask_mode = MODE;  // 0 none, 1 mask bytes, 2 stream state
+  typedef typename Mma<ST>::H H;
 
   __shared__ __attribute__((aligned(16))) uint8_t pos_lds[PROWS * PSTRIDE];
+  __shared__ __attribute__((aligned(16))) uint8_t v_lds[NW][16 * VSTRIDE];
   __shared__ float bd_lds[NW][TQ][PROWS];
   __shared__ float ac_lds[NW][TQ][KT];
-  __shared__ __attribute__((aligned(8))) float p_lds[NW][KT][TQ];
+  __shared__ __attribute__((aligned(16))) float p_lds[NW][TQ][KT];
+  __shared__ uint8_t ok_lds[NW][KT];
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int q16 = lane & 15;
   const int kg = lane >> 4;
-  const int sw = wave / SPLIT;   // stream slot in the workgroup
-  const int hf = wave % SPLIT;   // 64-column part of the head
-  const int w0 = sw * SPLIT;     // first wave of this stream
+  const int sw = wave / SPLIT;  // stream slot in the workgroup
+  const int hf = wave % SPLIT;  // 64-column part of the head
+  const int w0 = sw * SPLIT;    // first wave of this stream
   const int h = blockIdx.y;
   const int i0 = blockIdx.z * TQ;
   const int nq = min(TQ, p.T - i0);
-  const int b_raw = blockIdx.x * 4 + sw;
+  const int b_raw = blockIdx.x * SPW + sw;
   const bool active = b_raw < p.B;  // uniform per wave
   const int b = active ? b_raw : p.B - 1;
   const int hcol = h * DK + hf * 64;  // first column of the wave
   const int M = p.pg.max_pages;
-  constexpr int mask_mode = MODE;  // 0 none, 1 mask bytes, 2 stream state
+  const bool paged = p.pg.rows != nullptr;
 
-  // ---------------- prologue: every load independent of the page table
-  int A = 0, ring_lane = -1;
-  if (p.pg.rows) {
-    const int32_t* row = p.pg.rows + (int64_t)b * p.pg.rows_stride;
-    A = row[0];
-    ring_lane = row[1 + min(lane, M - 1)];
-  }
-  int64_t st_pr = 0, st_cl = 0, st_n = p.len_scalar;
-  if (mask_mode == 2) {
-    st_pr = p.st_proc[b];
-    st_cl = p.st_cl[b];
-    if (p.st_len) st_n = p.st_len[b];
-  }
+  // ---------------- prologue: every load independent of the page table,
+  //                  issued branch-free (absent inputs read a valid stand-in
+  //                  address and are replaced afterwards)
+  const int32_t* hdr = paged ? p.pg.rows + (int64_t)b * p.pg.rows_stride
+                             : reinterpret_cast<const int32_t*>(p.q);
+  const int hdr_a = hdr[0];
+  int ring_lane = hdr[paged ? 1 + min(lane, M - 1) : 0];
+  const int64_t* stp = mask_mode == 2 ? p.st_proc + b : reinterpret_cast<const int64_t*>(p.q);
+  const int64_t* stc = mask_mode == 2 ? p.st_cl + b : stp;
+  const int64_t* stn = (mask_mode == 2 && p.st_len) ? p.st_len + b : stp;
+  const int64_t st_pr_v = *stp, st_cl_v = *stc, st_n_v = *stn;
   // A operand source: row m = q16 is (q+u)_hi, (q+u)_lo, (q+v)_hi, (q+v)_lo of
   // query m & 1 for m < 8, zero above; element e of k-step ks is column
   // kg*16 + ks*8 + e of the wave's 64
@@ -663,76 +693,88 @@ __global__ void __launch_bounds__(256 * (DK / 64)) relpos_attn_mfma_kernel(const
       braw[ks] = ld16(brow + ks * 8);
     }
   }
+  // position rows and mask bytes of a tile
   u32x4 pst[PCH];
-  uint8_t mk[NT][TQ];
+  uint8_t mk[SK][TQ];
   auto load_tile_shared = [&](int jb) {
     const int rb = jb + p.T - i0 - TQ;
 #pragma unroll
     for (int c = 0; c < PCH; ++c) {
       const int idx = min((int)threadIdx.x + c * NTH, PROWS * CHR - 1);
-      const int r = idx / CHR;
-      const int ch = idx - r * CHR;
-      const int rc = min(max(rb + r, 0), p.pos_rows - 1);
-      pst[c] = ld16(p.pos + rc * p.pos_sr + h * DK + ch * 8);
+      const int rc = min(max(rb + idx / CHR, 0), p.pos_rows - 1);
+      pst[c] = ld16(p.pos + rc * p.pos_sr + h * DK + (idx % CHR) * 8);
     }
     if (mask_mode == 1) {
 #pragma unroll
-      for (int kt = 0; kt < NT; ++kt)
+      for (int r = 0; r < SK; ++r)
 #pragma unroll
         for (int ii = 0; ii < TQ; ++ii) {
           const int ic = min(i0 + ii, p.T - 1);
-          const int jc = min(jb + 16 * kt + q16, p.Lk - 1);
-          mk[kt][ii] = p.mask[b * p.m_sb + h * p.m_sh + (int64_t)ic * p.m_st + jc];
+          const int jc = min(jb + lane + 64 * r, p.Lk - 1);
+          mk[r][ii] = p.mask[b * p.m_sb + h * p.m_sh + (int64_t)ic * p.m_st + jc];
         }
     }
   };
   load_tile_shared(0);
+  __builtin_amdgcn_sched_barrier(0);  // all of the above in flight before any use
 
-  // ---------------- A operand (hi / lo split of the fp32 sums)
-  u32x4 aop[KS];
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    float qf[8], bf[8];
-    Tr<ST>::unpack(qraw[ks], qf);
-    Tr<ST>::unpack(braw[ks], bf);
-    uint32_t bits[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float x = (a_ii < nq ? qf[e] : 0.f) + bf[e];
-      float hi, dummy;
-      const uint32_t hb = Mma<ST>::round(x, &hi);
-      const uint32_t lb = Mma<ST>::round(x - hi, &dummy);
-      bits[e] = a_kind >= 4 ? 0u : ((a_kind & 1) ? lb : hb);
-    }
-    aop[ks] = u32x4{bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16),
-                    bits[4] | (bits[5] << 16), bits[6] | (bits[7] << 16)};
-  }
+  // ---------------- per-stream scalars
+  const int A = paged ? __builtin_amdgcn_readfirstlane(hdr_a) : 0;
+  if (!paged) ring_lane = -1;
+  // ring entry of the first page that holds a window position
+  const int win0 = A - p.left;
+  const uint32_t lp0 = (uint32_t)max(win0, 0) >> p.pg.page_shift;
+  const int r0 = paged ? (int)(lp0 % (uint32_t)M) : 0;
   StreamMask sm{};
   int qchunk[TQ];
   if (mask_mode == 2) {
-    sm.set(st_pr, st_cl, st_n, p.left, p.chunk_size, p.left_chunks);
+    auto u64 = [](int64_t v) {
+      const int lo = __builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+      const int hi = __builtin_amdgcn_readfirstlane((int)(v >> 32));
+      return (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+    };
+    const int64_t n = p.st_len ? u64(st_n_v) : p.len_scalar;
+    sm.set(u64(st_pr_v), u64(st_cl_v), n, p.left, p.chunk_size, p.left_chunks, p.c_magic);
 #pragma unroll
     for (int ii = 0; ii < TQ; ++ii) qchunk[ii] = sm.query_chunk(i0 + ii);
   }
 
-  // value-sum accumulators: lane = columns g*8 .. g*8+7 of keys rl (mod RLW)
-  const int g = lane % G;
-  const int rl = lane / G;
-  float acc[TQ][VEC];
+  // ---------------- A operand (high / low parts of the fp32 sums)
+  u32x4 aop[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    float qf[8], bf[8], x[8];
+    Tr<ST>::unpack(qraw[ks], qf);
+    Tr<ST>::unpack(braw[ks], bf);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = (a_ii < nq ? qf[e] : 0.f) + bf[e];
+    aop[ks] = split16<ST, 8, u32x4>(x, a_kind & 1);
+    if (a_kind >= 4) aop[ks] = u32x4{0u, 0u, 0u, 0u};
+  }
+
+  f32x4_t oacc[4];  // P.V: D rows (hi q0, hi q1, lo q0, lo q1), 4 column tiles of 16
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) oacc[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   float m_run[TQ], l_run[TQ];
 #pragma unroll
   for (int ii = 0; ii < TQ; ++ii) {
     m_run[ii] = NEG;
     l_run[ii] = 0.f;
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) acc[ii][e] = 0.f;
   }
-  const ST* kn_b = p.kn + b * p.k_sb;
-  const ST* vn_b = p.vn + b * p.v_sb;
-  const bool paged = p.pg.rows != nullptr;
+  const ST* kn_b = p.kn + b * p.k_sb + hcol + kg * 16;
+  const ST* vn_b = p.vn + b * p.v_sb + hcol + kg * 16;
+  const ST* kp_c = p.kp + hcol + kg * 16;
+  const ST* vp_c = p.vp + hcol + kg * 16;
+  const uint32_t pmask = (1u << p.pg.page_shift) - 1u;
+  uint8_t* vl = v_lds[wave];
+  const bool do_append = p.append && blockIdx.z == 0 && active;
 
-  for (int tile = 0; tile < p.tiles; ++tile) {
+  // MULTI: windows longer than one tile (the single-tile form is straight-line
+  // code, with nothing carried around a loop)
+  const int ntiles = MULTI ? p.tiles : 1;
+  for (int tile = 0; tile < ntiles; ++tile) {
     const int jb = tile * KT;
+    if (MULTI && tile > 0) load_tile_shared(jb);
 
     // ---- stage the position rows of the tile
     {
@@ -742,69 +784,56 @@ __global__ void __launch_bounds__(256 * (DK / 64)) relpos_attn_mfma_kernel(const
         const int idx = threadIdx.x + c * NTH;
         if (idx < PROWS * CHR) {
           const int r = idx / CHR;
-          const int ch = idx - r * CHR;
           const bool in = rb + r >= 0 && rb + r < p.pos_rows;
-          *reinterpret_cast<u32x4*>(pos_lds + r * PSTRIDE + ch * 16) =
+          *reinterpret_cast<u32x4*>(pos_lds + r * PSTRIDE + (idx % CHR) * 16) =
               in ? pst[c] : u32x4{0u, 0u, 0u, 0u};
         }
       }
     }
-    uint8_t mkt[NT][TQ];
-#pragma unroll
-    for (int kt = 0; kt < NT; ++kt)
-#pragma unroll
-      for (int ii = 0; ii < TQ; ++ii) mkt[kt][ii] = mask_mode == 1 ? mk[kt][ii] : (uint8_t)0;
 
-    // ---- K rows (MFMA B layout: lane = key q16, columns kg*16 ..) and V rows
-    //      (lane = columns g*8 .., key rl mod RLW): every page lookup first,
-    //      then all loads back to back
-    int kpos[NT], vpos[NV], kpage[NT], vpage[NV];
+    // ---- K and V rows of the tile, lane = key jb + 16*kt + q16, columns
+    //      kg*16 .. kg*16 + 15 of the wave's 64: page ids first, then loads
+    int page[NT];
 #pragma unroll
     for (int kt = 0; kt < NT; ++kt) {
-      kpos[kt] = A - p.left + min(jb + 16 * kt + q16, p.Lk - 1);
-      kpage[kt] = paged ? __shfl(ring_lane, (int)((((uint32_t)max(kpos[kt], 0)) >> p.pg.page_shift) %
-                                                  (uint32_t)M))
-                        : -1;
+      const int pos = win0 + min(jb + 16 * kt + q16, p.Lk - 1);
+      int ridx = r0 + (int)(((uint32_t)max(pos, 0) >> p.pg.page_shift) - lp0);
+      ridx = ridx >= M ? ridx - M : ridx;
+      page[kt] = __shfl(ring_lane, ridx);
     }
-#pragma unroll
-    for (int n = 0; n < NV; ++n) {
-      vpos[n] = A - p.left + min(jb + n * RLW + rl, p.Lk - 1);
-      vpage[n] = paged ? __shfl(ring_lane, (int)((((uint32_t)max(vpos[n], 0)) >> p.pg.page_shift) %
-                                                 (uint32_t)M))
-                       : -1;
-    }
-    u32x4 kr[NT][KS], vr[NV];
-    bool okk[NT], okv[NV];
-    const uint32_t pmask = (1u << p.pg.page_shift) - 1u;
+    u32x4 kr[NT][KS], vr[NT][KS];
+    bool okk[NT];
 #pragma unroll
     for (int kt = 0; kt < NT; ++kt) {
       const int j = jb + 16 * kt + q16;
       const int jc = min(j, p.Lk - 1);
+      const int pos = win0 + jc;
       const bool fresh = jc >= p.left;
-      const bool pok = kpos[kt] >= 0 && kpage[kt] >= 0 && kpage[kt] < p.pg.num_pages;
+      const bool pok = pos >= 0 && page[kt] >= 0 && page[kt] < p.pg.num_pages;
       okk[kt] = j < p.Lk && (fresh || pok);
-      const ST* ka = (fresh || !pok)
-                         ? kn_b + (int64_t)(fresh ? jc - p.left : 0) * p.k_st
-                         : p.kp + (int64_t)kpage[kt] * p.pg.page_elems +
-                               (int64_t)((uint32_t)kpos[kt] & pmask) * p.pg.D;
-      ka += hcol + kg * 16;
+      const ST* ka;
+      const ST* va;
+      if (jb + 16 * kt + 15 < p.left) {  // uniform: the whole tile is cached history
+        const int64_t off = (int64_t)(pok ? page[kt] : 0) * p.pg.page_elems +
+                            (int64_t)((uint32_t)max(pos, 0) & pmask) * p.pg.D;
+        // a key outside the stream's history: its K column is discarded with
+        // the score, but its V row enters the sum with weight zero, so it must
+        // be finite -- read this step's first frame instead
+        ka = kp_c + off;
+        va = pok ? vp_c + off : vn_b;
+      } else {
+        const int64_t off = (int64_t)(pok ? page[kt] : 0) * p.pg.page_elems +
+                            (int64_t)((uint32_t)max(pos, 0) & pmask) * p.pg.D;
+        const int t = fresh ? jc - p.left : 0;
+        const bool from_new = fresh || !pok;
+        ka = from_new ? kn_b + (int64_t)t * p.k_st : kp_c + off;
+        va = from_new ? vn_b + (int64_t)t * p.v_st : vp_c + off;
+      }
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) kr[kt][ks] = ld16(ka + ks * 8);
-    }
 #pragma unroll
-    for (int n = 0; n < NV; ++n) {
-      const int j = jb + n * RLW + rl;
-      const int jc = min(j, p.Lk - 1);
-      const bool fresh = jc >= p.left;
-      const bool pok = vpos[n] >= 0 && vpage[n] >= 0 && vpage[n] < p.pg.num_pages;
-      okv[n] = j < p.Lk && (fresh || pok);
-      const ST* va = (fresh || !pok)
-                         ? vn_b + (int64_t)(fresh ? jc - p.left : 0) * p.v_st
-                         : p.vp + (int64_t)vpage[n] * p.pg.page_elems +
-                               (int64_t)((uint32_t)vpos[n] & pmask) * p.pg.D;
-      vr[n] = ld16(va + hcol + g * VEC);
+      for (int ks = 0; ks < KS; ++ks) vr[kt][ks] = ld16(va + ks * 8);
     }
-    if (tile + 1 < p.tiles) load_tile_shared(jb + KT);  // prefetch behind K/V
     __syncthreads();  // position rows staged
 
     // ---- (q+v).pos over the wave's columns: D rows 4..7 (lanes 16..31)
@@ -814,125 +843,131 @@ __global__ void __launch_bounds__(256 * (DK / 64)) relpos_attn_mfma_kernel(const
       const uint8_t* src = pos_lds + (pt * 16 + q16) * PSTRIDE + (hf * 64 + kg * 16) * 2;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
-        d = Mma<ST>::run(aop[ks], *reinterpret_cast<const u32x4*>(src + ks * 16), d);
+        d = Mma<ST>::k32(aop[ks], *reinterpret_cast<const u32x4*>(src + ks * 16), d);
       if (kg == 1) {
         bd_lds[wave][0][pt * 16 + q16] = d[0] + d[2];
         bd_lds[wave][1][pt * 16 + q16] = d[1] + d[3];
       }
     }
-    // ---- (q+u).k over the wave's columns: D rows 0..3 (lanes 0..15)
+    // ---- (q+u).k over the wave's columns: D rows 0..3 (lanes 0..15), and the
+    //      fused append of this step's K rows (query group 0)
 #pragma unroll
     for (int kt = 0; kt < NT; ++kt) {
       f32x4_t d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) d = Mma<ST>::run(aop[ks], kr[kt][ks], d);
+      for (int ks = 0; ks < KS; ++ks) d = Mma<ST>::k32(aop[ks], kr[kt][ks], d);
       if (kg == 0) {
         ac_lds[wave][0][16 * kt + q16] = d[0] + d[2];
         ac_lds[wave][1][16 * kt + q16] = d[1] + d[3];
+        ok_lds[wave][16 * kt + q16] = okk[kt] ? 1 : 0;
+      }
+      if (do_append && jb + 16 * kt + 15 >= p.left && jb + 16 * kt < p.Lk) {  // uniform
+        const int j = jb + 16 * kt + q16;
+        const int pos = win0 + min(j, p.Lk - 1);
+        if (j >= p.left && j < p.Lk && page[kt] >= 0 && page[kt] < p.pg.num_pages) {
+          const int64_t off = (int64_t)page[kt] * p.pg.page_elems +
+                              (int64_t)((uint32_t)pos & pmask) * p.pg.D;
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks) {
+            st16(const_cast<ST*>(kp_c) + off + ks * 8, kr[kt][ks]);
+            st16(const_cast<ST*>(vp_c) + off + ks * 8, vr[kt][ks]);
+          }
+        }
       }
     }
     __syncthreads();  // partial dot products of the stream's waves in LDS
 
-    // ---- scores (lanes 0..15 hold key 16*kt + q16), softmax over the tile
-    float s[NT][TQ];
+    // ---- scores: lane handles keys lane + 64*r of the tile; online softmax
+    float s[SK][TQ];
+    bool okr[SK];
 #pragma unroll
-    for (int kt = 0; kt < NT; ++kt) {
-      const int j = jb + 16 * kt + q16;
-      const int jc = min(j, p.Lk - 1);
+    for (int r = 0; r < SK; ++r) {
+      const int kk = lane + 64 * r;  // key within the tile
+      const int kkc = min(kk, KT - 1);
+      const int j = jb + kk;
+      okr[r] = ok_lds[wave][kkc] != 0;
 #pragma unroll
       for (int ii = 0; ii < TQ; ++ii) {
         float ac = 0.f, bd = 0.f;
 #pragma unroll
         for (int x = 0; x < SPLIT; ++x) {
-          ac += ac_lds[w0 + x][ii][16 * kt + q16];
-          bd += bd_lds[w0 + x][ii][16 * kt + q16 + TQ - 1 - ii];
+          ac += ac_lds[w0 + x][ii][kkc];
+          bd += bd_lds[w0 + x][ii][kkc + TQ - 1 - ii];
         }
-        if (!okk[kt]) ac = 0.f;  // a key outside the stream's history reads as zeros
+        if (!okr[r]) ac = 0.f;  // a key outside the stream's history reads as zeros
         bool msk = false;
-        if (mask_mode == 1) msk = mkt[kt][ii] != 0;
-        if (mask_mode == 2) msk = sm.masked(i0 + ii, qchunk[ii], jc);
+        if (mask_mode == 1) msk = mk[r][ii] != 0;
+        if (mask_mode == 2) msk = sm.masked(i0 + ii, qchunk[ii], min(j, p.Lk - 1));
         const float sc = msk ? fmaf(ac, p.scale, MASKED) : (ac + bd) * p.scale;
-        s[kt][ii] = (kg == 0 && j < p.Lk && ii < nq) ? sc : NEG;
+        s[r][ii] = (kk < KT && j < p.Lk && ii < nq) ? sc : NEG;
       }
     }
+    float corr[TQ];
 #pragma unroll
     for (int ii = 0; ii < TQ; ++ii) {
       float tmax = NEG;
 #pragma unroll
-      for (int kt = 0; kt < NT; ++kt) tmax = fmaxf(tmax, s[kt][ii]);
-      const float mnew = fmaxf(m_run[ii], lane0(row16_max(tmax)));
-      const float corr = __builtin_amdgcn_exp2f(m_run[ii] - mnew);
+      for (int r = 0; r < SK; ++r) tmax = fmaxf(tmax, s[r][ii]);
+      const float mnew = fmaxf(m_run[ii], wave_max(tmax));
+      corr[ii] = __builtin_amdgcn_exp2f(m_run[ii] - mnew);
       m_run[ii] = mnew;
       float lsum = 0.f;
 #pragma unroll
-      for (int kt = 0; kt < NT; ++kt) {
-        const float e = s[kt][ii] > 0.5f * NEG ? __builtin_amdgcn_exp2f(s[kt][ii] - mnew) : 0.f;
+      for (int r = 0; r < SK; ++r) {
+        const int kk = lane + 64 * r;
+        const float e = s[r][ii] > 0.5f * NEG ? __builtin_amdgcn_exp2f(s[r][ii] - mnew) : 0.f;
         lsum += e;
-        if (kg == 0) p_lds[wave][16 * kt + q16][ii] = e;
+        // the value sum sees zeros for keys outside the stream's history
+        if (kk < KT) p_lds[wave][ii][kk] = okr[r] ? e : 0.f;
       }
-      l_run[ii] = l_run[ii] * corr + lane0(group_sum<16>(lsum));
+      l_run[ii] = l_run[ii] * corr[ii] + wave_sum(lsum);
+    }
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) acc[ii][e] *= corr;
+    for (int nt = 0; nt < 4; ++nt) {
+      oacc[nt][0] *= corr[0];
+      oacc[nt][1] *= corr[1];
+      oacc[nt][2] *= corr[0];
+      oacc[nt][3] *= corr[1];
     }
     wave_lds_sync();
 
-    // ---- value sum over the wave's columns
+    // ---- P.V, 16 keys at a time: stage the V rows, read them back transposed;
+    //      A rows 0..1 are the probabilities of the two queries, rows 2..3
+    //      their low parts (p = hi + lo), so D[q] + D[2 + q] is exact to ~2^-17
+    const bool p_row = q16 < 2 * TQ;
+    const bool p_low = q16 >= TQ;
 #pragma unroll
-    for (int n = 0; n < NV; ++n) {
-      const float2 pp = *reinterpret_cast<const float2*>(&p_lds[wave][n * RLW + rl][0]);
-      float vf[VEC];
-      Tr<ST>::unpack(vr[n], vf);
+    for (int kt = 0; kt < NT; ++kt) {
+      uint8_t* vrow = vl + q16 * VSTRIDE + kg * 32;
+      *reinterpret_cast<u32x4*>(vrow) = vr[kt][0];
+      *reinterpret_cast<u32x4*>(vrow + 16) = vr[kt][1];
+      const float4 pp = *reinterpret_cast<const float4*>(&p_lds[wave][q16 & 1][16 * kt + 4 * kg]);
+      const float pv[4] = {pp.x, pp.y, pp.z, pp.w};
+      i16x4_t pop = split16<ST, 4, i16x4_t>(pv, p_low);
+      if (!p_row) pop = i16x4_t{0, 0, 0, 0};
+      wave_lds_sync();
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        const float x = okv[n] ? vf[e] : 0.f;
-        acc[0][e] = fmaf(pp.x, x, acc[0][e]);
-        acc[1][e] = fmaf(pp.y, x, acc[1][e]);
+      for (int nt = 0; nt < 4; ++nt) {
+        const uint8_t* src = vl + (4 * kg + (q16 >> 2)) * VSTRIDE + (nt * 16 + 4 * (q16 & 3)) * 2;
+        const i16x4_t vt = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) i16x4_t*)src);
+        oacc[nt] = Mma<ST>::k16(pop, vt, oacc[nt]);
       }
+      wave_lds_sync();  // the next 16 rows overwrite the staging rows
     }
-
-    // ---- append this step's frames to the pages (query group 0 only); the
-    //      page ids were looked up above, outside any divergent branch
-    if (p.append && blockIdx.z == 0 && active) {
-#pragma unroll
-      for (int kt = 0; kt < NT; ++kt) {
-        const int j = jb + 16 * kt + q16;
-        const bool pok = kpage[kt] >= 0 && kpage[kt] < p.pg.num_pages;
-        if (j < p.Lk && j >= p.left && pok) {
-          ST* dst = p.kp + (int64_t)kpage[kt] * p.pg.page_elems +
-                    (int64_t)((uint32_t)kpos[kt] & pmask) * p.pg.D + hcol + kg * 16;
-#pragma unroll
-          for (int ks = 0; ks < KS; ++ks) st16(dst + ks * 8, kr[kt][ks]);
-        }
-      }
-#pragma unroll
-      for (int n = 0; n < NV; ++n) {
-        const int j = jb + n * RLW + rl;
-        const bool pok = vpage[n] >= 0 && vpage[n] < p.pg.num_pages;
-        if (j < p.Lk && j >= p.left && pok)
-          st16(p.vp + (int64_t)vpage[n] * p.pg.page_elems +
-                   (int64_t)((uint32_t)vpos[n] & pmask) * p.pg.D + hcol + g * VEC,
-               vr[n]);
-      }
-    }
-    __syncthreads();  // the next tile restages pos_lds and rewrites bd / ac / p
+    if (MULTI) __syncthreads();  // the next tile restages pos_lds and rewrites bd / ac
   }
 
-  // ---- combine the RLW key groups (same running max everywhere) and write
-#pragma unroll
-  for (int ii = 0; ii < TQ; ++ii)
-#pragma unroll
-    for (int off = G; off < 64; off <<= 1)
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) acc[ii][e] += __shfl_xor(acc[ii][e], off);
-  if (active && rl == 0) {
+  // ---- write: lanes 0..15 hold column nt*16 + q16 of both queries
+  if (active && kg == 0) {
 #pragma unroll
     for (int ii = 0; ii < TQ; ++ii) {
       if (ii >= nq) continue;
       const float inv = l_run[ii] > 0.f ? 1.f / l_run[ii] : 0.f;
-      float o[VEC];
+      ST* orow = p.out + b * p.o_sb + (int64_t)(i0 + ii) * p.o_st + hcol + q16;
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) o[e] = acc[ii][e] * inv;
-      st16(p.out + b * p.o_sb + (int64_t)(i0 + ii) * p.o_st + hcol + g * VEC, Tr<ST>::pack(o));
+      for (int nt = 0; nt < 4; ++nt)
+        *reinterpret_cast<H*>(orow + nt * 16) = (H)((oacc[nt][ii] + oacc[nt][2 + ii]) * inv);
     }
   }
 }
@@ -1189,17 +1224,26 @@ void pick_tiling(int Lk, int rlw, int hint, int* NR, int* tiles) {
 // pair of queries, key tiles of 16 * kMfmaTiles rows.
 constexpr int kMfmaTiles = 5;
 
-template <typename ST, int DK, int MODE>
-int launch_attn_mfma_mode(const pk_attn_args* a, const AttnK<ST>& k, hipStream_t s) {
-  dim3 grid((unsigned)((a->batch + 3) / 4), (unsigned)a->num_heads, (unsigned)((a->chunk + 1) / 2));
-  dim3 block(256u * (DK / 64));
+template <typename ST, int DK, int MODE, bool MULTI>
+int launch_attn_mfma_t(const pk_attn_args* a, const AttnK<ST>& k, hipStream_t s) {
+  constexpr int SPW = 4 / (DK / 64);  // streams per workgroup
+  dim3 grid((unsigned)((a->batch + SPW - 1) / SPW), (unsigned)a->num_heads,
+            (unsigned)((a->chunk + 1) / 2));
+  dim3 block(256u);
   if (a->start_event || a->stop_event) {
-    hipExtLaunchKernelGGL(relpos_attn_mfma_kernel<ST, DK, kMfmaTiles, MODE>, grid, block, 0u, s,
-                          (hipEvent_t)a->start_event, (hipEvent_t)a->stop_event, 0u, k);
+    hipExtLaunchKernelGGL(relpos_attn_mfma_kernel<ST, DK, kMfmaTiles, MODE, MULTI>, grid, block,
+                          0u, s, (hipEvent_t)a->start_event, (hipEvent_t)a->stop_event, 0u, k);
   } else {
-    hipLaunchKernelGGL((relpos_attn_mfma_kernel<ST, DK, kMfmaTiles, MODE>), grid, block, 0, s, k);
+    hipLaunchKernelGGL((relpos_attn_mfma_kernel<ST, DK, kMfmaTiles, MODE, MULTI>), grid, block, 0,
+                       s, k);
   }
   return check_launch("pk_paged_relpos_attn");
+}
+
+template <typename ST, int DK, int MODE>
+int launch_attn_mfma_mode(const pk_attn_args* a, const AttnK<ST>& k, hipStream_t s) {
+  if (k.tiles > 1) return launch_attn_mfma_t<ST, DK, MODE, true>(a, k, s);
+  return launch_attn_mfma_t<ST, DK, MODE, false>(a, k, s);
 }
 
 template <typename ST, int DK>
@@ -1288,6 +1332,12 @@ int attn_typed(const pk_attn_args* a, hipStream_t s) {
     k.len_scalar = a->length_scalar;
     k.chunk_size = a->chunk_size;
     k.left_chunks = a->left / a->chunk_size;
+    // chunk indices are floor((key_start % C + x) / C) with x < C + window + chunk
+    if ((int64_t)(2 * a->chunk_size + a->left + 2 * a->chunk) * a->chunk_size >= (1LL << 31))
+      return fail(PK_ERR_UNSUPPORTED, "%s: chunk_size %d too large for the in-kernel mask", what,
+                  a->chunk_size);
+    k.c_magic = a->chunk_size == 1 ? 0u
+                                   : (uint32_t)((1ULL << 32) / (uint64_t)a->chunk_size + 1ULL);
   }
   k.out = static_cast<ST*>(a->out);
   k.o_sb = a->out_stride_b;
