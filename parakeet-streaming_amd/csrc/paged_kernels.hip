@@ -598,29 +598,55 @@ __device__ static inline float wave_max(float v) {
 }
 __device__ static inline float wave_sum(float v) { return lane0(group_sum<64>(v)); }
 
+// Index-mode buffer access: a resource describes `nrows` rows of `stride`
+// bytes; a row index >= nrows reads zeros and drops stores (the hardware range
+// check), which is how absent rows -- positions before a stream's first frame,
+// pages a stream does not hold, keys past the window -- come out as the zeros
+// the reference's dense window holds there.
+extern "C" __device__ u32x4 pk_buffer_load_x4(__amdgpu_buffer_rsrc_t rsrc, int vindex, int voffset,
+                                              int soffset, int aux)
+    __asm("llvm.amdgcn.struct.ptr.buffer.load.v4i32");
+extern "C" __device__ void pk_buffer_store_x4(u32x4 data, __amdgpu_buffer_rsrc_t rsrc, int vindex,
+                                              int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.struct.ptr.buffer.store.v4i32");
+
+constexpr uint32_t kNoRow = 0xffffffffu;  // a row index every resource rejects
+constexpr int kMaxBufferStride = 16383;   // bytes, stride field of the resource
+
+__device__ static inline __amdgpu_buffer_rsrc_t rows_rsrc(const void* base, int stride_bytes,
+                                                          uint32_t nrows) {
+  // word 3 0x00020000: 32-bit data format, the setting untyped loads need on CDNA
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)stride_bytes,
+                                           (int)nrows, 0x00020000);
+}
+
 // Workgroup of 4 waves: 4 / SPLIT streams of one head h and one query pair,
 // each stream's head split over SPLIT = head_dim / 64 waves of 64 columns.
-// Per key tile of KT = 16*NT window rows:
-//   * the tile's position rows of head h (shared by the workgroup's streams)
-//     are staged once in LDS, rows padded by 16 bytes so the 16 lanes of an
-//     MFMA operand read hit distinct banks;
+// The window's keys are handled in score slots: per pass, NT tiles of 16 slots
+// hold cached history (window column j = jb + slot, read from the pages) and
+// one more tile holds this step's frames (j = left + slot - 16*NT, read from
+// the projection output); the frames' tile is live in the last pass only, and
+// a chunk is at most 16 frames.  So every load reads exactly one source, and
+// absent rows (positions before the stream's first frame, columns past the
+// history, slots past the chunk) read zeros through the buffer range check.
+// Per pass:
+//   * the position rows the pass needs (shared by the workgroup's streams) are
+//     staged once in LDS, rows padded by 16 bytes so the 16 lanes of an MFMA
+//     operand read hit distinct banks;
 //   * (q+u).k and (q+v).pos on 16x16x32 MFMAs: A rows 0..7 hold (q+u) and
 //     (q+v) of both queries split into high and low 16-bit parts, so the
 //     16-bit operands lose nothing against the fp32 query + bias sums; B is a
-//     tile of 16 K rows straight from the pages (lane = key, 16 columns) or of
-//     16 staged position rows; the SPLIT waves' partial sums meet in LDS;
-//   * scores and the online softmax spread over the 64 lanes (key = lane,
-//     lane + 64, ...);
+//     tile of 16 K rows (lane = key, 16 columns) or 16 staged position rows;
+//     the SPLIT waves' partial sums meet in LDS;
+//   * scores and the online softmax spread over the 64 lanes (slot = lane,
+//     lane + 64);
 //   * P.V on 16x16x16 MFMAs: A = the probabilities (high and low 16-bit
-//     parts), B = 16 V rows x
-//     16 columns transposed on the way out of LDS by ds_read_b64_tr_b16 (the
-//     wave writes its V tile row-major, 16 rows at a time, and each 16-lane
-//     group reads 4 rows x 16 columns back transposed).
-// Every load that does not depend on the page table (header, stream state,
-// queries, biases, position rows, mask bytes) is issued in one round trip; the
-// K and V rows of the whole tile follow back to back.  Per-stream values live
-// in scalar registers; the ring position of the window's first page is found
-// once per wave, so a row's page needs no division.
+//     parts), B = 16 V rows x 16 columns transposed on the way out of LDS by
+//     ds_read_b64_tr_b16 (the wave writes its V tile row-major and each 16-lane
+//     group reads 4 rows x 16 columns back transposed);
+//   * the fused append stores the frames' tile into the pages (query group 0).
+// Every load that does not depend on the page table is issued in one round
+// trip; all K and V rows of the pass follow back to back.
 template <typename ST, int DK, int NT, int MODE, bool MULTI>
 __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p) {
   constexpr int SPLIT = DK / 64;
@@ -628,28 +654,37 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
   constexpr int SPW = NW / SPLIT;  // streams per workgroup
   constexpr int NTH = 64 * NW;
   constexpr int TQ = 2;
-  constexpr int KS = 2;          // 16x16x32 k-steps over the wave's 64 columns
-  constexpr int KT = 16 * NT;    // keys per tile
-  constexpr int NPT = (KT + TQ - 1 + 15) / 16;  // position-row tiles
+  constexpr int KS = 2;            // 16x16x32 k-steps over the wave's 64 columns
+  constexpr int KT = 16 * NT;      // history slots per pass
+  constexpr int NS = KT + 16;      // slots per pass: history + this step's frames
+  constexpr int NPT = (NS + TQ - 1 + 15) / 16;  // position-row tiles
   constexpr int PROWS = 16 * NPT;
   constexpr int PSTRIDE = DK * 2 + 16;          // bytes per staged position row
   constexpr int CHR = DK / 8;                   // 16-byte chunks per staged row
   constexpr int PCH = (PROWS * CHR + NTH - 1) / NTH;  // staged chunks per thread
   constexpr int VSTRIDE = 64 * 2 + 16;          // bytes per staged V row
-  constexpr int SK = (KT + 63) / 64;            // scores per lane per query
+  constexpr int SK = (NS + 63) / 64;            // slots per lane per query
   constexpr float NEG = -1e30f;
   constexpr float MASKED = -1e5f * 1.4426950408889634f;  // -1e5 in log2 units
   constexpr int mask_mode = MODE;  // 0 none, 1 mask bytes, 2 stream state
+  constexpr int ES = 2;            // bytes per element
   typedef typename Mma<ST>::H H;
 
-  __shared__ __attribute__((aligned(16))) uint8_t pos_lds[PROWS * PSTRIDE];
-  __shared__ __attribute__((aligned(16))) uint8_t v_lds[NW][16 * VSTRIDE];
+  // The staged position rows are dead once the dot products are in LDS (the
+  // second barrier of a pass); the P.V staging (V tiles and the 16-bit high
+  // and low parts of the probabilities, [hi|lo][query][slot]) reuses their
+  // space.
+  constexpr int POS_BYTES = PROWS * PSTRIDE;
+  constexpr int PV_BYTES = NW * 16 * VSTRIDE + NW * 2 * TQ * NS * 2;
+  __shared__ __attribute__((aligned(16))) uint8_t stage_lds[POS_BYTES > PV_BYTES ? POS_BYTES : PV_BYTES];
   __shared__ float bd_lds[NW][TQ][PROWS];
-  __shared__ float ac_lds[NW][TQ][KT];
-  __shared__ __attribute__((aligned(16))) float p_lds[NW][TQ][KT];
-  __shared__ uint8_t ok_lds[NW][KT];
+  __shared__ float ac_lds[NW][TQ][NS];
+  uint8_t* const pos_lds = stage_lds;
+  uint8_t (*const v_lds)[16 * VSTRIDE] = reinterpret_cast<uint8_t (*)[16 * VSTRIDE]>(stage_lds);
+  uint16_t (*const p_lds)[2][TQ][NS] =
+      reinterpret_cast<uint16_t (*)[2][TQ][NS]>(stage_lds + NW * 16 * VSTRIDE);
 
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int q16 = lane & 15;
   const int kg = lane >> 4;
@@ -662,9 +697,32 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
   const int b_raw = blockIdx.x * SPW + sw;
   const bool active = b_raw < p.B;  // uniform per wave
   const int b = active ? b_raw : p.B - 1;
-  const int hcol = h * DK + hf * 64;  // first column of the wave
+  const int hcol = h * DK + hf * 64;       // first column of the wave
+  const int cbyte = (hcol + kg * 16) * ES;  // byte offset of the lane's 16 columns in a row
   const int M = p.pg.max_pages;
   const bool paged = p.pg.rows != nullptr;
+
+  // Every resource has a valid base and a non-zero row stride (the range check
+  // that turns absent rows into zeros is index-based); a zero stride can only
+  // come with a single row, where any stride addresses it.  Without pages the
+  // pool resources are never read or written.
+  const int dmodel = p.H * DK;
+  const int st_k = (int)(p.k_st > 0 ? p.k_st : dmodel) * ES;
+  const int st_v = (int)(p.v_st > 0 ? p.v_st : dmodel) * ES;
+  const int st_p = (int)(p.pos_sr > 0 ? p.pos_sr : dmodel) * ES;
+  const __amdgpu_buffer_rsrc_t r_kp =
+      paged ? rows_rsrc(p.kp, p.pg.D * ES, (uint32_t)p.pg.num_pages << p.pg.page_shift)
+            : rows_rsrc(p.kn, st_k, 0u);
+  const __amdgpu_buffer_rsrc_t r_vp =
+      paged ? rows_rsrc(p.vp, p.pg.D * ES, (uint32_t)p.pg.num_pages << p.pg.page_shift)
+            : rows_rsrc(p.vn, st_v, 0u);
+  const __amdgpu_buffer_rsrc_t r_kn = rows_rsrc(p.kn + b * p.k_sb, st_k, (uint32_t)p.T);
+  const __amdgpu_buffer_rsrc_t r_vn = rows_rsrc(p.vn + b * p.v_sb, st_v, (uint32_t)p.T);
+  const __amdgpu_buffer_rsrc_t r_pos = rows_rsrc(p.pos, st_p, (uint32_t)p.pos_rows);
+
+  // window column of score slot s in pass jb; the frames' slots follow the
+  // history slots
+  auto slot_col = [&](int jb, int s) { return s < KT ? jb + s : p.left + (s - KT); };
 
   // ---------------- prologue: every load independent of the page table,
   //                  issued branch-free (absent inputs read a valid stand-in
@@ -693,16 +751,25 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
       braw[ks] = ld16(brow + ks * 8);
     }
   }
-  // position rows and mask bytes of a tile
+  // this step's frames (last pass; they do not depend on the pages)
+  u32x4 kf[KS], vf[KS];
+  {
+    const uint32_t fr = q16 < p.T ? (uint32_t)q16 : kNoRow;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      kf[ks] = pk_buffer_load_x4(r_kn, fr, cbyte + ks * 16, 0, 0);
+      vf[ks] = pk_buffer_load_x4(r_vn, fr, cbyte + ks * 16, 0, 0);
+    }
+  }
+  // position rows (rows outside the table read zeros) and mask bytes of a pass
   u32x4 pst[PCH];
   uint8_t mk[SK][TQ];
-  auto load_tile_shared = [&](int jb) {
+  auto load_pass_shared = [&](int jb) {
     const int rb = jb + p.T - i0 - TQ;
 #pragma unroll
     for (int c = 0; c < PCH; ++c) {
       const int idx = min((int)threadIdx.x + c * NTH, PROWS * CHR - 1);
-      const int rc = min(max(rb + idx / CHR, 0), p.pos_rows - 1);
-      pst[c] = ld16(p.pos + rc * p.pos_sr + h * DK + (idx % CHR) * 8);
+      pst[c] = pk_buffer_load_x4(r_pos, rb + idx / CHR, (h * DK + (idx % CHR) * 8) * ES, 0, 0);
     }
     if (mask_mode == 1) {
 #pragma unroll
@@ -710,12 +777,12 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
 #pragma unroll
         for (int ii = 0; ii < TQ; ++ii) {
           const int ic = min(i0 + ii, p.T - 1);
-          const int jc = min(jb + lane + 64 * r, p.Lk - 1);
+          const int jc = min(max(slot_col(jb, min(lane + 64 * r, NS - 1)), 0), p.Lk - 1);
           mk[r][ii] = p.mask[b * p.m_sb + h * p.m_sh + (int64_t)ic * p.m_st + jc];
         }
     }
   };
-  load_tile_shared(0);
+  load_pass_shared(0);
   __builtin_amdgcn_sched_barrier(0);  // all of the above in flight before any use
 
   // ---------------- per-stream scalars
@@ -725,6 +792,18 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
   const int win0 = A - p.left;
   const uint32_t lp0 = (uint32_t)max(win0, 0) >> p.pg.page_shift;
   const int r0 = paged ? (int)(lp0 % (uint32_t)M) : 0;
+  const uint32_t pmask = (1u << p.pg.page_shift) - 1u;
+  // page row of window column j (a frame position of the stream), kNoRow if
+  // the stream holds none; every lane must be active (ds_bpermute)
+  auto page_row = [&](int j) {
+    const int pos = win0 + j;
+    int ridx = r0 + (int)(((uint32_t)max(pos, 0) >> p.pg.page_shift) - lp0);
+    ridx = ridx >= M ? ridx - M : ridx;
+    const int page = __shfl(ring_lane, ridx);
+    return (paged && pos >= 0 && page >= 0)
+               ? ((uint32_t)page << p.pg.page_shift) | ((uint32_t)pos & pmask)
+               : kNoRow;
+  };
   StreamMask sm{};
   int qchunk[TQ];
   if (mask_mode == 2) {
@@ -761,79 +840,43 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
     m_run[ii] = NEG;
     l_run[ii] = 0.f;
   }
-  const ST* kn_b = p.kn + b * p.k_sb + hcol + kg * 16;
-  const ST* vn_b = p.vn + b * p.v_sb + hcol + kg * 16;
-  const ST* kp_c = p.kp + hcol + kg * 16;
-  const ST* vp_c = p.vp + hcol + kg * 16;
-  const uint32_t pmask = (1u << p.pg.page_shift) - 1u;
   uint8_t* vl = v_lds[wave];
-  const bool do_append = p.append && blockIdx.z == 0 && active;
+  const bool do_append = p.append && blockIdx.z == 0 && active && paged;
 
-  // MULTI: windows longer than one tile (the single-tile form is straight-line
+  // MULTI: history longer than one pass (the single-pass form is straight-line
   // code, with nothing carried around a loop)
-  const int ntiles = MULTI ? p.tiles : 1;
-  for (int tile = 0; tile < ntiles; ++tile) {
-    const int jb = tile * KT;
-    if (MULTI && tile > 0) load_tile_shared(jb);
+  const int npass = MULTI ? p.tiles : 1;
+  for (int pass = 0; pass < npass; ++pass) {
+    const int jb = pass * KT;
+    const bool last = pass == npass - 1;  // the frames' slots are live
+    if (MULTI && pass > 0) load_pass_shared(jb);
 
-    // ---- stage the position rows of the tile
-    {
-      const int rb = jb + p.T - i0 - TQ;
+    // ---- stage the position rows of the pass
 #pragma unroll
-      for (int c = 0; c < PCH; ++c) {
-        const int idx = threadIdx.x + c * NTH;
-        if (idx < PROWS * CHR) {
-          const int r = idx / CHR;
-          const bool in = rb + r >= 0 && rb + r < p.pos_rows;
-          *reinterpret_cast<u32x4*>(pos_lds + r * PSTRIDE + (idx % CHR) * 16) =
-              in ? pst[c] : u32x4{0u, 0u, 0u, 0u};
-        }
-      }
+    for (int c = 0; c < PCH; ++c) {
+      const int idx = threadIdx.x + c * NTH;
+      if (c + 1 < PCH || idx < PROWS * CHR)
+        *reinterpret_cast<u32x4*>(pos_lds + (idx / CHR) * PSTRIDE + (idx % CHR) * 16) = pst[c];
     }
 
-    // ---- K and V rows of the tile, lane = key jb + 16*kt + q16, columns
-    //      kg*16 .. kg*16 + 15 of the wave's 64: page ids first, then loads
-    int page[NT];
-#pragma unroll
-    for (int kt = 0; kt < NT; ++kt) {
-      const int pos = win0 + min(jb + 16 * kt + q16, p.Lk - 1);
-      int ridx = r0 + (int)(((uint32_t)max(pos, 0) >> p.pg.page_shift) - lp0);
-      ridx = ridx >= M ? ridx - M : ridx;
-      page[kt] = __shfl(ring_lane, ridx);
-    }
-    u32x4 kr[NT][KS], vr[NT][KS];
-    bool okk[NT];
+    // ---- history K and V rows, lane = slot 16*kt + q16, columns kg*16 ..
+    //      kg*16 + 15 of the wave's 64: page rows first, then all loads
+    uint32_t prow[NT];
 #pragma unroll
     for (int kt = 0; kt < NT; ++kt) {
       const int j = jb + 16 * kt + q16;
-      const int jc = min(j, p.Lk - 1);
-      const int pos = win0 + jc;
-      const bool fresh = jc >= p.left;
-      const bool pok = pos >= 0 && page[kt] >= 0 && page[kt] < p.pg.num_pages;
-      okk[kt] = j < p.Lk && (fresh || pok);
-      const ST* ka;
-      const ST* va;
-      if (jb + 16 * kt + 15 < p.left) {  // uniform: the whole tile is cached history
-        const int64_t off = (int64_t)(pok ? page[kt] : 0) * p.pg.page_elems +
-                            (int64_t)((uint32_t)max(pos, 0) & pmask) * p.pg.D;
-        // a key outside the stream's history: its K column is discarded with
-        // the score, but its V row enters the sum with weight zero, so it must
-        // be finite -- read this step's first frame instead
-        ka = kp_c + off;
-        va = pok ? vp_c + off : vn_b;
-      } else {
-        const int64_t off = (int64_t)(pok ? page[kt] : 0) * p.pg.page_elems +
-                            (int64_t)((uint32_t)max(pos, 0) & pmask) * p.pg.D;
-        const int t = fresh ? jc - p.left : 0;
-        const bool from_new = fresh || !pok;
-        ka = from_new ? kn_b + (int64_t)t * p.k_st : kp_c + off;
-        va = from_new ? vn_b + (int64_t)t * p.v_st : vp_c + off;
-      }
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) kr[kt][ks] = ld16(ka + ks * 8);
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) vr[kt][ks] = ld16(va + ks * 8);
+      const uint32_t r = page_row(j);
+      prow[kt] = j < p.left ? r : kNoRow;
     }
+    u32x4 kr[NT][KS], vr[NT][KS];
+#pragma unroll
+    for (int kt = 0; kt < NT; ++kt)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kr[kt][ks] = pk_buffer_load_x4(r_kp, prow[kt], cbyte + ks * 16, 0, 0);
+    // the frames' page rows (append target): looked up with every lane
+    // active, then restricted to the lanes holding one of the chunk's frames
+    const uint32_t frow_all = page_row(p.left + q16);
+    const uint32_t frow = (last && q16 < p.T) ? frow_all : kNoRow;
     __syncthreads();  // position rows staged
 
     // ---- (q+v).pos over the wave's columns: D rows 4..7 (lanes 16..31)
@@ -849,57 +892,58 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
         bd_lds[wave][1][pt * 16 + q16] = d[1] + d[3];
       }
     }
-    // ---- (q+u).k over the wave's columns: D rows 0..3 (lanes 0..15), and the
-    //      fused append of this step's K rows (query group 0)
+    // ---- (q+u).k over the wave's columns: D rows 0..3 (lanes 0..15)
 #pragma unroll
-    for (int kt = 0; kt < NT; ++kt) {
+    for (int kt = 0; kt <= NT; ++kt) {
       f32x4_t d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) d = Mma<ST>::k32(aop[ks], kr[kt][ks], d);
+      for (int ks = 0; ks < KS; ++ks) d = Mma<ST>::k32(aop[ks], kt < NT ? kr[kt][ks] : kf[ks], d);
       if (kg == 0) {
         ac_lds[wave][0][16 * kt + q16] = d[0] + d[2];
         ac_lds[wave][1][16 * kt + q16] = d[1] + d[3];
-        ok_lds[wave][16 * kt + q16] = okk[kt] ? 1 : 0;
-      }
-      if (do_append && jb + 16 * kt + 15 >= p.left && jb + 16 * kt < p.Lk) {  // uniform
-        const int j = jb + 16 * kt + q16;
-        const int pos = win0 + min(j, p.Lk - 1);
-        if (j >= p.left && j < p.Lk && page[kt] >= 0 && page[kt] < p.pg.num_pages) {
-          const int64_t off = (int64_t)page[kt] * p.pg.page_elems +
-                              (int64_t)((uint32_t)pos & pmask) * p.pg.D;
-#pragma unroll
-          for (int ks = 0; ks < KS; ++ks) {
-            st16(const_cast<ST*>(kp_c) + off + ks * 8, kr[kt][ks]);
-            st16(const_cast<ST*>(vp_c) + off + ks * 8, vr[kt][ks]);
-          }
-        }
       }
     }
+    // ---- fused append of this step's K and V rows (query group 0): the row
+    //      index is valid only for lanes holding one of the chunk's frames
+    if (do_append && last) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        pk_buffer_store_x4(kf[ks], r_kp, frow, cbyte + ks * 16, 0, 0);
+        pk_buffer_store_x4(vf[ks], r_vp, frow, cbyte + ks * 16, 0, 0);
+      }
+    }
+    // ---- history V rows, issued once the K rows are consumed (half the
+    //      registers in flight); their latency overlaps the scores and softmax
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int kt = 0; kt < NT; ++kt)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) vr[kt][ks] = pk_buffer_load_x4(r_vp, prow[kt], cbyte + ks * 16, 0, 0);
     __syncthreads();  // partial dot products of the stream's waves in LDS
 
-    // ---- scores: lane handles keys lane + 64*r of the tile; online softmax
+    // ---- scores: lane handles slots lane + 64*r; online softmax
     float s[SK][TQ];
-    bool okr[SK];
 #pragma unroll
     for (int r = 0; r < SK; ++r) {
-      const int kk = lane + 64 * r;  // key within the tile
-      const int kkc = min(kk, KT - 1);
-      const int j = jb + kk;
-      okr[r] = ok_lds[wave][kkc] != 0;
+      const int sl = lane + 64 * r;
+      const int slc = min(sl, NS - 1);
+      const int j = slot_col(jb, slc);
+      const bool valid = sl < NS && (slc < KT ? j < p.left : (last && slc - KT < p.T));
 #pragma unroll
       for (int ii = 0; ii < TQ; ++ii) {
         float ac = 0.f, bd = 0.f;
+        // (q+v).pos row of column j for query i0 + ii, relative to the staged rows
+        const int prw = min(max(j - jb + TQ - 1 - ii, 0), PROWS - 1);
 #pragma unroll
         for (int x = 0; x < SPLIT; ++x) {
-          ac += ac_lds[w0 + x][ii][kkc];
-          bd += bd_lds[w0 + x][ii][kkc + TQ - 1 - ii];
+          ac += ac_lds[w0 + x][ii][slc];
+          bd += bd_lds[w0 + x][ii][prw];
         }
-        if (!okr[r]) ac = 0.f;  // a key outside the stream's history reads as zeros
         bool msk = false;
         if (mask_mode == 1) msk = mk[r][ii] != 0;
-        if (mask_mode == 2) msk = sm.masked(i0 + ii, qchunk[ii], min(j, p.Lk - 1));
+        if (mask_mode == 2) msk = sm.masked(i0 + ii, qchunk[ii], j);
         const float sc = msk ? fmaf(ac, p.scale, MASKED) : (ac + bd) * p.scale;
-        s[r][ii] = (kk < KT && j < p.Lk && ii < nq) ? sc : NEG;
+        s[r][ii] = (valid && ii < nq) ? sc : NEG;
       }
     }
     float corr[TQ];
@@ -914,11 +958,15 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
       float lsum = 0.f;
 #pragma unroll
       for (int r = 0; r < SK; ++r) {
-        const int kk = lane + 64 * r;
+        const int sl = lane + 64 * r;
         const float e = s[r][ii] > 0.5f * NEG ? __builtin_amdgcn_exp2f(s[r][ii] - mnew) : 0.f;
         lsum += e;
-        // the value sum sees zeros for keys outside the stream's history
-        if (kk < KT) p_lds[wave][ii][kk] = okr[r] ? e : 0.f;
+        if (sl < NS) {  // e = hi + lo in the operand type, exact to ~2^-17
+          const H hi = (H)e;
+          const H lo = (H)(e - (float)hi);
+          p_lds[wave][0][ii][sl] = __builtin_bit_cast(uint16_t, hi);
+          p_lds[wave][1][ii][sl] = __builtin_bit_cast(uint16_t, lo);
+        }
       }
       l_run[ii] = l_run[ii] * corr[ii] + wave_sum(lsum);
     }
@@ -931,20 +979,18 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
     }
     wave_lds_sync();
 
-    // ---- P.V, 16 keys at a time: stage the V rows, read them back transposed;
-    //      A rows 0..1 are the probabilities of the two queries, rows 2..3
-    //      their low parts (p = hi + lo), so D[q] + D[2 + q] is exact to ~2^-17
-    const bool p_row = q16 < 2 * TQ;
-    const bool p_low = q16 >= TQ;
+    // ---- P.V, 16 slots at a time: stage the V rows, read them back
+    //      transposed; A row m = q16 & 3 holds the high (m < 2) or low part of
+    //      query m & 1's probabilities, so D[q] + D[2 + q] is the product with
+    //      p = hi + lo; rows 4..15 repeat rows 0..3 and feed only D rows that
+    //      are never read
+    const uint16_t* p_arow = &p_lds[wave][(q16 >> 1) & 1][q16 & 1][0];
 #pragma unroll
-    for (int kt = 0; kt < NT; ++kt) {
+    for (int kt = 0; kt <= NT; ++kt) {
       uint8_t* vrow = vl + q16 * VSTRIDE + kg * 32;
-      *reinterpret_cast<u32x4*>(vrow) = vr[kt][0];
-      *reinterpret_cast<u32x4*>(vrow + 16) = vr[kt][1];
-      const float4 pp = *reinterpret_cast<const float4*>(&p_lds[wave][q16 & 1][16 * kt + 4 * kg]);
-      const float pv[4] = {pp.x, pp.y, pp.z, pp.w};
-      i16x4_t pop = split16<ST, 4, i16x4_t>(pv, p_low);
-      if (!p_row) pop = i16x4_t{0, 0, 0, 0};
+      *reinterpret_cast<u32x4*>(vrow) = kt < NT ? vr[kt][0] : vf[0];
+      *reinterpret_cast<u32x4*>(vrow + 16) = kt < NT ? vr[kt][1] : vf[1];
+      const i16x4_t pop = *reinterpret_cast<const i16x4_t*>(p_arow + 16 * kt + 4 * kg);
       wave_lds_sync();
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) {
@@ -955,7 +1001,7 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
       }
       wave_lds_sync();  // the next 16 rows overwrite the staging rows
     }
-    if (MULTI) __syncthreads();  // the next tile restages pos_lds and rewrites bd / ac
+    if (MULTI) __syncthreads();  // the next pass restages pos_lds and rewrites bd / ac
   }
 
   // ---- write: lanes 0..15 hold column nt*16 + q16 of both queries
@@ -963,7 +1009,7 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
 #pragma unroll
     for (int ii = 0; ii < TQ; ++ii) {
       if (ii >= nq) continue;
-      const float inv = l_run[ii] > 0.f ? 1.f / l_run[ii] : 0.f;
+      const float inv = l_run[ii] > 0.f ? __builtin_amdgcn_rcpf(l_run[ii]) : 0.f;
       ST* orow = p.out + b * p.o_sb + (int64_t)(i0 + ii) * p.o_st + hcol + q16;
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt)
@@ -1248,8 +1294,8 @@ int launch_attn_mfma_mode(const pk_attn_args* a, const AttnK<ST>& k, hipStream_t
 
 template <typename ST, int DK>
 int launch_attn_mfma(const pk_attn_args* a, AttnK<ST>& k, hipStream_t s) {
-  constexpr int KT = 16 * kMfmaTiles;
-  k.tiles = (k.Lk + KT - 1) / KT;
+  constexpr int KT = 16 * kMfmaTiles;  // history slots per pass
+  k.tiles = k.left > 0 ? (k.left + KT - 1) / KT : 1;
   if (k.mask) return launch_attn_mfma_mode<ST, DK, 1>(a, k, s);
   if (k.st_proc) return launch_attn_mfma_mode<ST, DK, 2>(a, k, s);
   return launch_attn_mfma_mode<ST, DK, 0>(a, k, s);
@@ -1353,7 +1399,16 @@ int attn_typed(const pk_attn_args* a, hipStream_t s) {
   if (a->num_heads > 65535 || a->chunk > 2 * 65535)
     return fail(PK_ERR_INVALID, "%s: num_heads or chunk exceeds the launch grid", what);
   if constexpr (!std::is_same<ST, float>::value) {
-    if (a->rows_per_lane == 0) {
+    // the matrix-core kernel addresses rows through buffer resources: row
+    // strides up to kMaxBufferStride bytes and fewer than 2^32 pool rows
+    const int64_t es = (int64_t)sizeof(ST);
+    auto row_bytes = [&](int64_t st) { return (st > 0 ? st : (int64_t)D) * es; };
+    const bool fits = (int64_t)D * es <= kMaxBufferStride &&
+                      row_bytes(a->key_stride_t) <= kMaxBufferStride &&
+                      row_bytes(a->value_stride_t) <= kMaxBufferStride &&
+                      row_bytes(a->pos_stride) <= kMaxBufferStride &&
+                      (!need_pages || ((int64_t)a->pages.num_pages * a->pages.page_size < (1LL << 32)));
+    if (a->rows_per_lane == 0 && fits && a->chunk <= 16) {
       if (DK == 64) return launch_attn_mfma<ST, 64>(a, k, s);
       return launch_attn_mfma<ST, 128>(a, k, s);
     }
