@@ -1,0 +1,232 @@
+"""GPU parity of the drop-in modules -- the reference's Python surfaces on the
+paged cache -- against the oracle:
+
+* ModelCache.update_attn_cache (parakeet/modules/cache.py:36-45): the returned
+  windows equal the dense shift buffer bit for bit, step after step, through
+  the full cache, prefix views (cache.py:65-77) and shuffled slot subsets (the
+  batches Scheduler.pack_states forms), with slot resets (cache.py:60-63);
+* ConformerAttention.forward (parakeet/modules/attention.py:85-125) with its
+  own projections: the module's q/k/v and position projections feed the
+  oracle's float64 rel-pos attention over the dense window, and linear_out is
+  applied in float64; with a cache over several steps, and without a cache;
+* ConformerEncoder (parakeet/modules/encoder.py:140-267): streaming steps of a
+  random-init 2-layer stack on the GPU against the same weights in float64 on
+  the CPU where every layer's attention is the oracle over a dense cache and
+  the masks are the oracle's loop (encoder.py:167-227); the state scalars
+  advance as encoder.py:257-260.
+"""
+
+import copy
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oa
+from oracle import masks as om
+from parakeet_amd.modules.attention import ConformerAttention, PositionalEncoding
+from parakeet_amd.modules.cache import ModelCache, StreamingState
+from parakeet_amd.modules.encoder import ConformerEncoder
+
+
+def _dense_shift(win, slot, layer, left, new):
+    """cache.py:37-44 for one stream: keep the last `left` frames, append."""
+    if left > 0:
+        win[slot, layer, :left] = win[slot, layer, -left:].copy()
+    win[slot, layer, left:] = new
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_model_cache_windows_match_dense(cuda, dtype):
+    print(f"\n[model-cache] {dtype}", flush=True)
+    left, right, D, Ly, N = 9, 1, 64, 2, 5
+    T = right + 1
+    L = left + T
+    mc = ModelCache(Ly, (left, right), D, 9, batch_size=N, device=cuda, dtype=dtype, page_size=4)
+    win_k = np.zeros((N, Ly, L, D))
+    win_v = np.zeros((N, Ly, L, D))
+    rng = np.random.default_rng(0)
+    g = torch.Generator().manual_seed(0)
+    for step in range(30):
+        if step % 7 == 6:
+            s = step % N
+            mc.reset_slot(s)
+            win_k[s] = 0
+            win_v[s] = 0
+        kind = step % 3
+        if kind == 0:
+            view, slots = mc, np.arange(N)
+        elif kind == 1:
+            view, slots = mc.view(3), np.arange(3)
+        else:
+            slots = rng.permutation(N)[:4]
+            view = mc.batch(slots)
+        B = len(slots)
+        for layer in range(Ly):
+            x = torch.randn(B, T, 3 * D, generator=g).to(dtype)
+            _, k, v = x.to(cuda).chunk(3, dim=-1)  # strided views, as qkv.chunk(3)
+            gk, gv = view.update_attn_cache(layer, k, v)
+            kc, vc = k.cpu().double().numpy(), v.cpu().double().numpy()
+            for b, s in enumerate(slots):
+                _dense_shift(win_k, s, layer, left, kc[b])
+                _dense_shift(win_v, s, layer, left, vc[b])
+            assert torch.equal(gk.cpu(), torch.from_numpy(win_k[slots, layer]).to(dtype)), f"step {step} layer {layer}"
+            assert torch.equal(gv.cpu(), torch.from_numpy(win_v[slots, layer]).to(dtype)), f"step {step} layer {layer}"
+    torch.cuda.synchronize()
+
+
+def _init_attention(att, D, seed):
+    g = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        for lin in (att.qkv, att.linear_pos, att.linear_out):
+            lin.weight.copy_(torch.randn(lin.weight.shape, generator=g) / math.sqrt(D))
+        att.pos_bias_u.copy_(torch.randn(att.pos_bias_u.shape, generator=g) * 0.02)
+        att.pos_bias_v.copy_(torch.randn(att.pos_bias_v.shape, generator=g) * 0.02)
+
+
+# fp32: the kernel's 1e-4; fp16: the kernel's 2e-3 plus linear_out's fp16
+# rounding of its input and output (outputs are O(1))
+ATT_TOL = {torch.float32: 1e-4, torch.float16: 6e-3}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_conformer_attention_matches_oracle(cuda, dtype):
+    print(f"\n[conformer-attention] {dtype}", flush=True)
+    H, dk, left, right, B = 8, 64, 20, 1, 3
+    D, T = H * dk, right + 1
+    L = left + T
+    att = ConformerAttention(0, H, D)
+    _init_attention(att, D, seed=1)
+    att = att.to(device=cuda, dtype=dtype)
+    pe = PositionalEncoding(D, 0.0, 128, 0.0)
+    pe.extend_pe(128, device=cuda)
+    mc = ModelCache(1, (left, right), D, 9, batch_size=B, device=cuda, dtype=dtype, page_size=16)
+    win_k = np.zeros((B, 1, L, D))
+    win_v = np.zeros((B, 1, L, D))
+    proc = np.zeros(B, dtype=np.int64)
+    g = torch.Generator().manual_seed(2)
+    w_out = att.linear_out.weight.detach().double().cpu().numpy()
+    bu = att.pos_bias_u.detach().double().cpu().numpy()
+    bv = att.pos_bias_v.detach().double().cpu().numpy()
+    worst = 0.0
+    for step in range(14):
+        x = torch.randn(B, T, D, generator=g).to(dtype).to(cuda)
+        _, pos_emb = pe(x, cache_len=left)
+        pos_emb = pos_emb.to(dtype)
+        cl = np.minimum(proc, left)
+        _, mask = om.create_streaming_masks(T, cl, proc, T, (left, right))
+        with torch.no_grad():
+            out = att(x, pos_emb, torch.from_numpy(mask).to(cuda), cache=mc)
+            q, k, v = (t.double().cpu().numpy() for t in att.qkv(x).chunk(3, dim=-1))
+            pos = att.linear_pos(pos_emb)[0].double().cpu().numpy()
+        for b in range(B):
+            _dense_shift(win_k, b, 0, left, k[b])
+            _dense_shift(win_v, b, 0, left, v[b])
+        core = oa.relpos_attention(q, win_k[:, 0], win_v[:, 0], pos, bu, bv, mask, H)
+        ref = core @ w_out.T
+        err = float(np.abs(out.double().cpu().numpy() - ref).max())
+        worst = max(worst, err)
+        assert err <= ATT_TOL[dtype], f"step {step}: max abs err {err:.3e}"
+        proc += T
+    print(f"  worst max-abs error {worst:.3e}", flush=True)
+    # without a cache the keys are this chunk's frames only
+    x = torch.randn(B, T, D, generator=g).to(dtype).to(cuda)
+    _, pos_emb = pe(x, cache_len=0)
+    pos_emb = pos_emb.to(dtype)
+    with torch.no_grad():
+        out = att(x, pos_emb, None, cache=None)
+        q, k, v = (t.double().cpu().numpy() for t in att.qkv(x).chunk(3, dim=-1))
+        pos = att.linear_pos(pos_emb)[0].double().cpu().numpy()
+    ref = oa.relpos_attention(q, k, v, pos, bu, bv, None, H) @ w_out.T
+    assert float(np.abs(out.double().cpu().numpy() - ref).max()) <= ATT_TOL[dtype]
+    torch.cuda.synchronize()
+
+
+class _DenseCache:
+    """Dense per-stream cache for the CPU reference encoder: K/V shift buffers
+    (cache.py:19-45) and the conv cache (cache.py:30-34,47-53)."""
+
+    def __init__(self, B, Ly, left, right, D, K):
+        self.left = left
+        self.k = np.zeros((B, Ly, left + right + 1, D))
+        self.v = np.zeros_like(self.k)
+        self.conv = torch.zeros(B, Ly, D, K - 1, dtype=torch.float64)
+
+    def get_conv_cache(self, layer):
+        return self.conv[:, layer]
+
+    def update_conv_cache(self, layer, state):
+        self.conv[:, layer] = state
+
+
+def _oracle_attention(att, left, H):
+    """Replaces ConformerAttention.forward on the CPU reference: the module's
+    projections, the dense cache update and the oracle's rel-pos attention."""
+
+    def forward(x, pos_emb, attn_mask=None, cache=None):
+        q, k, v = (t.numpy() for t in att.qkv(x).chunk(3, dim=-1))
+        pos = att.linear_pos(pos_emb)[0].numpy()
+        layer = att.layer_idx
+        for b in range(x.shape[0]):
+            _dense_shift(cache.k, b, layer, left, k[b])
+            _dense_shift(cache.v, b, layer, left, v[b])
+        core = oa.relpos_attention(
+            q, cache.k[:, layer], cache.v[:, layer], pos,
+            att.pos_bias_u.detach().numpy(), att.pos_bias_v.detach().numpy(), attn_mask.numpy(), H,
+        )
+        return att.linear_out(torch.from_numpy(core))
+
+    return forward
+
+
+@pytest.mark.gpu
+def test_encoder_streaming_matches_dense_reference(cuda):
+    print("\n[encoder] 2 layers fp32 vs float64 dense reference", flush=True)
+    left, right, D, H, Ly, B, K = 6, 1, 128, 2, 2, 3, 9
+    T = right + 1
+    torch.manual_seed(3)
+    enc = ConformerEncoder(
+        feat_in=80, hidden_size=D, ff_expansion_factor=2, num_layers=Ly, num_heads=H,
+        subsampling_factor=8, pos_emb_max_len=64, conv_kernel_size=K, att_context_size=[left, right],
+        subsampling_conv_channels=32, use_bias=False, page_size=4,
+    )
+    for layer in enc.layers:
+        _init_attention(layer.self_attn, D, seed=10 + layer.layer_idx)
+    ref = copy.deepcopy(enc).double()
+    enc = enc.to(cuda)
+    state = enc.init_streaming_state(batch_size=B, device=cuda, dtype=torch.float32)
+    dense = _DenseCache(B, Ly, left, right, D, K)
+    for layer in ref.layers:
+        layer.self_attn.forward = _oracle_attention(layer.self_attn, left, H)
+    proc = np.zeros(B, dtype=np.int64)
+    cl = np.zeros(B, dtype=np.int64)
+
+    def ref_masks(current_len, cache_lengths, processed_frames, device, lengths):
+        pad, att = om.create_streaming_masks(
+            current_len, cache_lengths.numpy(), processed_frames.numpy(), lengths.numpy(), (left, right)
+        )
+        return torch.from_numpy(pad), torch.from_numpy(att)
+
+    ref._create_streaming_masks = ref_masks
+    g = torch.Generator().manual_seed(4)
+    worst = 0.0
+    for step in range(12):
+        x = torch.randn(B, T, D, generator=g)
+        # the engine passes per-stream lengths as a tensor (model_runner.py:285-291)
+        lengths = torch.full((B,), T, dtype=torch.int64)
+        with torch.no_grad():
+            out, state = enc(x.to(cuda), state, length=lengths.to(cuda))
+            rstate = StreamingState(dense, torch.from_numpy(proc.copy()), torch.from_numpy(cl.copy()))
+            rout, _ = ref(x.double(), rstate, length=lengths)
+        err = float((out.double().cpu() - rout).abs().max())
+        worst = max(worst, err)
+        assert err <= 2e-4, f"step {step}: max abs err {err:.3e}"
+        proc += T
+        cl = np.minimum(cl + T, left)
+        assert state.processed_frames.cpu().tolist() == proc.tolist()
+        assert state.cache_lengths.cpu().tolist() == cl.tolist()
+    print(f"  worst max-abs error {worst:.3e}", flush=True)
+    torch.cuda.synchronize()
