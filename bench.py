@@ -19,6 +19,7 @@ Prints one JSON line on stdout; progress goes to stderr.
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import math
 import os
@@ -70,14 +71,47 @@ def build_runner(cfg, device, rows_per_lane=0):
     return shape, runner, churn
 
 
-def churn_step(runner, churn, events=None) -> int:
+def churn_step(runner, churn, events=None, graph=False) -> int:
     import numpy as np
 
     departed, _arrived = churn.step()
     runner.reset_slots(departed)
     active = np.asarray(churn.active(), dtype=np.int32)
-    runner.step(active, events)
+    runner.step(active, events, graph=graph)
     return int(active.shape[0])
+
+
+TRAFFIC_SUMMARY = os.path.join(HERE, "profiles", "relpos_attn_large_bf16_230streams_hbm_counters.md")
+
+
+def measured_traffic(config_name: str, avg_streams: float):
+    """HBM bytes per launch of the attention kernel on this workload, from the
+    committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (copy-calibrated), when
+    that summary covers the same configuration and batch; None otherwise."""
+    import re
+
+    if config_name != "large" or not os.path.exists(TRAFFIC_SUMMARY):
+        return None
+    txt = open(TRAFFIC_SUMMARY).read()
+    m = re.search(r"^traffic_bytes_per_launch: (\d+)$", txt, re.M)
+    n = re.search(r"^traffic_streams: (\d+)$", txt, re.M)
+    if not m or not n or abs(avg_streams - int(n.group(1))) > 0.5:
+        return None
+    return int(m.group(1))
+
+
+def copy_probe(megabytes: int, reps: int) -> dict:
+    """A plain device copy of known size (reads and writes `megabytes` MiB per
+    launch): the calibration run for the HBM byte counters."""
+    import torch
+
+    n = megabytes << 20
+    a = torch.ones(n // 2, dtype=torch.bfloat16, device="cuda:0")
+    b = torch.empty_like(a)
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    return {"copy_probe_bytes_read": n, "copy_probe_bytes_written": n, "launches": reps}
 
 
 def cpu_baseline(shape, streams: int, budget_s: float, seed: int) -> dict:
@@ -132,6 +166,9 @@ def main() -> int:
     ap.add_argument("--preroll", type=int, default=60, help="untimed steps before warmup to reach steady-state windows")
     ap.add_argument("--rows-per-lane", type=int, default=0)
     ap.add_argument("--no-kernel-events", action="store_true")
+    ap.add_argument("--kernel-event-steps", type=int, default=50, help="eager steps timed per kernel for the roofline")
+    ap.add_argument("--graph", action="store_true", help="replay every step's launches from one HIP graph (grid sized for all slots)")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB", help="only run a device copy of MIB MiB (counter calibration)")
     ap.add_argument("--cpu-baseline-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -153,10 +190,17 @@ def main() -> int:
         print("bench.py needs a HIP device", file=sys.stderr)
         return 1
     device = torch.device("cuda:0")
+    if args.copy_probe:
+        print(json.dumps(copy_probe(args.copy_probe, max(1, args.steps))), flush=True)
+        return 0
     cfg = CONFIGS[args.config]
     log(f"config {args.config}: building workload")
     shape, runner, churn = build_runner(cfg, device, args.rows_per_lane)
     Ly = shape.layers
+    # the objects built so far live for the whole run: keep them out of the
+    # collector's scans, so a full collection in the step loop stays short
+    gc.collect()
+    gc.freeze()
 
     with torch.inference_mode():
         for _ in range(args.preroll):
@@ -168,11 +212,39 @@ def main() -> int:
         torch.cuda.synchronize()
         log(f"warmup {args.warmup} steps done")
 
+        use_graph = args.graph
+        if use_graph:
+            runner.capture()
+            for _ in range(max(1, args.warmup // 2)):
+                churn_step(runner, churn, graph=True)
+            torch.cuda.synchronize()
+            log("graph captured and replayed")
+
+        # timed pass 1: the step loop as it serves (host page work + one upload +
+        # every layer's launch; replayed from one HIP graph with --graph)
         K = args.steps
+        batches = []
+        step_ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        start.record()
+        for k in range(K):
+            step_ev[k][0].record()
+            batches.append(churn_step(runner, churn, graph=use_graph))
+            step_ev[k][1].record()
+        stop.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        log(f"timed {K} steps done")
+
+        # timed pass 2: every kernel between its own HIP events (eager launches),
+        # for the roofline
         use_ev = not args.no_kernel_events
-        ev_pairs = []
+        K2 = min(K, args.kernel_event_steps)
+        ev_pairs, ev_batches = [], []
         if use_ev:
-            for _ in range(K):
+            for _ in range(K2):
                 pairs = []
                 for _ in range(Ly):
                     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -182,23 +254,17 @@ def main() -> int:
                 ev_pairs.append(pairs)
             torch.cuda.synchronize()
             handles = [[(ops._event_handle(a), ops._event_handle(b)) for a, b in pairs] for pairs in ev_pairs]
-        batches = []
-        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        start.record()
-        for k in range(K):
-            batches.append(churn_step(runner, churn, handles[k] if use_ev else None))
-        stop.record()
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-        log(f"timed {K} steps done")
+            for k in range(K2):
+                ev_batches.append(churn_step(runner, churn, handles[k]))
+            torch.cuda.synchronize()
+            log(f"timed {K2} steps with per-kernel events done")
 
     ms_total = start.elapsed_time(stop)
     ms_per_step = ms_total / K
+    gpu_ms_per_step = sum(a.elapsed_time(b) for a, b in step_ev) / K
     per_stream = runner.bytes_per_stream()
     shared = runner.bytes_shared_per_launch()
-    total_bytes = sum(B * Ly * per_stream + Ly * shared for B in batches)
+    total_bytes = sum(B * Ly * per_stream + Ly * shared for B in ev_batches)
     kern_ms = None
     if use_ev:
         kern_ms = sum(a.elapsed_time(b) for pairs in ev_pairs for a, b in pairs)
@@ -236,7 +302,9 @@ def main() -> int:
             "stream_slots": cfg["slots"],
             "avg_active_streams": round(avg_B, 1),
             "parallelism": "single GPU",
+            "launch": "one HIP graph replay per step (all layers)" if use_graph else "one host launch per layer",
         },
+        "gpu_ms_per_step": round(gpu_ms_per_step, 4),
         "concurrent_streams": {
             "measured_batch": round(avg_B, 1),
             "pool_capacity_hbm": pool_capacity,
@@ -252,9 +320,10 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel": "relpos_attn_kernel (fused append + paged rel-pos attention)",
-            "avg_kernel_us": round(1000.0 * kern_ms / (K * Ly), 3),
+            "traffic": measured_traffic(args.config, float(np.mean(ev_batches))),
+            "kernel": "relpos_attn_mfma_kernel (fused append + paged rel-pos attention)",
+            "avg_kernel_us": round(1000.0 * kern_ms / (len(ev_batches) * Ly), 3),
+            "kernel_event_steps": len(ev_batches),
             "bytes_per_stream_layer": per_stream,
         }
         result["paged_attn_hbm_gbs"] = round(achieved, 1)

@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define PK_ABI_VERSION 2
+#define PK_ABI_VERSION 3
 
 enum pk_dtype { PK_DTYPE_F32 = 0, PK_DTYPE_F16 = 1, PK_DTYPE_BF16 = 2 };
 
@@ -138,6 +138,12 @@ int pk_kv_gather(const pk_kv_gather_args* args, void* stream);
  *   both NULL      no mask.
  * All floating tensors share `dtype`.  head_dim must be 64 or 128.
  * start_event/stop_event: optional hipEvent_t pair timing this kernel alone.
+ * live_streams: optional int32 in device memory.  When set, `batch` is the row
+ * count of every batch array (rows, query/key/value, out, mask, state) and only
+ * streams 0 .. *live_streams - 1 are attended, appended and written; the count is
+ * read when the kernel runs, so one launch recorded in a HIP graph serves a batch
+ * whose size changes from step to step (the reference re-packs a batch of the
+ * current size every step, scheduler.py:128-170).  NULL: all `batch` streams.
  */
 typedef struct pk_attn_args {
   int32_t dtype;
@@ -179,6 +185,7 @@ typedef struct pk_attn_args {
   int32_t rows_per_lane; /* tuning: key rows per lane per tile, 0 = automatic */
   void* start_event;
   void* stop_event;
+  const int32_t* live_streams;
 } pk_attn_args;
 int pk_paged_relpos_attn(const pk_attn_args* args, void* stream);
 

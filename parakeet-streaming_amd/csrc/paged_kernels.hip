@@ -210,8 +210,9 @@ struct AttnK {
   uint32_t c_magic;
   ST* out;
   int64_t o_sb, o_st;
-  int32_t B, T, H, left, Lk, append, tiles;
-  float scale;  // log2(e) / sqrt(head_dim)
+  int32_t B, T, H, left, Lk, append, tiles;  // B: rows of the batch arrays
+  const int32_t* nact;  // streams 0..*nact-1 are live (nullptr: all B)
+  float scale;          // log2(e) / sqrt(head_dim)
 };
 
 // Streaming-mask state of one stream (encoder.py:186-212), 32-bit.  The key and
@@ -285,6 +286,7 @@ __global__ void __launch_bounds__(64) relpos_attn_kernel(const AttnK<ST> p) {
   const int rl = lane / G;
   const int b = blockIdx.x / p.H;
   const int h = blockIdx.x - b * p.H;
+  if (p.nact && b >= *p.nact) return;  // the wave's stream is not live this step
   const int i0 = blockIdx.y * TQ;
   const int nq = min(TQ, p.T - i0);
   const int col = h * DK + g * VEC;
@@ -691,12 +693,12 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
   const int sw = wave / SPLIT;  // stream slot in the workgroup
   const int hf = wave % SPLIT;  // 64-column part of the head
   const int w0 = sw * SPLIT;    // first wave of this stream
+  const int sb = blockIdx.x;  // stream block
   const int h = blockIdx.y;
   const int i0 = blockIdx.z * TQ;
   const int nq = min(TQ, p.T - i0);
-  const int b_raw = blockIdx.x * SPW + sw;
-  const bool active = b_raw < p.B;  // uniform per wave
-  const int b = active ? b_raw : p.B - 1;
+  const int b_raw = sb * SPW + sw;
+  const int b = min(b_raw, p.B - 1);  // loads stay inside the batch arrays
   const int hcol = h * DK + hf * 64;       // first column of the wave
   const int cbyte = (hcol + kg * 16) * ES;  // byte offset of the lane's 16 columns in a row
   const int M = p.pg.max_pages;
@@ -735,6 +737,7 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
   const int64_t* stc = mask_mode == 2 ? p.st_cl + b : stp;
   const int64_t* stn = (mask_mode == 2 && p.st_len) ? p.st_len + b : stp;
   const int64_t st_pr_v = *stp, st_cl_v = *stc, st_n_v = *stn;
+  const int32_t nact_v = p.nact ? *p.nact : p.B;
   // A operand source: row m = q16 is (q+u)_hi, (q+u)_lo, (q+v)_hi, (q+v)_lo of
   // query m & 1 for m < 8, zero above; element e of k-step ks is column
   // kg*16 + ks*8 + e of the wave's 64
@@ -784,6 +787,14 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
   };
   load_pass_shared(0);
   __builtin_amdgcn_sched_barrier(0);  // all of the above in flight before any use
+
+  // ---------------- live streams: a launch recorded once for a batch that
+  //                  changes reads the live count from the device; workgroups
+  //                  past it end here (workgroup-uniform, so no barrier is left
+  //                  waiting)
+  const int nact = min(__builtin_amdgcn_readfirstlane(nact_v), p.B);
+  if (sb * SPW >= nact) return;
+  const bool active = b_raw < nact;  // uniform per wave
 
   // ---------------- per-stream scalars
   const int A = paged ? __builtin_amdgcn_readfirstlane(hdr_a) : 0;
@@ -1389,6 +1400,7 @@ int attn_typed(const pk_attn_args* a, hipStream_t s) {
   k.o_sb = a->out_stride_b;
   k.o_st = a->out_stride_t;
   k.B = a->batch;
+  k.nact = a->live_streams;
   k.T = a->chunk;
   k.H = a->num_heads;
   k.left = a->left;

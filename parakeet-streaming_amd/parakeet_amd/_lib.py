@@ -15,7 +15,7 @@ from pathlib import Path
 LIB_NAME = "libparakeet_paged.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -119,6 +119,7 @@ class AttnArgs(ctypes.Structure):
         ("rows_per_lane", c_int32),
         ("start_event", c_void_p),
         ("stop_event", c_void_p),
+        ("live_streams", c_void_p),
     ]
 
 

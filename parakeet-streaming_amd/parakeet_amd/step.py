@@ -5,10 +5,11 @@ This is the hot path of ``_encode_step`` (parakeet/engine/model_runner.py:254-30
 reduced to its paged-cache work, for serving loops that drive the kernels
 directly and for measurement:
 
-  1. open the step on the host page pool (evict / allocate) and upload, in two
-     asynchronous copies from pinned memory, the batch's page rows and its
-     processed_frames / cache_lengths (the reference gathers these per step with
-     index_select, parakeet/engine/scheduler.py:128-170);
+  1. open the step on the host page pool (evict / allocate) and upload, in one
+     asynchronous copy from pinned memory, the live stream count, the batch's
+     processed_frames / cache_lengths and its block-table rows (the reference
+     gathers the state per step with index_select, parakeet/engine/scheduler.py:
+     128-170);
   2. per layer: one kernel -- fused page append + paged rel-pos attention with
      the streaming mask evaluated in the kernel from the stream state
      (attention.py:97-121, encoder.py:167-227);
@@ -17,6 +18,11 @@ directly and for measurement:
 The engine always feeds whole chunks (parakeet/engine/sequence.py:137-146), so
 ``length`` is the chunk for every stream and the state advance is known on the
 host without a device round trip.
+
+Every device pointer the launches use is fixed for the life of the object (the
+batch arrays are sized for all slots and the live count is read on the device),
+so ``capture()`` can record all layers' launches once in a HIP graph and
+``step(..., graph=True)`` replays it for a batch of any size.
 
 The qkv projection output of every layer is an input ([slots, T, 3D] per
 layer, q | k | v; batch row b reads row b); the outputs land in per-layer
@@ -35,6 +41,8 @@ from ._lib import AttnArgs, check, lib
 from .pool import PagePool
 from .synth import Shape
 
+_HDR = 16  # bytes before the state: the int32 live count, padded
+
 
 class AttentionStep:
     def __init__(
@@ -51,34 +59,45 @@ class AttentionStep:
         rows_per_lane: int = 0,
     ):
         self.shape = shape
-        self.num_slots = int(num_slots)
+        self.num_slots = S = int(num_slots)
         self.device = device
         T, D, Ly = shape.chunk, shape.d_model, shape.layers
-        self.pool = PagePool(num_slots, shape.page_size, shape.left, T, num_pages=num_pages, page_order=page_order)
+        self.pool = PagePool(S, shape.page_size, shape.left, T, num_pages=num_pages, page_order=page_order)
         M = self.pool.max_pages
         self.k_pages = torch.empty((Ly, self.pool.num_pages, shape.page_size, D), dtype=shape.dtype, device=device)
         self.v_pages = torch.empty_like(self.k_pages)
-        self.rows = torch.zeros((num_slots, 1 + M), dtype=torch.int32, device=device)
-        # batch-ordered processed_frames [0, B) then cache_lengths [B, 2B)
-        self.state = torch.zeros(2 * num_slots, dtype=torch.int64, device=device)
+        # one upload per step: [live count | pad][processed_frames[S] | cache_lengths[S]][rows[S][1+M]]
+        self._state_off = _HDR
+        self._rows_off = _HDR + 16 * S
+        self._meta_bytes = self._rows_off + 4 * S * (1 + M)
+        self.meta = torch.zeros(self._meta_bytes, dtype=torch.uint8, device=device)
+        self.live, self.state, self.rows = self._views(self.meta)
         # per-slot streaming state, advanced on the host (length == chunk)
-        self.h_proc = np.zeros(num_slots, dtype=np.int64)
-        self.h_cl = np.zeros(num_slots, dtype=np.int64)
-        self.out = [torch.empty((num_slots, T, D), dtype=shape.dtype, device=device) for _ in range(Ly)]
-        if len(qkv) != Ly or any(tuple(x.shape) != (num_slots, T, 3 * D) for x in qkv):
-            raise ValueError(f"qkv must be {Ly} tensors of shape {(num_slots, T, 3 * D)}")
+        self.h_proc = np.zeros(S, dtype=np.int64)
+        self.h_cl = np.zeros(S, dtype=np.int64)
+        self.out = [torch.empty((S, T, D), dtype=shape.dtype, device=device) for _ in range(Ly)]
+        if len(qkv) != Ly or any(tuple(x.shape) != (S, T, 3 * D) for x in qkv):
+            raise ValueError(f"qkv must be {Ly} tensors of shape {(S, T, 3 * D)}")
         self.qkv = qkv
         self.pos, self.bias_u, self.bias_v = pos, bias_u, bias_v
-        # pinned staging for the per-step uploads, ring of 4: a buffer is reused
-        # only after the copy that read it has completed
+        # pinned staging, ring of 4: a buffer is reused only after the copy that
+        # read it has completed
         depth = 4
-        self._stage_rows = [torch.empty((num_slots, 1 + M), dtype=torch.int32, pin_memory=True) for _ in range(depth)]
-        self._stage_state = [torch.empty(2 * num_slots, dtype=torch.int64, pin_memory=True) for _ in range(depth)]
-        self._stage_ev: list[torch.cuda.Event | None] = [None] * depth
+        self._stage = [torch.zeros(self._meta_bytes, dtype=torch.uint8, pin_memory=True) for _ in range(depth)]
+        self._stage_ev = [torch.cuda.Event() for _ in range(depth)]
+        self._stage_used = [False] * depth
         self._stage_i = 0
         self._args = [self._attn_args(layer, rows_per_lane) for layer in range(Ly)]
         self._stream = ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
         self.batch = 0
+        self.graph: torch.cuda.CUDAGraph | None = None
+
+    def _views(self, buf: torch.Tensor):
+        S, M = self.num_slots, self.pool.max_pages
+        live = buf[0:4].view(torch.int32)
+        state = buf[self._state_off : self._rows_off].view(torch.int64)
+        rows = buf[self._rows_off :].view(torch.int32).view(S, 1 + M)
+        return live, state, rows
 
     # ------------------------------------------------------------ arg structs
     def _attn_args(self, layer: int, rows_per_lane: int) -> AttnArgs:
@@ -103,7 +122,7 @@ class AttentionStep:
         a.bias_u, a.bias_v = bu.data_ptr(), bv.data_ptr()
         # streaming mask from the stream state (encoder.py:167-227), length == chunk
         a.processed_frames = self.state.data_ptr()
-        a.cache_lengths = self.state.data_ptr()  # set per batch in run()
+        a.cache_lengths = self.state.data_ptr() + 8 * self.num_slots
         a.length_scalar = sh.chunk
         a.chunk_size = sh.right + 1
         o = self.out[layer]
@@ -124,26 +143,28 @@ class AttentionStep:
 
     # ------------------------------------------------------------ one step
     def open(self, slots: np.ndarray) -> int:
-        """Host page work + uploads for the batch ``slots``; returns B."""
+        """Host page work + the upload for the batch ``slots``; returns B."""
         slots = np.ascontiguousarray(slots, dtype=np.int32)
         B = int(slots.shape[0])
-        if B > self.num_slots:
-            raise ValueError(f"batch of {B} streams exceeds {self.num_slots} slots")
+        S = self.num_slots
+        if B > S:
+            raise ValueError(f"batch of {B} streams exceeds {S} slots")
         i = self._stage_i
-        self._stage_i = (i + 1) % len(self._stage_rows)
-        ev = self._stage_ev[i]
-        if ev is not None:
-            ev.synchronize()
-        rows_h = self._stage_rows[i]
-        self.pool.advance(slots, out=rows_h.numpy())
-        st = self._stage_state[i].numpy()
+        self._stage_i = (i + 1) % len(self._stage)
+        if self._stage_used[i]:
+            self._stage_ev[i].synchronize()
+        buf = self._stage[i]
+        live, state, rows = self._views(buf)
+        live.fill_(B)
+        st = state.numpy()
         st[:B] = self.h_proc[slots]
-        st[B : 2 * B] = self.h_cl[slots]
-        self.rows[:B].copy_(rows_h[:B], non_blocking=True)
-        self.state[: 2 * B].copy_(self._stage_state[i][: 2 * B], non_blocking=True)
-        ev = torch.cuda.Event()
-        ev.record()
-        self._stage_ev[i] = ev
+        st[S : S + B] = self.h_cl[slots]
+        if B:
+            self.pool.advance(slots, out=rows.numpy())
+        n = self._rows_off + 4 * B * (1 + self.pool.max_pages)
+        self.meta[:n].copy_(buf[:n], non_blocking=True)
+        self._stage_ev[i].record()
+        self._stage_used[i] = True
         # encoder.py:257-260 with length == chunk
         T = self.shape.chunk
         self.h_proc[slots] += T
@@ -152,25 +173,49 @@ class AttentionStep:
         return B
 
     def run(self, events=None) -> None:
-        """All layers' fused append + attention for the batch opened last.
-        ``events``: optional per-layer (start, stop) pairs timing each kernel."""
+        """All layers' fused append + attention for the batch opened last, one
+        launch per layer sized to the batch.  ``events``: optional per-layer
+        (start, stop) pairs timing each kernel."""
         B = self.batch
         if B == 0:
             return
         L = lib()
-        cl_ptr = self.state.data_ptr() + 8 * B
         for layer, a in enumerate(self._args):
             a.batch = B
-            a.cache_lengths = cl_ptr
+            a.live_streams = None
             if events is not None:
                 a.start_event, a.stop_event = events[layer]
             else:
                 a.start_event = a.stop_event = None
             check(L.pk_paged_relpos_attn(ctypes.byref(a), self._stream), "pk_paged_relpos_attn")
 
-    def step(self, slots: np.ndarray, events=None) -> None:
+    def capture(self) -> None:
+        """Records every layer's launch in a HIP graph: the launches cover all
+        slots and read the live count from the device, so one recording serves
+        every batch size.  The recording holds no memset and no allocation."""
+        L = lib()
+        g = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream(self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.graph(g, stream=side):
+            stream = ctypes.c_void_p(torch.cuda.current_stream(self.device).cuda_stream)
+            for a in self._args:
+                a.batch = self.num_slots
+                a.live_streams = self.live.data_ptr()
+                a.start_event = a.stop_event = None
+                check(L.pk_paged_relpos_attn(ctypes.byref(a), stream), "pk_paged_relpos_attn")
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        self.graph = g
+
+    def step(self, slots: np.ndarray, events=None, graph: bool = False) -> None:
         self.open(slots)
-        self.run(events)
+        if graph:
+            if self.graph is None:
+                self.capture()
+            if self.batch:
+                self.graph.replay()
+        else:
+            self.run(events)
 
     # ------------------------------------------------------------ accounting
     def bytes_per_stream(self) -> int:

@@ -22,8 +22,8 @@ from parakeet_amd.step import AttentionStep
 TOL = {torch.float32: 1e-4, torch.float16: 2e-3, torch.bfloat16: 1e-2}
 
 
-def _run(cuda, shape, slots, steps, seed, rows_per_lane=0):
-    print(f"\n[step] {shape.name} slots={slots} steps={steps} nr={rows_per_lane}", flush=True)
+def _run(cuda, shape, slots, steps, seed, rows_per_lane=0, graph=False):
+    print(f"\n[step] {shape.name} slots={slots} steps={steps} nr={rows_per_lane} graph={graph}", flush=True)
     T, D, Ly, L, left = shape.chunk, shape.d_model, shape.layers, shape.window, shape.left
     g = torch.Generator().manual_seed(seed)
     rng = np.random.default_rng(seed)
@@ -60,7 +60,7 @@ def _run(cuda, shape, slots, steps, seed, rows_per_lane=0):
             x = torch.randn(B, T, 3 * D, generator=g).to(shape.dtype)
             qkv[layer][:B].copy_(x.to(cuda))
             frames.append(x.double().numpy())
-        st.step(batch)
+        st.step(batch, graph=graph)
         _, mask = om.create_streaming_masks(T, cl[batch], proc[batch], T, (left, shape.right))
         for layer in range(Ly):
             q, k, v = np.split(frames[layer], 3, axis=-1)
@@ -110,3 +110,13 @@ def test_step_t14_chunks(cuda):
     straddle pages and several query groups per stream."""
     shape = synth.Shape("large-t14-bf16", 2, 1024, 8, right=13, dtype=torch.bfloat16)
     _run(cuda, shape, slots=4, steps=14, seed=7)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", [SMALL, LARGE], ids=lambda s: s.name)
+def test_step_graph_replays_match_oracle(cuda, shape):
+    """All layers recorded once in a HIP graph and replayed every step for
+    batches of changing size (the live count is read on the device); between
+    replays the test's own eager work runs (uploads, gathers, copies back,
+    synchronizations) and every replay is checked against the oracle."""
+    _run(cuda, shape, slots=6, steps=30, seed=8, graph=True)
