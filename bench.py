@@ -102,16 +102,35 @@ def measured_traffic(config_name: str, avg_streams: float):
 
 def copy_probe(megabytes: int, reps: int) -> dict:
     """A plain device copy of known size (reads and writes `megabytes` MiB per
-    launch): the calibration run for the HBM byte counters."""
+    launch): the calibration run for the HBM byte counters, and the ceiling of
+    one launch that moves the same bytes as an attention launch.  The copies
+    cycle over enough buffer pairs (>= 1 GiB of sources) that the reads come
+    from HBM, not from the 256 MB last-level cache; each copy is timed with
+    HIP events on the launch stream."""
     import torch
 
     n = megabytes << 20
-    a = torch.ones(n // 2, dtype=torch.bfloat16, device="cuda:0")
-    b = torch.empty_like(a)
-    for _ in range(reps):
-        b.copy_(a)
+    pairs = max(2, -(-1024 // max(1, megabytes)))
+    src = [torch.ones(n // 2, dtype=torch.bfloat16, device="cuda:0") for _ in range(pairs)]
+    dst = [torch.empty_like(s) for s in src]
+    for i in range(pairs):  # warm
+        dst[i].copy_(src[i])
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
     torch.cuda.synchronize()
-    return {"copy_probe_bytes_read": n, "copy_probe_bytes_written": n, "launches": reps}
+    for r in range(reps):
+        ev[r][0].record()
+        dst[r % pairs].copy_(src[r % pairs])
+        ev[r][1].record()
+    torch.cuda.synchronize()
+    us = 1000.0 * sum(a.elapsed_time(b) for a, b in ev) / reps
+    return {
+        "copy_probe_bytes_read": n,
+        "copy_probe_bytes_written": n,
+        "launches": reps,
+        "avg_us": round(us, 3),
+        "gbs": round(2 * n / (us * 1e-6) / 1e9, 1),
+        "frac_of_peak": round(2 * n / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+    }
 
 
 def cpu_baseline(shape, streams: int, budget_s: float, seed: int) -> dict:
@@ -171,6 +190,7 @@ def main() -> int:
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB", help="only run a device copy of MIB MiB (counter calibration)")
     ap.add_argument("--cpu-baseline-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-copy-ceiling", action="store_true", help="skip the same-bytes device copy timing")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -327,6 +347,19 @@ def main() -> int:
             "bytes_per_stream_layer": per_stream,
         }
         result["paged_attn_hbm_gbs"] = round(achieved, 1)
+        if not args.no_copy_ceiling:
+            # the same bytes moved by one plain device copy launch (half read,
+            # half written): what one launch of this size reaches on this GPU
+            launch_bytes = total_bytes / max(1, len(ev_batches) * Ly)
+            mib = max(1, int(round(launch_bytes / 2 / (1 << 20))))
+            cp = copy_probe(mib, 100)
+            result["roofline"]["copy_same_bytes"] = {
+                "bytes": 2 * cp["copy_probe_bytes_read"],
+                "avg_us": cp["avg_us"],
+                "gbs": cp["gbs"],
+                "frac": cp["frac_of_peak"],
+            }
+            log(f"same-bytes copy: {cp['avg_us']} us, {cp['gbs']} GB/s")
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
         try:
