@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define PK_ABI_VERSION 3
+#define PK_ABI_VERSION 4
 
 enum pk_dtype { PK_DTYPE_F32 = 0, PK_DTYPE_F16 = 1, PK_DTYPE_BF16 = 2 };
 
@@ -214,6 +214,69 @@ typedef struct pk_mask_args {
   uint8_t* pad_mask;
 } pk_mask_args;
 int pk_streaming_mask(const pk_mask_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * pk_conv_step -- one streaming step of the middle of the Conformer convolution
+ * module for a batch, with each stream's convolution cache read and written in
+ * place:  GLU of the pointwise-conv1 output, padded frames set to zero, causal
+ * depthwise convolution over [cache ; this step's frames], LayerNorm over the
+ * channels, SiLU.  Replaces, per layer:
+ *   parakeet/modules/convolution.py:152-158  (F.glu, masked_fill, depthwise_conv,
+ *       batch_norm -- a LayerNorm --, activation);
+ *   CausalConv1d.update_cache convolution.py:37-47 (cat of cache and frames; the
+ *       next cache is the last kernel-1 frames);
+ *   ModelCache.get_conv_cache / update_conv_cache parakeet/modules/cache.py:47-53;
+ *   the conv rows of the per-step batch gather / scatter
+ *       parakeet/engine/scheduler.py:157-168,193-201 (the cache is addressed
+ *       through `slots` instead of being copied in and out of a batch buffer).
+ * The two pointwise convolutions (kernel size 1) stay plain GEMMs.
+ *
+ * glu_in    : [batch][chunk][2*d_model] pointwise-conv1 output, frame-major, element
+ *             strides (stride_b, stride_t), channels contiguous; output channel c is
+ *             glu_in[..c] * sigmoid(glu_in[..d_model + c]).
+ * cache     : [num_slots][num_layers][kernel - 1][d_model] of `dtype`, contiguous;
+ *             row r of a stream-layer holds the frame kernel-1-r steps before the
+ *             step's first frame (all zeros for a fresh stream, cache.py:30-34).
+ *             Stream b uses slot slots[b] (slots NULL: slot b); the slots of one
+ *             call must be distinct.
+ * pad_mask  : uint8 [batch][chunk] (1 = padded frame), or NULL: then frame t of
+ *             stream b is padded when t >= lengths[b] (lengths NULL: length_scalar).
+ * dw_weight : [d_model][kernel] (Conv1d weight [d_model][1][kernel]); dw_bias
+ *             [d_model] or NULL; ln_weight, ln_bias [d_model]; ln_eps.
+ * out       : [batch][chunk][d_model], element strides (stride_b, stride_t).
+ * One dtype for every tensor; fp32 arithmetic; the frames written to the cache
+ * are the GLU outputs rounded to `dtype`, as the reference's cache holds them.
+ * kernel in {3, 5, 7, 9} (the reference models use 9, config.py:13); d_model a
+ * multiple of 8 (fp16/bf16) or 4 (fp32), at most 4096 (fp16/bf16) or 2048 (fp32).
+ */
+typedef struct pk_conv_args {
+  int32_t dtype;
+  int32_t device;
+  int32_t batch;
+  int32_t chunk;
+  int32_t d_model;
+  int32_t kernel;
+  const void* glu_in;
+  int64_t glu_in_stride_b;
+  int64_t glu_in_stride_t;
+  void* cache;
+  int32_t num_slots;
+  int32_t num_layers;
+  int32_t layer;
+  const int32_t* slots;
+  const uint8_t* pad_mask;
+  const int64_t* lengths;
+  int64_t length_scalar;
+  const void* dw_weight;
+  const void* dw_bias;
+  const void* ln_weight;
+  const void* ln_bias;
+  float ln_eps;
+  void* out;
+  int64_t out_stride_b;
+  int64_t out_stride_t;
+} pk_conv_args;
+int pk_conv_step(const pk_conv_args* args, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Host page pool: FIFO free-page queue and per-slot page rings.  Thread safe

@@ -65,9 +65,10 @@ def build(verbose: bool = False) -> Path:
     inc = [f"-I{INCLUDE}", f"-I{CSRC}"]
     objs: list[Path] = []
 
-    kern_obj = BUILD_DIR / "paged_kernels.o"
-    _run([HIPCC, *HIP_FLAGS, *inc, "-x", "hip", "-c", str(CSRC / "paged_kernels.hip"), "-o", str(kern_obj)], verbose)
-    objs.append(kern_obj)
+    for name in ("paged_kernels.hip", "conv_kernels.hip"):
+        obj = BUILD_DIR / (Path(name).stem + ".o")
+        _run([HIPCC, *HIP_FLAGS, *inc, "-x", "hip", "-c", str(CSRC / name), "-o", str(obj)], verbose)
+        objs.append(obj)
 
     for name in ("page_pool.cpp", "pk_common.cpp"):
         obj = BUILD_DIR / (Path(name).stem + ".o")

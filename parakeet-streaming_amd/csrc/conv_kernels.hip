@@ -1,0 +1,276 @@
+// gfx950 kernel of the Conformer convolution module's streaming step, with each
+// stream's convolution cache read and written in place
+// (parakeet/modules/convolution.py:37-47,150-158; parakeet/modules/cache.py:47-53).
+//
+//   conv_step_kernel  GLU -> padded frames zeroed -> causal depthwise conv over
+//                     [cache ; frames] -> LayerNorm over channels -> SiLU; the
+//                     next cache is written back in place
+//
+// One workgroup per stream.  Lane l of the workgroup owns the channels
+// [l*VEC, (l+1)*VEC) -- one 16-byte chunk, 8 fp16/bf16 or 4 fp32 channels -- so
+// every frame row (cache, GLU input, output) is read and written as whole
+// 16-byte lanes.  A lane keeps a window of `kernel` frames of its channels in
+// registers: the cache rows first, then each new frame's GLU output rounded to
+// the storage type (the value the reference's concatenated tensor holds).  After
+// the last frame the window holds exactly the next cache; each lane owns its
+// channels, so the rows go back to the cache with no ordering hazard and no
+// separate shift.
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "pk_common.h"
+#include "pk_device.h"
+
+namespace pk {
+
+template <typename ST>
+struct ConvK {
+  const ST* h;  // [B][T][2D] pointwise-conv1 output
+  int64_t h_sb, h_st;
+  ST* cache;  // [slots][layers][K-1][D]
+  int32_t num_slots, num_layers, layer;
+  const int32_t* slots;
+  const uint8_t* pad;  // [B][T], 1 = padded
+  const int64_t* lengths;
+  int64_t len_scalar;
+  const ST* w;     // [D][K]
+  const ST* bias;  // [D] or nullptr
+  const ST* lnw;   // [D]
+  const ST* lnb;   // [D]
+  float eps;
+  ST* out;  // [B][T][D]
+  int64_t o_sb, o_st;
+  int32_t T, D;
+};
+
+// x rounded to the storage type and back.
+template <typename ST>
+__device__ static inline float round_to(float x);
+template <>
+__device__ inline float round_to<float>(float x) {
+  return x;
+}
+template <>
+__device__ inline float round_to<_Float16>(float x) {
+  return (float)(_Float16)x;
+}
+template <>
+__device__ inline float round_to<bf16_t>(float x) {
+  return __uint_as_float(f32_to_bf16_bits(x) << 16);
+}
+
+// Sum over the workgroup's waves, in every thread.  Every thread of the
+// workgroup calls it the same number of times (the frame loop is uniform).
+__device__ static inline float block_sum(float v, float* red, int nw) {
+  v = group_sum<64>(v);
+  if (nw == 1) return v;
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[wave] = v;
+  __syncthreads();
+  float s = 0.f;
+  for (int i = 0; i < nw; ++i) s += red[i];
+  __syncthreads();  // `red` is rewritten by the next call
+  return s;
+}
+
+constexpr int kConvMaxWaves = 8;
+
+template <typename ST, int K>
+__global__ void __launch_bounds__(64 * kConvMaxWaves) conv_step_kernel(const ConvK<ST> p) {
+  constexpr int VEC = Tr<ST>::VEC;
+  constexpr int R = K - 1;  // cache rows
+  __shared__ float red[kConvMaxWaves];
+
+  const int b = blockIdx.x;
+  const int nw = blockDim.x >> 6;
+  const int nchunk = p.D / VEC;
+  const bool own = (int)threadIdx.x < nchunk;  // lanes past d_model hold no channels
+  const int c0 = min((int)threadIdx.x, nchunk - 1) * VEC;
+  const int slot = p.slots ? p.slots[b] : b;
+  // a slot outside the cache is a caller error the host wrapper rejects; the
+  // kernel leaves such a stream untouched rather than address outside the cache
+  if (slot < 0 || slot >= p.num_slots) return;  // workgroup-uniform
+  ST* const crow = p.cache + ((int64_t)slot * p.num_layers + p.layer) * R * p.D + c0;
+  const ST* const hb = p.h + b * p.h_sb + c0;
+  ST* const ob = p.out + b * p.o_sb + c0;
+
+  // depthwise taps of the lane's channels: the [VEC][K] block of the [D][K]
+  // weight is VEC*K contiguous elements, K chunks of VEC
+  float w[VEC][K];
+  {
+    const ST* wp = p.w + (int64_t)c0 * K;
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      float f[VEC];
+      Tr<ST>::unpack(ld16(wp + i * VEC), f);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) w[(i * VEC + e) / K][(i * VEC + e) % K] = f[e];
+    }
+  }
+  float bias[VEC], lw[VEC], lb[VEC];
+  if (p.bias) {
+    Tr<ST>::unpack(ld16(p.bias + c0), bias);
+  } else {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) bias[e] = 0.f;
+  }
+  Tr<ST>::unpack(ld16(p.lnw + c0), lw);
+  Tr<ST>::unpack(ld16(p.lnb + c0), lb);
+
+  // window rows 0..R-1: the cache (the R frames before this step's first)
+  float win[K][VEC];
+#pragma unroll
+  for (int r = 0; r < R; ++r) Tr<ST>::unpack(ld16(crow + (int64_t)r * p.D), win[r]);
+
+  const uint8_t* padb = p.pad ? p.pad + (int64_t)b * p.T : nullptr;
+  const int64_t len = p.lengths ? p.lengths[b] : p.len_scalar;
+  const float inv_d = 1.f / (float)p.D;
+
+  for (int t = 0; t < p.T; ++t) {
+    // this frame's GLU output (convolution.py:152-155), zero where padded
+    float a[VEC], g[VEC];
+    Tr<ST>::unpack(ld16(hb + t * p.h_st), a);
+    Tr<ST>::unpack(ld16(hb + t * p.h_st + p.D), g);
+    const bool valid = padb ? padb[t] == 0 : (int64_t)t < len;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float v = a[e] / (1.f + __expf(-g[e]));
+      win[R][e] = valid ? round_to<ST>(v) : 0.f;
+    }
+    // causal depthwise conv: output t sees window rows 0..R = frames t..t+R of
+    // [cache ; frames] (convolution.py:43-46, Conv1d cross-correlation)
+    float y[VEC];
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      float acc = bias[e];
+#pragma unroll
+      for (int k = 0; k < K; ++k) acc = fmaf(w[e][k], win[k][e], acc);
+      y[e] = acc;
+      s += acc;
+    }
+    // LayerNorm over d_model (convolution.py:156), two-pass mean / variance
+    const float mean = block_sum(own ? s : 0.f, red, nw) * inv_d;
+    float q = 0.f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float d = y[e] - mean;
+      q = fmaf(d, d, q);
+    }
+    const float var = block_sum(own ? q : 0.f, red, nw) * inv_d;
+    const float rstd = rsqrtf(var + p.eps);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float z = (y[e] - mean) * rstd * lw[e] + lb[e];
+      y[e] = z / (1.f + __expf(-z));  // SiLU (convolution.py:157)
+    }
+    if (own) st16(ob + t * p.o_st, Tr<ST>::pack(y));
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) win[k][e] = win[k + 1][e];
+    }
+  }
+  // the window now holds the last R frames of [cache ; frames]: the next cache
+  // (convolution.py:46, next_cache = new_x[:, :, -(K-1):])
+  if (own) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) st16(crow + (int64_t)r * p.D, Tr<ST>::pack(win[r]));
+  }
+}
+
+namespace {
+
+template <typename ST, int K>
+int launch_conv(const ConvK<ST>& k, int batch, hipStream_t s) {
+  constexpr int VEC = Tr<ST>::VEC;
+  const int nchunk = k.D / VEC;
+  const int nw = (nchunk + 63) / 64;
+  hipLaunchKernelGGL((conv_step_kernel<ST, K>), dim3((unsigned)batch), dim3(64u * nw), 0, s, k);
+  return check_launch("pk_conv_step");
+}
+
+template <typename ST>
+int conv_typed(const pk_conv_args* a, hipStream_t s) {
+  constexpr int VEC = Tr<ST>::VEC;
+  const char* what = "pk_conv_step";
+  if (a->batch < 0 || a->chunk <= 0)
+    return fail(PK_ERR_INVALID, "%s: need batch >= 0 and chunk > 0", what);
+  if (a->d_model <= 0 || a->d_model % VEC != 0 || a->d_model > 64 * kConvMaxWaves * VEC)
+    return fail(PK_ERR_INVALID, "%s: d_model %d must be a positive multiple of %d, at most %d",
+                what, a->d_model, VEC, 64 * kConvMaxWaves * VEC);
+  if (a->num_slots <= 0 || a->num_layers <= 0 || a->layer < 0 || a->layer >= a->num_layers)
+    return fail(PK_ERR_INVALID, "%s: layer %d / layers %d / slots %d out of range", what,
+                a->layer, a->num_layers, a->num_slots);
+  if (!a->slots && a->batch > a->num_slots)
+    return fail(PK_ERR_INVALID, "%s: batch %d exceeds %d slots", what, a->batch, a->num_slots);
+  if (a->batch == 0) return PK_OK;
+  if (!a->glu_in || !a->cache || !a->dw_weight || !a->ln_weight || !a->ln_bias || !a->out)
+    return fail(PK_ERR_INVALID, "%s: a tensor pointer is NULL", what);
+  const void* ptrs[7] = {a->glu_in, a->cache, a->dw_weight, a->ln_weight, a->ln_bias, a->out,
+                         a->dw_bias ? a->dw_bias : a->ln_bias};
+  for (const void* q : ptrs)
+    if (!aligned16(q)) return fail(PK_ERR_INVALID, "%s: tensors must be 16-byte aligned", what);
+  const int64_t strides[4] = {a->glu_in_stride_b, a->glu_in_stride_t, a->out_stride_b,
+                              a->out_stride_t};
+  for (int64_t st : strides)
+    if (st < 0 || st % VEC != 0)
+      return fail(PK_ERR_INVALID, "%s: strides must be non-negative multiples of %d elements",
+                  what, VEC);
+  if (a->chunk > 1 && (a->glu_in_stride_t < 2 * (int64_t)a->d_model ||
+                       a->out_stride_t < (int64_t)a->d_model))
+    return fail(PK_ERR_INVALID, "%s: frame strides overlap a frame's channels", what);
+  if (!(a->ln_eps >= 0.f)) return fail(PK_ERR_INVALID, "%s: ln_eps must be >= 0", what);
+
+  ConvK<ST> k{};
+  k.h = static_cast<const ST*>(a->glu_in);
+  k.h_sb = a->glu_in_stride_b;
+  k.h_st = a->glu_in_stride_t;
+  k.cache = static_cast<ST*>(a->cache);
+  k.num_slots = a->num_slots;
+  k.num_layers = a->num_layers;
+  k.layer = a->layer;
+  k.slots = a->slots;
+  k.pad = a->pad_mask;
+  k.lengths = a->lengths;
+  k.len_scalar = a->length_scalar;
+  k.w = static_cast<const ST*>(a->dw_weight);
+  k.bias = static_cast<const ST*>(a->dw_bias);
+  k.lnw = static_cast<const ST*>(a->ln_weight);
+  k.lnb = static_cast<const ST*>(a->ln_bias);
+  k.eps = a->ln_eps;
+  k.out = static_cast<ST*>(a->out);
+  k.o_sb = a->out_stride_b;
+  k.o_st = a->out_stride_t;
+  k.T = a->chunk;
+  k.D = a->d_model;
+  if (a->kernel != 3 && a->kernel != 5 && a->kernel != 7 && a->kernel != 9)
+    return fail(PK_ERR_UNSUPPORTED, "%s: kernel size %d not built (3, 5, 7, 9)", what, a->kernel);
+  DeviceGuard dg(a->device);
+  if (!dg.ok) return fail(PK_ERR_HIP, "%s: cannot select device %d", what, a->device);
+  switch (a->kernel) {
+    case 3: return launch_conv<ST, 3>(k, a->batch, s);
+    case 5: return launch_conv<ST, 5>(k, a->batch, s);
+    case 7: return launch_conv<ST, 7>(k, a->batch, s);
+    case 9: return launch_conv<ST, 9>(k, a->batch, s);
+    default:
+      return fail(PK_ERR_UNSUPPORTED, "%s: kernel size %d not built (3, 5, 7, 9)", what, a->kernel);
+  }
+}
+
+}  // namespace
+}  // namespace pk
+
+extern "C" int pk_conv_step(const pk_conv_args* a, void* stream) {
+  pk::clear_error();
+  if (!a) return pk::fail(PK_ERR_INVALID, "pk_conv_step: args is NULL");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (a->dtype) {
+    case PK_DTYPE_F32: return pk::conv_typed<float>(a, s);
+    case PK_DTYPE_F16: return pk::conv_typed<_Float16>(a, s);
+    case PK_DTYPE_BF16: return pk::conv_typed<pk::bf16_t>(a, s);
+    default: return pk::fail(PK_ERR_INVALID, "pk_conv_step: unknown dtype %d", a->dtype);
+  }
+}

@@ -15,7 +15,7 @@ from pathlib import Path
 LIB_NAME = "libparakeet_paged.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -139,12 +139,43 @@ class MaskArgs(ctypes.Structure):
     ]
 
 
+class ConvArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", c_int32),
+        ("device", c_int32),
+        ("batch", c_int32),
+        ("chunk", c_int32),
+        ("d_model", c_int32),
+        ("kernel", c_int32),
+        ("glu_in", c_void_p),
+        ("glu_in_stride_b", c_int64),
+        ("glu_in_stride_t", c_int64),
+        ("cache", c_void_p),
+        ("num_slots", c_int32),
+        ("num_layers", c_int32),
+        ("layer", c_int32),
+        ("slots", c_void_p),
+        ("pad_mask", c_void_p),
+        ("lengths", c_void_p),
+        ("length_scalar", c_int64),
+        ("dw_weight", c_void_p),
+        ("dw_bias", c_void_p),
+        ("ln_weight", c_void_p),
+        ("ln_bias", c_void_p),
+        ("ln_eps", ctypes.c_float),
+        ("out", c_void_p),
+        ("out_stride_b", c_int64),
+        ("out_stride_t", c_int64),
+    ]
+
+
 # name -> (restype, argtypes); exactly the functions include/parakeet_paged.h declares
 SIGNATURES = {
     "pk_kv_append": (c_int, [POINTER(KvAppendArgs), c_void_p]),
     "pk_kv_gather": (c_int, [POINTER(KvGatherArgs), c_void_p]),
     "pk_paged_relpos_attn": (c_int, [POINTER(AttnArgs), c_void_p]),
     "pk_streaming_mask": (c_int, [POINTER(MaskArgs), c_void_p]),
+    "pk_conv_step": (c_int, [POINTER(ConvArgs), c_void_p]),
     "pk_pool_create": (
         c_int,
         [c_int32, c_int32, c_int32, c_int32, c_int32, POINTER(c_int32), POINTER(c_void_p)],

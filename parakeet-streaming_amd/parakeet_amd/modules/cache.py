@@ -105,7 +105,12 @@ class ModelCache:
             (self.num_layers, self.pool.num_pages, self.page_size, self.embed_dim), device=device, dtype=dtype
         )
         self.v_pages = torch.empty_like(self.k_pages)
-        self.conv = torch.zeros((batch_size, self.num_layers, self.embed_dim, self.conv_cache_len), device=device, dtype=dtype)
+        # conv state per slot, frame-major: row r of [slot, layer] is column r of
+        # the reference's [D, kernel-1] cache (cache.py:30-34), so a frame's
+        # channels are contiguous for the fused conv step
+        self.conv_frames = torch.zeros(
+            (batch_size, self.num_layers, self.conv_cache_len, self.embed_dim), device=device, dtype=dtype
+        )
         self._base = self
         self._staging = None
         self._set_slots(np.arange(batch_size, dtype=np.int32))
@@ -117,6 +122,7 @@ class ModelCache:
         self._prefix = bool(n == 0 or np.array_equal(self._slots, np.arange(n, dtype=np.int32)))
         dev = self._base.k_pages.device
         self._slot_index = None if self._prefix else torch.as_tensor(self._slots, dtype=torch.long).to(dev)
+        self._slots_i32 = torch.as_tensor(self._slots, dtype=torch.int32).to(dev)
         self._rows = torch.zeros((n, 1 + self.max_pages), dtype=torch.int32, device=dev)
         self._seen: set[int] = set()
         self._step_open = False
@@ -138,7 +144,7 @@ class ModelCache:
             "max_pages",
             "k_pages",
             "v_pages",
-            "conv",
+            "conv_frames",
         ):
             setattr(view, name, getattr(base, name))
         view._base = base
@@ -258,24 +264,70 @@ class ModelCache:
         return ops.kv_gather(self.paged(), layer_idx, self.batch_size, self.attn_cache_len, self.chunk)
 
     # ------------------------------------------------------------------- conv
+    @property
+    def conv(self) -> Tensor:
+        """All slots' conv state in the reference's [N, Ly, D, kernel-1] layout
+        (parakeet/modules/cache.py:30-34), as a view."""
+        return self.conv_frames.transpose(2, 3)
+
     def get_conv_cache(self, layer_idx: int) -> Tensor:
+        """[B, D, kernel-1] conv state of this batch (cache.py:47-48)."""
         if self._prefix:
-            return self.conv[: self.batch_size, layer_idx]
-        return self.conv[self._slot_index, layer_idx]
+            return self.conv_frames[: self.batch_size, layer_idx].transpose(1, 2)
+        return self.conv_frames[self._slot_index, layer_idx].transpose(1, 2)
 
     def update_conv_cache(self, layer_idx: int, state: Tensor) -> None:
+        """Stores a [B, D, kernel-1] conv state (cache.py:50-53); None is a no-op,
+        which is what the fused step returns after updating the cache in place."""
         if state is None:
             return
+        frames = state.transpose(1, 2)
         if self._prefix:
-            self.conv[: self.batch_size, layer_idx].copy_(state)
+            self.conv_frames[: self.batch_size, layer_idx].copy_(frames)
         else:
-            self.conv[self._slot_index, layer_idx] = state
+            self.conv_frames[self._slot_index, layer_idx] = frames.to(self.conv_frames.dtype)
+
+    def conv_ref(self, layer_idx: int) -> "ConvCacheRef":
+        """Handle that makes ConformerConvolution.forward update this batch's conv
+        state in place (the fused step) instead of returning a new state."""
+        if not 0 <= layer_idx < self.num_layers:
+            raise IndexError(f"layer {layer_idx} out of range [0, {self.num_layers})")
+        return ConvCacheRef(self, int(layer_idx))
+
+    def conv_step(
+        self,
+        layer_idx: int,
+        glu_in: Tensor,
+        pad_mask: Tensor | None,
+        dw_weight: Tensor,
+        dw_bias: Tensor | None,
+        ln_weight: Tensor,
+        ln_bias: Tensor,
+        eps: float,
+    ) -> Tensor:
+        """GLU -> pad mask -> causal depthwise conv over [state ; frames] ->
+        LayerNorm -> SiLU for this batch, the state of each stream's slot updated
+        in place (convolution.py:37-47,152-157 with cache.py:47-53)."""
+        if glu_in.shape[0] != self.batch_size:
+            raise ValueError(f"batch {glu_in.shape[0]} != cache rows {self.batch_size}")
+        return ops.conv_step(
+            glu_in,
+            self.conv_frames,
+            dw_weight,
+            ln_weight,
+            ln_bias,
+            layer=layer_idx,
+            slots=None if self._prefix else self._slots_i32,
+            pad_mask=pad_mask,
+            dw_bias=dw_bias,
+            eps=eps,
+        )
 
     # ------------------------------------------------------------------ reset
     def reset(self) -> None:
         """All slots empty (parakeet/modules/cache.py:55-58)."""
         self.pool.reset_all()
-        self.conv.zero_()
+        self.conv_frames.zero_()
         self._step_open = False
         self._seen = set()
 
@@ -284,7 +336,15 @@ class ModelCache:
         as zeros again (parakeet/modules/cache.py:60-63)."""
         pool_slot = int(self._slots[slot])
         self.pool.reset_slot(pool_slot)
-        self.conv[pool_slot].zero_()
+        self.conv_frames[pool_slot].zero_()
+
+
+@dataclass
+class ConvCacheRef:
+    """One layer of a batch's conv state, updated in place by the fused step."""
+
+    cache: ModelCache
+    layer_idx: int
 
 
 @dataclass
@@ -301,4 +361,4 @@ class StreamingState:
         return int(self.cache_lengths)
 
 
-__all__ = ["ModelCache", "StreamingState"]
+__all__ = ["ConvCacheRef", "ModelCache", "StreamingState"]

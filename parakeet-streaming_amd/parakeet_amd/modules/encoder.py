@@ -9,8 +9,10 @@
 * ``forward`` keeps the layer loop and the state advance (encoder.py:229-267);
   the attention of every layer runs on the paged cache.
 
-The feed-forward, layer-norm and convolution blocks are plain torch modules with
-the reference's parameter names (encoder.py:11-81, convolution.py:8-52,107-162,
+The convolution module's GLU / depthwise conv / LayerNorm / SiLU runs as one HIP
+launch with each stream's conv state updated in place (convolution.py:107-162,
+cache.py:47-53); the feed-forward blocks, layer norms and pointwise projections
+are torch modules with the reference's parameter names (encoder.py:11-81,
 feedforward.py:4-26); the convolution subsampling front end (``pre_encode``) is
 not part of this package.
 """
@@ -23,7 +25,7 @@ from torch.nn import functional as F
 
 from .. import ops
 from .attention import ConformerAttention, PositionalEncoding
-from .cache import ModelCache, StreamingState
+from .cache import ConvCacheRef, ModelCache, StreamingState
 
 
 class ConformerFeedForward(nn.Module):
@@ -43,23 +45,24 @@ class ConformerFeedForward(nn.Module):
 
 class CausalConv1d(nn.Conv1d):
     """Depthwise conv whose left context comes from a per-stream cache of
-    kernel_size-1 frames (parakeet/modules/convolution.py:8-52)."""
+    kernel_size-1 frames (parakeet/modules/convolution.py:8-52); holds the
+    parameters, the step itself runs in ConformerConvolution."""
 
     def __init__(self, in_channels, out_channels, kernel_size, stride=1, padding=(0, 0), dilation=1, groups=1, bias=True):
         self._left_padding = padding[0]
         self._right_padding = padding[1]
         super().__init__(in_channels, out_channels, kernel_size, stride=stride, padding=0, dilation=dilation, groups=groups, bias=bias)
 
-    def forward(self, x: Tensor, cache: Tensor | None = None):
-        B, C, _ = x.shape
-        if cache is None:
-            cache = torch.zeros(B, C, self.kernel_size[0] - 1, device=x.device, dtype=x.dtype)
-        x = torch.cat([cache, F.pad(x, pad=(0, self._right_padding))], dim=-1)
-        next_cache = x[:, :, -cache.size(-1) :]
-        return super().forward(x), next_cache
-
 
 class ConformerConvolution(nn.Module):
+    """pointwise conv -> [GLU -> pad mask -> causal depthwise conv with the
+    stream's cache -> LayerNorm -> SiLU] -> pointwise conv
+    (parakeet/modules/convolution.py:107-162).  The bracket is one HIP launch
+    (``pk_conv_step``); the pointwise convolutions (kernel size 1) are matrix
+    products.  ``cache`` is the reference's [B, D, kernel-1] state (a new state is
+    returned), None (zeros), or a ``ConvCacheRef`` from ``ModelCache.conv_ref``
+    (the batch's state is updated in place and None is returned)."""
+
     def __init__(self, hidden_size, kernel_size, use_bias=False):
         super().__init__()
         self.d_model = hidden_size
@@ -72,13 +75,37 @@ class ConformerConvolution(nn.Module):
         self.activation = nn.SiLU()
         self.pointwise_conv2 = nn.Conv1d(hidden_size, hidden_size, kernel_size=1, bias=use_bias)
 
-    def forward(self, x: Tensor, pad_mask: Tensor, cache: Tensor | None = None):
-        x = F.glu(self.pointwise_conv1(x.transpose(1, 2)), dim=1)
-        x = x.masked_fill(pad_mask.unsqueeze(1), 0.0)
-        x, cache = self.depthwise_conv(x, cache=cache)
-        x = self.batch_norm(x.transpose(1, 2)).transpose(1, 2)
-        x = self.pointwise_conv2(self.activation(x))
-        return x.transpose(1, 2), cache
+    def _middle(self, h: Tensor, pad_mask: Tensor | None, frames: Tensor, layer: int = 0, slots=None) -> Tensor:
+        dw = self.depthwise_conv
+        return ops.conv_step(
+            h,
+            frames,
+            dw.weight,
+            self.batch_norm.weight,
+            self.batch_norm.bias,
+            layer=layer,
+            slots=slots,
+            pad_mask=pad_mask,
+            dw_bias=dw.bias,
+            eps=self.batch_norm.eps,
+        )
+
+    def forward(self, x: Tensor, pad_mask: Tensor, cache=None):
+        h = F.linear(x, self.pointwise_conv1.weight.squeeze(-1), self.pointwise_conv1.bias)
+        if isinstance(cache, ConvCacheRef):
+            bn, dw = self.batch_norm, self.depthwise_conv
+            y = cache.cache.conv_step(cache.layer_idx, h, pad_mask, dw.weight, dw.bias, bn.weight, bn.bias, bn.eps)
+            new_cache = None
+        else:
+            B, K = x.shape[0], self.kernel_size
+            if cache is None:
+                frames = torch.zeros((B, 1, K - 1, self.d_model), dtype=x.dtype, device=x.device)
+            else:
+                frames = cache.transpose(1, 2).unsqueeze(1).contiguous()
+            y = self._middle(h, pad_mask, frames)
+            new_cache = frames[:, 0].transpose(1, 2)
+        out = F.linear(y, self.pointwise_conv2.weight.squeeze(-1), self.pointwise_conv2.bias)
+        return out, new_cache
 
 
 class ConformerLayer(nn.Module):
@@ -102,9 +129,7 @@ class ConformerLayer(nn.Module):
         residual = x
         residual = residual + 0.5 * self.feed_forward1(self.norm_feed_forward1(residual))
         residual = residual + self.self_attn(self.norm_self_att(residual), pos_emb, attn_mask=attn_mask, cache=cache)
-        conv_out, conv_cache = self.conv(
-            self.norm_conv(residual), pad_mask=pad_mask, cache=cache.get_conv_cache(self.layer_idx)
-        )
+        conv_out, conv_cache = self.conv(self.norm_conv(residual), pad_mask=pad_mask, cache=cache.conv_ref(self.layer_idx))
         cache.update_conv_cache(self.layer_idx, conv_cache)
         residual = residual + conv_out
         residual = residual + 0.5 * self.feed_forward2(self.norm_feed_forward2(residual))

@@ -13,7 +13,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from ._lib import AttnArgs, KvAppendArgs, KvGatherArgs, MaskArgs, PagedLayout, check, lib
+from ._lib import AttnArgs, ConvArgs, KvAppendArgs, KvGatherArgs, MaskArgs, PagedLayout, check, lib
 
 _DTYPES = {
     torch.float32: _lib.DTYPE_F32,
@@ -324,3 +324,88 @@ def streaming_mask(
     a.pad_mask = pad.data_ptr()
     check(lib().pk_streaming_mask(ctypes.byref(a), _stream(dev)), "pk_streaming_mask")
     return pad, att
+
+
+def conv_step(
+    glu_in: torch.Tensor,
+    cache: torch.Tensor,
+    dw_weight: torch.Tensor,
+    ln_weight: torch.Tensor,
+    ln_bias: torch.Tensor,
+    *,
+    layer: int = 0,
+    slots: torch.Tensor | None = None,
+    pad_mask: torch.Tensor | None = None,
+    lengths: torch.Tensor | int | None = None,
+    dw_bias: torch.Tensor | None = None,
+    eps: float = 1e-5,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """One streaming step of the convolution module's middle for a batch:
+    SiLU(LayerNorm(depthwise_conv([cache ; mask(GLU(glu_in))]))), with each
+    stream's cache updated in place (parakeet/modules/convolution.py:37-47,
+    152-157; parakeet/modules/cache.py:47-53).  Returns [B, T, D].
+
+    glu_in: [B, T, 2D] pointwise-conv1 output (channels last, unit inner stride);
+    cache: [num_slots, num_layers, K-1, D] contiguous, stream b in slot
+    ``slots[b]`` (int32 [B] on the device, distinct values; None: slot b);
+    pad_mask: [B, T] bool/uint8 (True = padded) or None, then frames t >=
+    ``lengths`` (int64 [B] on the device, or one int; None: no padding) are padded;
+    dw_weight: [D, 1, K] or [D, K]; ln_weight/ln_bias: [D]; dw_bias: [D] or None."""
+    B, T, D2 = glu_in.shape
+    if D2 % 2:
+        raise ValueError(f"glu_in has {D2} channels; the GLU needs an even count")
+    D = D2 // 2
+    dt = glu_in.dtype
+    if glu_in.stride(2) != 1:
+        raise ValueError("glu_in: last dimension must be contiguous")
+    if cache.dim() != 4 or cache.shape[3] != D or cache.dtype != dt or not cache.is_contiguous():
+        raise ValueError(f"cache must be contiguous [slots, layers, K-1, {D}] of {dt}, got {tuple(cache.shape)} {cache.dtype}")
+    S, Ly, R, _ = (int(x) for x in cache.shape)
+    K = R + 1
+    w = dw_weight.reshape(dw_weight.shape[0], -1) if dw_weight.dim() == 3 else dw_weight
+    if tuple(w.shape) != (D, K) or w.dtype != dt or not w.is_contiguous():
+        raise ValueError(f"dw_weight must be contiguous [{D}, 1, {K}] or [{D}, {K}] of {dt}")
+    vecs = [("ln_weight", ln_weight), ("ln_bias", ln_bias)] + ([("dw_bias", dw_bias)] if dw_bias is not None else [])
+    for name, v in vecs:
+        if tuple(v.shape) != (D,) or v.dtype != dt or not v.is_contiguous():
+            raise ValueError(f"{name} must be contiguous [{D}] of {dt}")
+    tensors = [glu_in, cache, w, ln_weight, ln_bias] + ([dw_bias] if dw_bias is not None else [])
+    if slots is not None:
+        if slots.dtype != torch.int32 or tuple(slots.shape) != (B,) or not slots.is_contiguous():
+            raise ValueError(f"slots must be contiguous int32 [{B}]")
+        tensors.append(slots)
+    elif B > S:
+        raise ValueError(f"batch {B} exceeds {S} cache slots")
+    if not 0 <= int(layer) < Ly:
+        raise IndexError(f"layer {layer} out of range [0, {Ly})")
+    dev = _require_device(*tensors)
+    if out is None:
+        out = torch.empty((B, T, D), dtype=dt, device=dev)
+    _rows3(out, "out", B, T, D, dt)
+    a = ConvArgs()
+    a.dtype = dtype_code(dt)
+    a.device = dev.index if dev.index is not None else torch.cuda.current_device()
+    a.batch, a.chunk, a.d_model, a.kernel = B, T, D, K
+    a.glu_in, a.glu_in_stride_b, a.glu_in_stride_t = glu_in.data_ptr(), glu_in.stride(0), glu_in.stride(1)
+    a.cache, a.num_slots, a.num_layers, a.layer = cache.data_ptr(), S, Ly, int(layer)
+    a.slots = slots.data_ptr() if slots is not None else None
+    if pad_mask is not None:
+        if pad_mask.dtype not in (torch.bool, torch.uint8) or tuple(pad_mask.shape) != (B, T):
+            raise ValueError(f"pad_mask must be bool/uint8 [{B}, {T}]")
+        pad_mask = pad_mask.contiguous()
+        if pad_mask.device != dev:
+            raise ValueError("pad_mask on a different device")
+        a.pad_mask = pad_mask.data_ptr()
+    elif isinstance(lengths, torch.Tensor):
+        if lengths.dtype != torch.int64 or tuple(lengths.shape) != (B,) or not lengths.is_contiguous() or lengths.device != dev:
+            raise ValueError(f"lengths must be contiguous int64 [{B}] on {dev}")
+        a.lengths = lengths.data_ptr()
+    else:
+        a.length_scalar = T if lengths is None else int(lengths)
+    a.dw_weight = w.data_ptr()
+    a.dw_bias = dw_bias.data_ptr() if dw_bias is not None else None
+    a.ln_weight, a.ln_bias, a.ln_eps = ln_weight.data_ptr(), ln_bias.data_ptr(), float(eps)
+    a.out, a.out_stride_b, a.out_stride_t = out.data_ptr(), out.stride(0), out.stride(1)
+    check(lib().pk_conv_step(ctypes.byref(a), _stream(dev)), "pk_conv_step")
+    return out

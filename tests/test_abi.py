@@ -56,6 +56,7 @@ def test_every_declared_symbol_is_exported_and_bound():
         ("pk_kv_gather_args", _lib.KvGatherArgs),
         ("pk_attn_args", _lib.AttnArgs),
         ("pk_mask_args", _lib.MaskArgs),
+        ("pk_conv_args", _lib.ConvArgs),
     ],
 )
 def test_struct_layout_matches_header(cname, pyclass):
@@ -69,6 +70,7 @@ def test_null_args_rejected_without_gpu():
     assert lib.pk_kv_append(None, None) == _lib.PK_ERR_INVALID
     assert lib.pk_kv_gather(None, None) == _lib.PK_ERR_INVALID
     assert lib.pk_streaming_mask(None, None) == _lib.PK_ERR_INVALID
+    assert lib.pk_conv_step(None, None) == _lib.PK_ERR_INVALID
 
 
 def test_mask_args_validated_before_launch():
@@ -77,3 +79,20 @@ def test_mask_args_validated_before_launch():
     assert _lib.lib().pk_streaming_mask(ctypes.byref(a), None) == _lib.PK_ERR_INVALID
     a.chunk = 2
     assert _lib.lib().pk_streaming_mask(ctypes.byref(a), None) == _lib.PK_ERR_INVALID  # NULL state
+
+
+def test_conv_args_validated_before_launch():
+    L = _lib.lib()
+    a = _lib.ConvArgs()
+    a.dtype, a.batch, a.chunk, a.d_model, a.kernel = _lib.DTYPE_F16, 2, 2, 512, 9
+    a.num_slots, a.num_layers, a.layer = 4, 3, 0
+    assert L.pk_conv_step(ctypes.byref(a), None) == _lib.PK_ERR_INVALID  # NULL tensors
+    assert "NULL" in _lib.last_error()
+    a.d_model = 500  # not a multiple of 8 channels
+    assert L.pk_conv_step(ctypes.byref(a), None) == _lib.PK_ERR_INVALID
+    a.d_model, a.layer = 512, 3  # layer out of range
+    assert L.pk_conv_step(ctypes.byref(a), None) == _lib.PK_ERR_INVALID
+    a.layer, a.batch = 0, 5  # more streams than slots without a slot map
+    assert L.pk_conv_step(ctypes.byref(a), None) == _lib.PK_ERR_INVALID
+    a.batch, a.dtype = 0, 7
+    assert L.pk_conv_step(ctypes.byref(a), None) == _lib.PK_ERR_INVALID  # unknown dtype

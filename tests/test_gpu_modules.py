@@ -11,9 +11,10 @@ paged cache -- against the oracle:
   applied in float64; with a cache over several steps, and without a cache;
 * ConformerEncoder (parakeet/modules/encoder.py:140-267): streaming steps of a
   random-init 2-layer stack on the GPU against the same weights in float64 on
-  the CPU where every layer's attention is the oracle over a dense cache and
-  the masks are the oracle's loop (encoder.py:167-227); the state scalars
-  advance as encoder.py:257-260.
+  the CPU where every layer's attention is the oracle over a dense cache, every
+  layer's convolution step is the oracle's (convolution.py:150-158 with its
+  dense conv cache) and the masks are the oracle's loop (encoder.py:167-227);
+  the state scalars advance as encoder.py:257-260.
 """
 
 import copy
@@ -23,7 +24,10 @@ import numpy as np
 import pytest
 import torch
 
+import torch.nn.functional as F
+
 from oracle import attention as oa
+from oracle import conv as oc
 from oracle import masks as om
 from parakeet_amd.modules.attention import ConformerAttention, PositionalEncoding
 from parakeet_amd.modules.cache import ModelCache, StreamingState
@@ -161,6 +165,26 @@ class _DenseCache:
     def update_conv_cache(self, layer, state):
         self.conv[:, layer] = state
 
+    conv_ref = get_conv_cache  # the CPU reference's conv step takes the state tensor
+
+
+def _oracle_conv(conv):
+    """Replaces ConformerConvolution.forward on the CPU reference: the module's
+    pointwise projections around the oracle's streaming step over the dense
+    [B, D, K-1] conv cache."""
+
+    def forward(x, pad_mask, cache=None):
+        bn, dw = conv.batch_norm, conv.depthwise_conv
+        h = F.linear(x, conv.pointwise_conv1.weight.squeeze(-1)).numpy()
+        y, nxt = oc.conv_module_step(
+            h, cache.transpose(1, 2).numpy(), pad_mask.numpy(), dw.weight.detach().numpy().reshape(conv.d_model, -1),
+            None, bn.weight.detach().numpy(), bn.bias.detach().numpy(), bn.eps,
+        )
+        out = F.linear(torch.from_numpy(y), conv.pointwise_conv2.weight.squeeze(-1))
+        return out, torch.from_numpy(nxt).transpose(1, 2)
+
+    return forward
+
 
 def _oracle_attention(att, left, H):
     """Replaces ConformerAttention.forward on the CPU reference: the module's
@@ -201,6 +225,7 @@ def test_encoder_streaming_matches_dense_reference(cuda):
     dense = _DenseCache(B, Ly, left, right, D, K)
     for layer in ref.layers:
         layer.self_attn.forward = _oracle_attention(layer.self_attn, left, H)
+        layer.conv.forward = _oracle_conv(layer.conv)
     proc = np.zeros(B, dtype=np.int64)
     cl = np.zeros(B, dtype=np.int64)
 
