@@ -176,12 +176,133 @@ def cpu_baseline(shape, streams: int, budget_s: float, seed: int) -> dict:
     }
 
 
+def encoder_bench(args, device) -> int:
+    """``--config e2e``: the streaming FastConformer encoder step after the front
+    end -- a random-init small model (17 layers, d_model 512, 8 heads, feed-forward
+    x4, depthwise conv kernel 9, left context 70, 2 frames per step), fp16, 128
+    streams, all live.  Per step and layer: the torch projections and feed-forward
+    GEMMs, the fused paged attention (pk_paged_relpos_attn) and the fused conv step
+    with the per-stream conv cache in place (pk_conv_step); streaming masks from one
+    launch (pk_streaming_mask); the state advance (encoder.py:229-267).  Input:
+    seeded N(0,1) subsampled frames resident on the GPU (the log-mel + 8x
+    subsampling front end is not part of this step).  Also times the conv step
+    alone per launch on the same shape."""
+    import numpy as np
+    import torch
+
+    from parakeet_amd import ops
+    from parakeet_amd.modules.encoder import ConformerEncoder
+
+    B, D, H, Ly, K, left, right = 128, 512, 8, 17, 9, 70, 1
+    T = right + 1
+    dt = torch.float16
+    torch.manual_seed(4)
+    enc = ConformerEncoder(
+        feat_in=80, hidden_size=D, ff_expansion_factor=4, num_layers=Ly, num_heads=H, subsampling_factor=8,
+        pos_emb_max_len=5000, conv_kernel_size=K, att_context_size=[left, right], subsampling_conv_channels=256,
+        use_bias=False,
+    )
+    with torch.no_grad():
+        for layer in enc.layers:
+            layer.self_attn.pos_bias_u.normal_(0.0, 0.02)
+            layer.self_attn.pos_bias_v.normal_(0.0, 0.02)
+    enc = enc.to(dt).to(device).eval()
+    state = enc.init_streaming_state(batch_size=B, device=device, dtype=dt)
+    g = torch.Generator().manual_seed(5)
+    xs = [torch.randn(B, T, D, generator=g).to(dt).to(device) for _ in range(8)]
+    length = torch.full((B,), T, dtype=torch.int64, device=device)
+    gc.collect()
+    gc.freeze()
+    with torch.inference_mode():
+        for i in range(args.warmup + 36):  # past the 70-frame window
+            enc(xs[i % len(xs)], state, length=length)
+        torch.cuda.synchronize()
+        K_steps = args.steps
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        start.record()
+        for i in range(K_steps):
+            enc(xs[i % len(xs)], state, length=length)
+        stop.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        ms = start.elapsed_time(stop) / K_steps
+        log(f"timed {K_steps} encoder steps")
+        # the conv step alone on the same shape and cache: one launch per layer,
+        # recorded once in a HIP graph and replayed, so the host's launch cost
+        # stays out of the per-launch time
+        conv = enc.layers[0].conv
+        h = torch.randn(B, T, 2 * D, generator=g).to(dt).to(device)
+        frames = state.cache.conv_frames
+
+        def conv_all_layers():
+            for layer in range(Ly):
+                ops.conv_step(h, frames, conv.depthwise_conv.weight, conv.batch_norm.weight, conv.batch_norm.bias,
+                              layer=layer, eps=conv.batch_norm.eps)
+
+        side = torch.cuda.Stream(device)
+        side.wait_stream(torch.cuda.current_stream(device))
+        with torch.cuda.stream(side):
+            conv_all_layers()  # warm outside the capture
+        torch.cuda.current_stream(device).wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            conv_all_layers()
+        torch.cuda.synchronize()
+        reps = 20
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            graph.replay()
+        b.record()
+        torch.cuda.synchronize()
+        conv_us = 1000.0 * a.elapsed_time(b) / (reps * Ly)
+    s = 2
+    conv_bytes = B * s * (T * 2 * D + 2 * (K - 1) * D + T * D) + s * D * (K + 2)
+    result = {
+        "metric": "streaming encoder steps/sec (small FastConformer, 17 layers, after the front end) at 1 GPU",
+        "value": round(1000.0 / ms, 2),
+        "unit": "steps/s",
+        "n_gpus": 1,
+        "steps": K_steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (seeded N(0,1) subsampled frames, random-init weights, pos biases N(0,0.02))",
+        "config": {
+            "workload": "small FastConformer encoder step: 17 layers x (FF/2, paged rel-pos MHA, conv module with "
+            "per-stream cache, FF/2, LN), 128 streams all live, 2 frames per step",
+            "layers": Ly,
+            "d_model": D,
+            "heads": H,
+            "conv_kernel": K,
+            "left_context": left,
+            "frames_per_step": T,
+            "streams": B,
+            "parallelism": "single GPU",
+        },
+        "conv_step": {
+            "kernel": "conv_step_kernel (GLU, pad mask, causal depthwise conv with cache, LayerNorm, SiLU)",
+            "avg_kernel_us": round(conv_us, 3),
+            "bytes_per_launch": conv_bytes,
+            "gbs": round(conv_bytes / (conv_us * 1e-6) / 1e9, 1),
+            "frac_of_peak": round(conv_bytes / (conv_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        },
+        "wall_s": round(wall, 3),
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", choices=sorted(CONFIGS), default="large")
+    ap.add_argument("--config", choices=sorted(CONFIGS) + ["e2e"], default="large")
     ap.add_argument("--preroll", type=int, default=60, help="untimed steps before warmup to reach steady-state windows")
     ap.add_argument("--rows-per-lane", type=int, default=0)
     ap.add_argument("--no-kernel-events", action="store_true")
@@ -213,6 +334,8 @@ def main() -> int:
     if args.copy_probe:
         print(json.dumps(copy_probe(args.copy_probe, max(1, args.steps))), flush=True)
         return 0
+    if args.config == "e2e":
+        return encoder_bench(args, device)
     cfg = CONFIGS[args.config]
     log(f"config {args.config}: building workload")
     shape, runner, churn = build_runner(cfg, device, args.rows_per_lane)
