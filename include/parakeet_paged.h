@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define PK_ABI_VERSION 4
+#define PK_ABI_VERSION 5
 
 enum pk_dtype { PK_DTYPE_F32 = 0, PK_DTYPE_F16 = 1, PK_DTYPE_BF16 = 2 };
 
@@ -277,6 +277,148 @@ typedef struct pk_conv_args {
   int64_t out_stride_t;
 } pk_conv_args;
 int pk_conv_step(const pk_conv_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Pre-encode front end: pcm -> log-mel (pk_fe_step) -> 8x convolution
+ * subsampling (pk_subsample), batched over streams whose state lives in device
+ * rings addressed by slot.
+ *
+ * pk_fe_step -- store each stream's new samples in its sample ring and compute
+ * the log-mel features of frames [frame0, frame0 + n_frames) into its mel ring.
+ * Replaces, per stream and push:
+ *   FeatureExtractor.push / _trim_samples parakeet/modules/feature_extractor.py:97-151
+ *       (the host keeps the frame counters; the ring replaces the trimmed buffer);
+ *   FeatureExtractor._compute_features feature_extractor.py:63-88 (dither,
+ *       pre-emphasis, centred STFT with constant padding, power, Slaney mel, log);
+ *   the feature half of ModelRunner._run_pre_encode
+ *       parakeet/engine/model_runner.py:193-196 and the pcm16 -> float conversion of
+ *       parakeet/server.py:442.
+ * Frame f of a stream is computed from its global samples as the reference's
+ * centred STFT sees them: y[i] = xd[i] - preemph * xd[i-1] (xd[-1] = 0),
+ * xd[i] = x[i] + dither * N(i); y[i] = 0 for i < 0 or i >= samples pushed so
+ * far; frame f = y[f*hop - n_fft/2 + n] * w[n], the win_length window in the
+ * middle of n_fft.  N(i) is a standard normal from Philox4x32-10 with counter
+ * (i mod 2^32, i / 2^32, noise_id, 0) and key (seed mod 2^32, seed / 2^32),
+ * Box-Muller on the first two words (the reference draws torch.randn per push).
+ *
+ * streams     : device array [batch] of pk_fe_stream.  The host guarantees for
+ *               each stream that sample_base + n_new - (frame0*hop - n_fft/2 +
+ *               (n_fft - win)/2 - 1) <= ring_size (every sample a frame reads is
+ *               still in the ring and not overwritten by this call) and that
+ *               n_frames <= mel_ring_rows; slots of one call are distinct.
+ * samples     : new samples of stream b at samples + b*samples_stride, int16 pcm
+ *               (value / 32768) or float32, by pcm_dtype.
+ * sample_ring : float32 [num_slots][ring_size]; global sample i of a slot at
+ *               i mod ring_size.  mel_ring: float32 [num_slots][mel_ring_rows]
+ *               [n_mels]; frame f of a slot at row f mod mel_ring_rows.
+ * window      : float32 [win_length]; fb: float32 [n_mels][n_fft/2 + 1]; fb_range:
+ *               int32 [n_mels][2], the bins [first, end) where row m of fb is not 0.
+ * n_fft = 512; win_length <= n_fft; ring_size, mel_ring_rows powers of two;
+ * n_mels <= 128; max_new, max_frames bound n_new and n_frames over the batch
+ * (they size the grid).  Entries out of these bounds are skipped by the kernel.
+ */
+enum pk_pcm { PK_PCM_S16 = 0, PK_PCM_F32 = 1 };
+
+typedef struct pk_fe_stream {
+  int32_t slot;
+  int32_t n_new;
+  int64_t sample_base; /* samples pushed to the slot before this call */
+  int32_t frame0;
+  int32_t n_frames;
+  uint32_t noise_id;
+  int32_t reserved;
+} pk_fe_stream;
+
+typedef struct pk_fe_args {
+  int32_t device;
+  int32_t batch;
+  const pk_fe_stream* streams;
+  int32_t pcm_dtype;
+  const void* samples;
+  int64_t samples_stride;
+  float* sample_ring;
+  int32_t num_slots;
+  int32_t ring_size;
+  float* mel_ring;
+  int32_t mel_ring_rows;
+  int32_t n_mels;
+  const float* window;
+  int32_t win_length;
+  int32_t n_fft;
+  int32_t hop;
+  const float* fb;
+  const int32_t* fb_range;
+  float preemph;
+  float dither;
+  uint64_t seed;
+  float log_guard;
+  int32_t max_new;
+  int32_t max_frames;
+} pk_fe_args;
+int pk_fe_step(const pk_fe_args* args, void* stream);
+
+/* pk_subsample -- ConvSubsampling's convolution stack for a batch of feature
+ * windows: CausalConv2D(1 -> C, 3x3, stride 2) + ReLU, then twice
+ * [depthwise CausalConv2D(3x3, stride 2), pointwise 1x1 C -> C, ReLU], with the
+ * time masks of MaskedConvSequential, flattened per output frame as
+ * [channel][freq] (the input of ConvSubsampling.out).  Replaces
+ *   ConvSubsampling.forward / conv_forward parakeet/modules/subsample.py:140-152,177-179
+ *       up to `out` (which stays a plain GEMM);
+ *   MaskedConvSequential.forward subsample.py:30-57;
+ *   CausalConv2D.forward parakeet/modules/convolution.py:94-104;
+ *   the window assembly and drop of ModelRunner._run_pre_encode
+ *       parakeet/engine/model_runner.py:198-234 (the window is read in place from
+ *       the mel ring; the cache is the ring's previous rows).
+ * Stream b's window is feature rows row0 .. row0 + rows - 1 of block `slot`
+ * (taken mod feat_rows when feat_ring is set); rows >= length are masked; output
+ * frames drop .. drop + n_out - 1 of the stack go to rows out_row .. of `out`.
+ *
+ * feats : float32 [feat_slots][feat_rows][n_mels] (the mel ring, or plain
+ *         features); values are rounded to `dtype` on entry.
+ * w0,b0 : conv.0 [C][1][3][3], [C];  w2,b2 / w5,b5: depthwise [C][1][3][3], [C];
+ * w3,b3 / w6,b6: pointwise [C][C][1][1], [C].  Biases may be NULL.  All of `dtype`.
+ * out   : [out_rows][C * F3] of `dtype`, F3 = the frequency size after three
+ *         stride-2 convolutions (n_mels -> n_mels/2 + 1, three times).
+ * C in {64, 128, 256}; n_mels <= 128; fp32 accumulation, each layer's output
+ * rounded to `dtype` as the reference's tensors hold them.
+ */
+typedef struct pk_sub_stream {
+  int32_t slot;
+  int32_t row0;
+  int32_t rows;
+  int32_t length;
+  int32_t drop;
+  int32_t n_out;
+  int32_t out_row;
+  int32_t reserved;
+} pk_sub_stream;
+
+typedef struct pk_sub_args {
+  int32_t dtype;
+  int32_t device;
+  int32_t batch;
+  const pk_sub_stream* streams;
+  const float* feats;
+  int32_t feat_slots;
+  int32_t feat_rows;
+  int32_t feat_ring;
+  int32_t n_mels;
+  int32_t channels;
+  const void* w0;
+  const void* b0;
+  const void* w2;
+  const void* b2;
+  const void* w3;
+  const void* b3;
+  const void* w5;
+  const void* b5;
+  const void* w6;
+  const void* b6;
+  void* out;
+  int32_t out_rows;
+  int32_t max_out;
+} pk_sub_args;
+int pk_subsample(const pk_sub_args* args, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Host page pool: FIFO free-page queue and per-slot page rings.  Thread safe

@@ -45,22 +45,6 @@ struct ConvK {
   int32_t T, D;
 };
 
-// x rounded to the storage type and back.
-template <typename ST>
-__device__ static inline float round_to(float x);
-template <>
-__device__ inline float round_to<float>(float x) {
-  return x;
-}
-template <>
-__device__ inline float round_to<_Float16>(float x) {
-  return (float)(_Float16)x;
-}
-template <>
-__device__ inline float round_to<bf16_t>(float x) {
-  return __uint_as_float(f32_to_bf16_bits(x) << 16);
-}
-
 // Sum over the workgroup's waves, in every thread.  Every thread of the
 // workgroup calls it the same number of times (the frame loop is uniform).
 __device__ static inline float block_sum(float v, float* red, int nw) {

@@ -393,7 +393,6 @@ __global__ void __launch_bounds__(64) relpos_attn_kernel(const AttnK<ST> p) {
 // fused append + paged relative-position attention on the matrix cores
 // (fp16 / bf16)
 
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 
 // 16-bit operand type of the matrix-core path, with the two MFMA shapes used:

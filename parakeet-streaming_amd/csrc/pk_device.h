@@ -13,6 +13,7 @@ namespace pk {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------------------
 // element traits: 16-byte chunk <-> fp32 registers
@@ -103,6 +104,41 @@ struct Tr<bf16_t> {
     return v;
   }
 };
+
+// x rounded to the storage type and back.
+template <typename ST>
+__device__ static inline float round_to(float x);
+template <>
+__device__ inline float round_to<float>(float x) {
+  return x;
+}
+template <>
+__device__ inline float round_to<_Float16>(float x) {
+  return (float)(_Float16)x;
+}
+template <>
+__device__ inline float round_to<bf16_t>(float x) {
+  return __uint_as_float(f32_to_bf16_bits(x) << 16);
+}
+
+// one element: fp32 <-> storage type
+template <typename ST>
+__device__ static inline ST to_st(float x);
+template <>
+__device__ inline float to_st<float>(float x) {
+  return x;
+}
+template <>
+__device__ inline _Float16 to_st<_Float16>(float x) {
+  return (_Float16)x;
+}
+template <>
+__device__ inline bf16_t to_st<bf16_t>(float x) {
+  return bf16_t{(uint16_t)f32_to_bf16_bits(x)};
+}
+__device__ static inline float from_st(float v) { return v; }
+__device__ static inline float from_st(_Float16 v) { return (float)v; }
+__device__ static inline float from_st(bf16_t v) { return __uint_as_float((uint32_t)v.bits << 16); }
 
 template <typename ST>
 __device__ static inline u32x4 ld16(const ST* p) {

@@ -15,7 +15,7 @@ from pathlib import Path
 LIB_NAME = "libparakeet_paged.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -27,6 +27,9 @@ PK_ERR_UNSUPPORTED = -2
 PK_ERR_EXHAUSTED = -3
 PK_ERR_HIP = -4
 PK_ERR_STATE = -5
+
+PCM_S16 = 0
+PCM_F32 = 1
 
 
 class PagedLayout(ctypes.Structure):
@@ -169,6 +172,88 @@ class ConvArgs(ctypes.Structure):
     ]
 
 
+class FeStream(ctypes.Structure):
+    _fields_ = [
+        ("slot", c_int32),
+        ("n_new", c_int32),
+        ("sample_base", c_int64),
+        ("frame0", c_int32),
+        ("n_frames", c_int32),
+        ("noise_id", ctypes.c_uint32),
+        ("reserved", c_int32),
+    ]
+
+
+class FeArgs(ctypes.Structure):
+    _fields_ = [
+        ("device", c_int32),
+        ("batch", c_int32),
+        ("streams", c_void_p),
+        ("pcm_dtype", c_int32),
+        ("samples", c_void_p),
+        ("samples_stride", c_int64),
+        ("sample_ring", c_void_p),
+        ("num_slots", c_int32),
+        ("ring_size", c_int32),
+        ("mel_ring", c_void_p),
+        ("mel_ring_rows", c_int32),
+        ("n_mels", c_int32),
+        ("window", c_void_p),
+        ("win_length", c_int32),
+        ("n_fft", c_int32),
+        ("hop", c_int32),
+        ("fb", c_void_p),
+        ("fb_range", c_void_p),
+        ("preemph", ctypes.c_float),
+        ("dither", ctypes.c_float),
+        ("seed", ctypes.c_uint64),
+        ("log_guard", ctypes.c_float),
+        ("max_new", c_int32),
+        ("max_frames", c_int32),
+    ]
+
+
+class SubStream(ctypes.Structure):
+    _fields_ = [
+        ("slot", c_int32),
+        ("row0", c_int32),
+        ("rows", c_int32),
+        ("length", c_int32),
+        ("drop", c_int32),
+        ("n_out", c_int32),
+        ("out_row", c_int32),
+        ("reserved", c_int32),
+    ]
+
+
+class SubArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", c_int32),
+        ("device", c_int32),
+        ("batch", c_int32),
+        ("streams", c_void_p),
+        ("feats", c_void_p),
+        ("feat_slots", c_int32),
+        ("feat_rows", c_int32),
+        ("feat_ring", c_int32),
+        ("n_mels", c_int32),
+        ("channels", c_int32),
+        ("w0", c_void_p),
+        ("b0", c_void_p),
+        ("w2", c_void_p),
+        ("b2", c_void_p),
+        ("w3", c_void_p),
+        ("b3", c_void_p),
+        ("w5", c_void_p),
+        ("b5", c_void_p),
+        ("w6", c_void_p),
+        ("b6", c_void_p),
+        ("out", c_void_p),
+        ("out_rows", c_int32),
+        ("max_out", c_int32),
+    ]
+
+
 # name -> (restype, argtypes); exactly the functions include/parakeet_paged.h declares
 SIGNATURES = {
     "pk_kv_append": (c_int, [POINTER(KvAppendArgs), c_void_p]),
@@ -176,6 +261,8 @@ SIGNATURES = {
     "pk_paged_relpos_attn": (c_int, [POINTER(AttnArgs), c_void_p]),
     "pk_streaming_mask": (c_int, [POINTER(MaskArgs), c_void_p]),
     "pk_conv_step": (c_int, [POINTER(ConvArgs), c_void_p]),
+    "pk_fe_step": (c_int, [POINTER(FeArgs), c_void_p]),
+    "pk_subsample": (c_int, [POINTER(SubArgs), c_void_p]),
     "pk_pool_create": (
         c_int,
         [c_int32, c_int32, c_int32, c_int32, c_int32, POINTER(c_int32), POINTER(c_void_p)],

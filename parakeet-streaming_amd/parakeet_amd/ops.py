@@ -13,7 +13,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from ._lib import AttnArgs, ConvArgs, KvAppendArgs, KvGatherArgs, MaskArgs, PagedLayout, check, lib
+from ._lib import AttnArgs, ConvArgs, FeArgs, KvAppendArgs, KvGatherArgs, MaskArgs, PagedLayout, SubArgs, check, lib
 
 _DTYPES = {
     torch.float32: _lib.DTYPE_F32,
@@ -408,4 +408,146 @@ def conv_step(
     a.ln_weight, a.ln_bias, a.ln_eps = ln_weight.data_ptr(), ln_bias.data_ptr(), float(eps)
     a.out, a.out_stride_b, a.out_stride_t = out.data_ptr(), out.stride(0), out.stride(1)
     check(lib().pk_conv_step(ctypes.byref(a), _stream(dev)), "pk_conv_step")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# pre-encode front end
+
+
+@dataclass
+class FeTables:
+    """Device constants of one feature extractor (feature_extractor.py:11-57):
+    the Hann window, the Slaney filterbank [n_mels, n_fft/2+1] and, per mel
+    band, the bin range where its weights are not zero."""
+
+    window: torch.Tensor  # float32 [win_length]
+    fb: torch.Tensor  # float32 [n_mels, n_fft//2 + 1]
+    fb_range: torch.Tensor  # int32 [n_mels, 2]
+    n_fft: int
+    hop: int
+    preemph: float
+    log_guard: float
+
+    @property
+    def n_mels(self) -> int:
+        return int(self.fb.shape[0])
+
+
+def _check_f32(t: torch.Tensor, name: str, dim: int) -> None:
+    if t.dtype != torch.float32 or t.dim() != dim or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous float32 tensor with {dim} dimensions")
+
+
+def fe_step(
+    streams: torch.Tensor,
+    batch: int,
+    samples: torch.Tensor | None,
+    sample_ring: torch.Tensor,
+    mel_ring: torch.Tensor,
+    tables: FeTables,
+    *,
+    dither: float,
+    seed: int,
+    max_new: int,
+    max_frames: int,
+) -> None:
+    """Stores new samples and writes the log-mel frames of ``batch`` streams
+    (pk_fe_step; feature_extractor.py:63-151).  ``streams``: device bytes
+    holding ``batch`` pk_fe_stream records; ``samples``: [batch, >= max_new]
+    int16 pcm or float32 (None when max_new == 0); rings: float32 [S, R] and
+    [S, M, n_mels]."""
+    _check_f32(sample_ring, "sample_ring", 2)
+    _check_f32(mel_ring, "mel_ring", 3)
+    S, R = (int(x) for x in sample_ring.shape)
+    if mel_ring.shape[0] != S or mel_ring.shape[2] != tables.n_mels:
+        raise ValueError(f"mel_ring must be [{S}, rows, {tables.n_mels}]")
+    nb = tables.n_fft // 2 + 1
+    if tables.fb.dtype != torch.float32 or tables.fb.dim() != 2 or tables.fb.shape[1] != nb or not tables.fb.is_contiguous():
+        raise ValueError(f"fb must be contiguous float32 [n_mels, {nb}]")
+    if tables.fb_range.dtype != torch.int32 or tuple(tables.fb_range.shape) != (tables.n_mels, 2) or not tables.fb_range.is_contiguous():
+        raise ValueError(f"fb_range must be contiguous int32 [{tables.n_mels}, 2]")
+    if tables.window.dtype != torch.float32 or tables.window.dim() != 1 or not tables.window.is_contiguous():
+        raise ValueError("window must be a contiguous float32 vector")
+    tensors = [streams, sample_ring, mel_ring, tables.window, tables.fb, tables.fb_range]
+    a = FeArgs()
+    if samples is not None:
+        if samples.dim() != 2 or samples.stride(1) != 1 or samples.shape[0] < batch:
+            raise ValueError("samples must be [batch, n] with unit inner stride")
+        if samples.dtype == torch.int16:
+            a.pcm_dtype = _lib.PCM_S16
+        elif samples.dtype == torch.float32:
+            a.pcm_dtype = _lib.PCM_F32
+        else:
+            raise TypeError(f"samples must be int16 pcm or float32, got {samples.dtype}")
+        if samples.shape[1] < max_new:
+            raise ValueError(f"samples has {samples.shape[1]} columns < max_new {max_new}")
+        a.samples, a.samples_stride = samples.data_ptr(), samples.stride(0)
+        tensors.append(samples)
+    else:
+        if max_new:
+            raise ValueError("max_new > 0 needs samples")
+        a.pcm_dtype, a.samples_stride = _lib.PCM_F32, 0
+    if streams.dtype != torch.uint8 or streams.numel() < 32 * batch:
+        raise ValueError("streams must hold batch x 32 bytes of pk_fe_stream records")
+    dev = _require_device(*tensors)
+    a.device = dev.index if dev.index is not None else torch.cuda.current_device()
+    a.batch, a.streams = int(batch), streams.data_ptr()
+    a.sample_ring, a.num_slots, a.ring_size = sample_ring.data_ptr(), S, R
+    a.mel_ring, a.mel_ring_rows, a.n_mels = mel_ring.data_ptr(), int(mel_ring.shape[1]), tables.n_mels
+    a.window, a.win_length = tables.window.data_ptr(), int(tables.window.shape[0])
+    a.n_fft, a.hop = tables.n_fft, tables.hop
+    a.fb, a.fb_range = tables.fb.data_ptr(), tables.fb_range.data_ptr()
+    a.preemph, a.dither, a.seed, a.log_guard = tables.preemph, float(dither), int(seed) & (2**64 - 1), tables.log_guard
+    a.max_new, a.max_frames = int(max_new), int(max_frames)
+    check(lib().pk_fe_step(ctypes.byref(a), _stream(dev)), "pk_fe_step")
+
+
+SUB_KEYS = ("conv.0", "conv.2", "conv.3", "conv.5", "conv.6")
+
+
+def subsample(
+    streams: torch.Tensor,
+    batch: int,
+    feats: torch.Tensor,
+    ring: bool,
+    weights: dict,
+    out: torch.Tensor,
+    *,
+    max_out: int,
+) -> torch.Tensor:
+    """ConvSubsampling's convolution stack for ``batch`` windows (pk_subsample;
+    subsample.py:30-57,140-152).  ``feats``: float32 [slots, rows, n_mels];
+    ``weights``: {"conv.0.weight": [C,1,3,3], "conv.0.bias": [C] or None, ...}
+    for conv.0/2/3/5/6 in the model dtype; ``out``: [rows_out, C * F3]."""
+    _check_f32(feats, "feats", 3)
+    w0 = weights["conv.0.weight"]
+    dt, C = w0.dtype, int(w0.shape[0])
+    F = int(feats.shape[2])
+    F3 = ((F // 2 + 1) // 2 + 1) // 2 + 1
+    shapes = {"conv.0": (C, 1, 3, 3), "conv.2": (C, 1, 3, 3), "conv.3": (C, C, 1, 1), "conv.5": (C, 1, 3, 3), "conv.6": (C, C, 1, 1)}
+    a = SubArgs()
+    tensors = [streams, feats, out]
+    for key in SUB_KEYS:
+        w, bias = weights[key + ".weight"], weights.get(key + ".bias")
+        if tuple(w.shape) != shapes[key] or w.dtype != dt or not w.is_contiguous():
+            raise ValueError(f"{key}.weight must be contiguous {shapes[key]} of {dt}")
+        if bias is not None and (tuple(bias.shape) != (C,) or bias.dtype != dt or not bias.is_contiguous()):
+            raise ValueError(f"{key}.bias must be contiguous [{C}] of {dt}")
+        n = key.split(".")[1]
+        setattr(a, "w" + n, w.data_ptr())
+        setattr(a, "b" + n, bias.data_ptr() if bias is not None else None)
+        tensors += [w] + ([bias] if bias is not None else [])
+    if out.dim() != 2 or out.shape[1] != C * F3 or out.dtype != dt or not out.is_contiguous():
+        raise ValueError(f"out must be contiguous [rows, {C * F3}] of {dt}")
+    if streams.dtype != torch.uint8 or streams.numel() < 32 * batch:
+        raise ValueError("streams must hold batch x 32 bytes of pk_sub_stream records")
+    dev = _require_device(*tensors)
+    a.dtype = dtype_code(dt)
+    a.device = dev.index if dev.index is not None else torch.cuda.current_device()
+    a.batch, a.streams = int(batch), streams.data_ptr()
+    a.feats, a.feat_slots, a.feat_rows, a.feat_ring = feats.data_ptr(), int(feats.shape[0]), int(feats.shape[1]), int(bool(ring))
+    a.n_mels, a.channels = F, C
+    a.out, a.out_rows, a.max_out = out.data_ptr(), int(out.shape[0]), int(max_out)
+    check(lib().pk_subsample(ctypes.byref(a), _stream(dev)), "pk_subsample")
     return out

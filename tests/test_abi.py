@@ -57,6 +57,10 @@ def test_every_declared_symbol_is_exported_and_bound():
         ("pk_attn_args", _lib.AttnArgs),
         ("pk_mask_args", _lib.MaskArgs),
         ("pk_conv_args", _lib.ConvArgs),
+        ("pk_fe_stream", _lib.FeStream),
+        ("pk_fe_args", _lib.FeArgs),
+        ("pk_sub_stream", _lib.SubStream),
+        ("pk_sub_args", _lib.SubArgs),
     ],
 )
 def test_struct_layout_matches_header(cname, pyclass):
@@ -71,6 +75,8 @@ def test_null_args_rejected_without_gpu():
     assert lib.pk_kv_gather(None, None) == _lib.PK_ERR_INVALID
     assert lib.pk_streaming_mask(None, None) == _lib.PK_ERR_INVALID
     assert lib.pk_conv_step(None, None) == _lib.PK_ERR_INVALID
+    assert lib.pk_fe_step(None, None) == _lib.PK_ERR_INVALID
+    assert lib.pk_subsample(None, None) == _lib.PK_ERR_INVALID
 
 
 def test_mask_args_validated_before_launch():
@@ -96,3 +102,39 @@ def test_conv_args_validated_before_launch():
     assert L.pk_conv_step(ctypes.byref(a), None) == _lib.PK_ERR_INVALID
     a.batch, a.dtype = 0, 7
     assert L.pk_conv_step(ctypes.byref(a), None) == _lib.PK_ERR_INVALID  # unknown dtype
+
+
+def test_struct_sizes_match_the_header_alignment():
+    # the per-stream headers are read by the kernels as 32-byte records
+    assert ctypes.sizeof(_lib.FeStream) == 32 and ctypes.sizeof(_lib.SubStream) == 32
+
+
+def test_front_end_args_validated_before_launch():
+    L = _lib.lib()
+    a = _lib.FeArgs()
+    a.batch, a.n_fft, a.win_length, a.hop, a.n_mels = 4, 512, 400, 160, 80
+    a.ring_size, a.mel_ring_rows, a.num_slots, a.max_new, a.max_frames = 8192, 32, 4, 2560, 16
+    a.samples_stride, a.pcm_dtype = 2560, _lib.PCM_S16
+    assert L.pk_fe_step(ctypes.byref(a), None) == _lib.PK_ERR_INVALID  # NULL tensors
+    assert "NULL" in _lib.last_error()
+    a.n_fft = 400
+    assert L.pk_fe_step(ctypes.byref(a), None) == _lib.PK_ERR_UNSUPPORTED
+    a.n_fft, a.ring_size = 512, 8000  # not a power of two
+    assert L.pk_fe_step(ctypes.byref(a), None) == _lib.PK_ERR_INVALID
+    a.ring_size, a.max_frames = 8192, 33  # more frames than the mel ring holds
+    assert L.pk_fe_step(ctypes.byref(a), None) == _lib.PK_ERR_INVALID
+    a.max_frames, a.n_mels = 16, 129
+    assert L.pk_fe_step(ctypes.byref(a), None) == _lib.PK_ERR_UNSUPPORTED
+    a.n_mels, a.win_length = 80, 401  # n_fft - win odd
+    assert L.pk_fe_step(ctypes.byref(a), None) == _lib.PK_ERR_INVALID
+
+    s = _lib.SubArgs()
+    s.dtype, s.batch, s.n_mels, s.channels, s.feat_slots, s.feat_rows, s.feat_ring = _lib.DTYPE_F16, 4, 80, 256, 4, 32, 1
+    s.out_rows, s.max_out = 8, 2
+    assert L.pk_subsample(ctypes.byref(s), None) == _lib.PK_ERR_INVALID  # NULL tensors
+    s.channels = 96
+    assert L.pk_subsample(ctypes.byref(s), None) == _lib.PK_ERR_UNSUPPORTED
+    s.channels, s.feat_rows = 256, 30  # a ring needs a power of two
+    assert L.pk_subsample(ctypes.byref(s), None) == _lib.PK_ERR_INVALID
+    s.feat_rows, s.dtype = 32, 9
+    assert L.pk_subsample(ctypes.byref(s), None) == _lib.PK_ERR_INVALID
