@@ -176,62 +176,172 @@ def cpu_baseline(shape, streams: int, budget_s: float, seed: int) -> dict:
     }
 
 
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16
+
+
+def synth_pcm(streams: int, n: int, seed: int):
+    """int16 pcm per stream: 3 sinusoids of random frequency (100-4000 Hz),
+    amplitude and phase, plus Gaussian noise at 20 dB SNR."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    t = np.arange(n, dtype=np.float64) / 16000.0
+    out = np.empty((streams, n), dtype=np.int16)
+    for b in range(streams):
+        f = rng.uniform(100.0, 4000.0, 3)
+        a = rng.uniform(0.05, 0.3, 3)
+        ph = rng.uniform(0.0, 2 * np.pi, 3)
+        sig = (a[:, None] * np.sin(2 * np.pi * f[:, None] * t[None, :] + ph[:, None])).sum(0)
+        sig += rng.standard_normal(n) * np.sqrt(np.mean(sig**2) / 100.0)
+        out[b] = np.clip(np.round(sig * 32767.0), -32768, 32767).astype(np.int16)
+    return out
+
+
+def _graph_time_us(fn, device, reps: int = 20, inner: int = 10) -> float:
+    """Average time of the launches ``fn`` makes: ``inner`` calls recorded in one
+    HIP graph, replayed ``reps`` times, so neither the host's launch cost nor the
+    graph's own launch shows in the per-call time."""
+    import torch
+
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        fn()  # warm outside the capture
+    torch.cuda.current_stream(device).wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        for _ in range(inner):
+            fn()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return 1000.0 * a.elapsed_time(b) / (reps * inner)
+
+
+def front_end_cpu_baseline(sub_sd: dict, budget_s: float, seed: int) -> dict:
+    """The oracle's per-stream pre-encode (FeatureExtractor.push + ConvSubsampling
+    on the [cache ; new] window + drop, model_runner.py:181-252) on one host core,
+    on 160 ms chunks of one stream, for about ``budget_s`` seconds."""
+    import numpy as np
+
+    from oracle import frontend as ofe
+
+    from threadpoolctl import threadpool_limits
+
+    p = ofe.FeParams(n_mels=80)
+    st = ofe.PreEncodeState(ofe.FeState(p, noise_id=1, seed=1), sub_sd, store_dtype=None)
+    pcm = synth_pcm(1, 1440 + 2560 * 400, seed)[0].astype(np.float32) / 32768.0
+    with threadpool_limits(limits=1):  # one core, BLAS included
+        st.push(pcm[:1440])
+        pos, chunks, t0 = 1440, 0, time.perf_counter()
+        while time.perf_counter() - t0 < budget_s and pos + 2560 <= len(pcm):
+            st.push(pcm[pos : pos + 2560])
+            pos += 2560
+            chunks += 1
+        el = time.perf_counter() - t0
+    return {"chunks_per_s": chunks / el, "chunks": chunks, "seconds": el}
+
+
 def encoder_bench(args, device) -> int:
-    """``--config e2e``: the streaming FastConformer encoder step after the front
-    end -- a random-init small model (17 layers, d_model 512, 8 heads, feed-forward
-    x4, depthwise conv kernel 9, left context 70, 2 frames per step), fp16, 128
-    streams, all live.  Per step and layer: the torch projections and feed-forward
-    GEMMs, the fused paged attention (pk_paged_relpos_attn) and the fused conv step
-    with the per-stream conv cache in place (pk_conv_step); streaming masks from one
-    launch (pk_streaming_mask); the state advance (encoder.py:229-267).  Input:
-    seeded N(0,1) subsampled frames resident on the GPU (the log-mel + 8x
-    subsampling front end is not part of this step).  Also times the conv step
-    alone per launch on the same shape."""
+    """``--config e2e``: one streaming step of a random-init small FastConformer
+    from pcm16 -- 128 streams, each fed a 160 ms chunk (2560 samples) per step:
+    the batched front end (pk_fe_step: sample ring, dither, pre-emphasis, FFT,
+    Slaney mel, log; pk_subsample: the 8x convolution stack over each stream's
+    [9 cached + 16 new] mel window; the ``out`` GEMM; model_runner.py:181-252),
+    then the encoder (17 layers, d_model 512, 8 heads, feed-forward x4,
+    depthwise conv kernel 9, left context 70, 2 frames per step: torch
+    projections and feed-forward GEMMs, pk_paged_relpos_attn, pk_conv_step,
+    pk_streaming_mask; encoder.py:229-267), fp16.  Input: int16 pcm of 3
+    random sinusoids (100-4000 Hz) plus noise at 20 dB SNR, resident on the GPU.
+    Also times the front-end kernels and the conv step alone per launch."""
     import numpy as np
     import torch
 
     from parakeet_amd import ops
     from parakeet_amd.modules.encoder import ConformerEncoder
+    from parakeet_amd.modules.frontend import ConvSubsampling, FeatureExtractor, PreEncoder
 
     B, D, H, Ly, K, left, right = 128, 512, 8, 17, 9, 70, 1
+    n_mels, C = 80, 256
     T = right + 1
+    hop, chunk = 160, 2560
     dt = torch.float16
     torch.manual_seed(4)
     enc = ConformerEncoder(
-        feat_in=80, hidden_size=D, ff_expansion_factor=4, num_layers=Ly, num_heads=H, subsampling_factor=8,
-        pos_emb_max_len=5000, conv_kernel_size=K, att_context_size=[left, right], subsampling_conv_channels=256,
+        feat_in=n_mels, hidden_size=D, ff_expansion_factor=4, num_layers=Ly, num_heads=H, subsampling_factor=8,
+        pos_emb_max_len=5000, conv_kernel_size=K, att_context_size=[left, right], subsampling_conv_channels=C,
         use_bias=False,
     )
+    sub = ConvSubsampling(D, C, n_mels, 8)
     with torch.no_grad():
         for layer in enc.layers:
             layer.self_attn.pos_bias_u.normal_(0.0, 0.02)
             layer.self_attn.pos_bias_v.normal_(0.0, 0.02)
-    enc = enc.to(dt).to(device).eval()
+        for mod in sub.conv:
+            if isinstance(mod, torch.nn.Conv2d):
+                mod.weight.normal_(0.0, mod.weight[0].numel() ** -0.5)
+    enc = enc.to(dt).to(device).eval().requires_grad_(False)
+    sub = sub.to(dt).to(device).eval().requires_grad_(False)
+    fx = FeatureExtractor(n_mels=n_mels, seed=6, device=device)
+    pre = PreEncoder(fx, sub, num_slots=B, device=device)
+    slots = np.arange(B)
+    for s in slots:
+        pre.reset_slot(s)
     state = enc.init_streaming_state(batch_size=B, device=device, dtype=dt)
-    g = torch.Generator().manual_seed(5)
-    xs = [torch.randn(B, T, D, generator=g).to(dt).to(device) for _ in range(8)]
+    pre_steps = 36 + args.warmup
+    n_total = 1440 + chunk * (pre_steps + args.steps)
+    log(f"synthesising {B} x {n_total} pcm16 samples")
+    pcm = torch.from_numpy(synth_pcm(B, n_total, seed=7)).to(device)
     length = torch.full((B,), T, dtype=torch.int64, device=device)
+    pos = 0
+
+    def step():
+        nonlocal pos
+        n = 1440 if pos == 0 else chunk
+        rows, counts, first = pre.step(slots, pcm[:, pos : pos + n], n, False)
+        pos += n
+        if not (counts == T).all():
+            raise RuntimeError(f"front end gave {counts.min()}..{counts.max()} frames per stream, expected {T}")
+        enc(rows.view(B, T, D), state, length=length)
+
     gc.collect()
     gc.freeze()
     with torch.inference_mode():
-        for i in range(args.warmup + 36):  # past the 70-frame window
-            enc(xs[i % len(xs)], state, length=length)
+        for _ in range(pre_steps):  # past the 70-frame window
+            step()
         torch.cuda.synchronize()
         K_steps = args.steps
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
         start.record()
-        for i in range(K_steps):
-            enc(xs[i % len(xs)], state, length=length)
+        for _ in range(K_steps):
+            step()
         stop.record()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
         ms = start.elapsed_time(stop) / K_steps
-        log(f"timed {K_steps} encoder steps")
-        # the conv step alone on the same shape and cache: one launch per layer,
-        # recorded once in a HIP graph and replayed, so the host's launch cost
-        # stays out of the per-launch time
+        log(f"timed {K_steps} steps from pcm16")
+
+        # the front-end kernels alone on the last step's records (re-running a
+        # step's records recomputes the same frames into the same ring rows)
+        fe_args = dict(dither=fx.dither, seed=fx.seed, max_new=chunk, max_frames=16)
+        samples = pcm[:, pos - chunk : pos]
+        flat = torch.empty((B * T, C * sub.final_freq_dim), dtype=dt, device=device)
+        w = sub.conv_weights()
+        fe_us = _graph_time_us(lambda: ops.fe_step(pre.hdr[: 32 * B], B, samples, pre.sample_ring, pre.mel_ring,
+                                                   pre.tables, **fe_args), device)
+        sub_us = _graph_time_us(lambda: ops.subsample(pre.hdr[32 * B :], B, pre.mel_ring, True, w, flat, max_out=T),
+                                device)
+        lin_us = _graph_time_us(lambda: torch.nn.functional.linear(flat, sub.out.weight, sub.out.bias), device)
+        log("timed the front-end kernels")
+
+        # the conv step alone on the same shape and cache
         conv = enc.layers[0].conv
+        g = torch.Generator().manual_seed(5)
         h = torch.randn(B, T, 2 * D, generator=g).to(dt).to(device)
         frames = state.cache.conv_frames
 
@@ -240,27 +350,30 @@ def encoder_bench(args, device) -> int:
                 ops.conv_step(h, frames, conv.depthwise_conv.weight, conv.batch_norm.weight, conv.batch_norm.bias,
                               layer=layer, eps=conv.batch_norm.eps)
 
-        side = torch.cuda.Stream(device)
-        side.wait_stream(torch.cuda.current_stream(device))
-        with torch.cuda.stream(side):
-            conv_all_layers()  # warm outside the capture
-        torch.cuda.current_stream(device).wait_stream(side)
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=side):
-            conv_all_layers()
-        torch.cuda.synchronize()
-        reps = 20
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        for _ in range(reps):
-            graph.replay()
-        b.record()
-        torch.cuda.synchronize()
-        conv_us = 1000.0 * a.elapsed_time(b) / (reps * Ly)
+        conv_us = _graph_time_us(conv_all_layers, device, inner=1) / Ly
     s = 2
     conv_bytes = B * s * (T * 2 * D + 2 * (K - 1) * D + T * D) + s * D * (K + 2)
+    # front-end algorithmic work per step (steady state: 16 new frames, window of 25)
+    F1, F2, F3 = 41, 21, 11
+    fe_bytes = B * (chunk * 2 + chunk * 4 + 16 * n_mels * 4)  # pcm in, ring write, mel rows out
+    # the MACs the 2 kept output frames of each stream depend on: conv.0 rows 2..12,
+    # first depthwise + pointwise rows 2..6, second depthwise + pointwise rows 2..3
+    sub_macs = B * (11 * F1 * C * 9 + 5 * F2 * C * 9 + 5 * F2 * C * C + 2 * F3 * C * 9 + 2 * F3 * C * C)
+    sub_tflops = 2 * sub_macs / (sub_us * 1e-6) / 1e12
+    cpu = None
+    if not args.no_cpu_baseline:
+        sd = {k: v.detach().double().cpu().numpy() for k, v in sub.state_dict().items()}
+        cb = front_end_cpu_baseline(sd, min(args.cpu_baseline_seconds, 10.0), seed=8)
+        cpu = {
+            "value": round(cb["chunks_per_s"] / B, 4),
+            "unit": "front-end steps/s (128 streams x 160 ms)",
+            "cores": 1,
+            "kind": "port",
+            "sample": f"{cb['chunks']} chunks of 160 ms of one stream through the oracle's FeatureExtractor.push + "
+            f"ConvSubsampling (float64 numpy) in {cb['seconds']:.1f} s, scaled to 128 streams per step",
+        }
     result = {
-        "metric": "streaming encoder steps/sec (small FastConformer, 17 layers, after the front end) at 1 GPU",
+        "metric": "streaming encoder steps/sec from pcm16 (small FastConformer: front end + 17 layers) at 1 GPU",
         "value": round(1000.0 / ms, 2),
         "unit": "steps/s",
         "n_gpus": 1,
@@ -271,10 +384,11 @@ def encoder_bench(args, device) -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp16",
-        "data": "synthetic (seeded N(0,1) subsampled frames, random-init weights, pos biases N(0,0.02))",
+        "data": "synthetic pcm16 (3 random sinusoids 100-4000 Hz + noise at 20 dB SNR), random-init weights, pos biases N(0,0.02)",
         "config": {
-            "workload": "small FastConformer encoder step: 17 layers x (FF/2, paged rel-pos MHA, conv module with "
-            "per-stream cache, FF/2, LN), 128 streams all live, 2 frames per step",
+            "workload": "small FastConformer step from pcm16: 160 ms per stream -> log-mel (80) -> 8x conv "
+            "subsampling -> 17 layers x (FF/2, paged rel-pos MHA, conv module with per-stream cache, FF/2, LN), "
+            "128 streams all live, 2 encoder frames per step",
             "layers": Ly,
             "d_model": D,
             "heads": H,
@@ -282,7 +396,26 @@ def encoder_bench(args, device) -> int:
             "left_context": left,
             "frames_per_step": T,
             "streams": B,
+            "n_mels": n_mels,
+            "subsampling_channels": C,
             "parallelism": "single GPU",
+        },
+        "front_end": {
+            "fe_kernel_us": round(fe_us, 3),
+            "subsample_kernel_us": round(sub_us, 3),
+            "out_gemm_us": round(lin_us, 3),
+            "fe_bytes_per_launch": fe_bytes,
+            "fe_gbs": round(fe_bytes / (fe_us * 1e-6) / 1e9, 1),
+            "subsample_flops_per_launch": 2 * sub_macs,
+            "roofline": {
+                "bound": "mfma",
+                "achieved": round(sub_tflops, 2),
+                "peak": MFMA_F16_PEAK_TFLOPS,
+                "unit": "TFLOP/s",
+                "frac": round(sub_tflops / MFMA_F16_PEAK_TFLOPS, 5),
+                "kernel": "subsample_kernel",
+            },
+            "cpu_baseline": cpu,
         },
         "conv_step": {
             "kernel": "conv_step_kernel (GLU, pad mask, causal depthwise conv with cache, LayerNorm, SiLU)",

@@ -98,11 +98,20 @@ __device__ static inline void dft4(float2* v) {
   v[3] = make_float2(t1.x - t3.y, t1.y + t3.x);  // t1 + i t3
 }
 
+constexpr int kMaxWin = kNfft;
+constexpr int kMaxHop = kNfft;
+constexpr int kSpanMax = (kFeWaves - 1) * kMaxHop + kMaxWin + 1;  // samples the frames of a workgroup read
+constexpr int kBand = 32;  // filterbank weights per band staged in LDS
+
+template <int PCM>
 __global__ void __launch_bounds__(64 * kFeWaves) fe_kernel(const FeK p) {
-  __shared__ float2 tw[kCplx];        // e^{-2 pi i m / 256}
-  __shared__ float2 tw2[kBins];       // e^{-2 pi i k / 512}, k <= 256
+  __shared__ float2 tw[kCplx];   // e^{-2 pi i m / 256}
+  __shared__ float2 tw2[kBins];  // e^{-2 pi i k / 512}, k <= 256
   __shared__ float2 buf[kFeWaves][kCplx];
   __shared__ float pw[kFeWaves][kBins + 3];
+  __shared__ float xs[kSpanMax + 3];  // dithered samples of the workgroup's frames
+  __shared__ float win_s[kMaxWin];
+  __shared__ float fbw[kMaxMels][kBand];  // band m's weights from its first bin on
 
   const int b = blockIdx.y;
   const pk_fe_stream s = p.streams[b];
@@ -112,18 +121,85 @@ __global__ void __launch_bounds__(64 * kFeWaves) fe_kernel(const FeK p) {
   const int64_t total = s.sample_base + s.n_new;
   const int rmask = p.ring_size - 1;
   float* ring = p.ring + (int64_t)s.slot * p.ring_size;
+  const int tid = threadIdx.x;
 
-  // new samples -> ring (this call reads only ring entries of older samples)
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < s.n_new;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const float x = p.pcm == PK_PCM_S16
-                        ? (float)((const int16_t*)p.samples)[b * p.s_stride + i] * (1.0f / 32768.0f)
-                        : ((const float*)p.samples)[b * p.s_stride + i];
-    ring[(s.sample_base + i) & rmask] = x;
+  // (with no new samples the input may be NULL: read the ring instead, discarded)
+  const void* smp = p.samples ? p.samples : (const void*)p.ring;
+  const int64_t sst = p.samples ? b * p.s_stride : 0;
+  auto sample_in = [&](int64_t o) -> float {
+    if constexpr (PCM == PK_PCM_S16)
+      return (float)((const int16_t*)smp)[sst + o] * (1.0f / 32768.0f);
+    else
+      return ((const float*)smp)[sst + o];
+  };
+  // new samples -> ring (this call reads only ring entries of older samples);
+  // four loads per thread in flight before their stores
+  constexpr int kCopy = 4;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i0 = (int64_t)blockIdx.x * blockDim.x + tid; i0 < s.n_new; i0 += kCopy * stride) {
+    float x[kCopy];
+#pragma unroll
+    for (int u = 0; u < kCopy; ++u) x[u] = sample_in(min(i0 + u * stride, (int64_t)s.n_new - 1));
+#pragma unroll
+    for (int u = 0; u < kCopy; ++u)
+      if (i0 + u * stride < s.n_new) ring[(s.sample_base + i0 + u * stride) & rmask] = x[u];
   }
-  if ((int)blockIdx.x * kFeWaves >= s.n_frames) return;  // no frame for this workgroup
+  const int j0 = blockIdx.x * kFeWaves;
+  if (j0 >= s.n_frames) return;  // no frame for this workgroup
+  const int nf = min(kFeWaves, s.n_frames - j0);
+  const int wl = (kNfft - p.win) / 2;
+  const int64_t f0 = (int64_t)s.frame0 + j0;
+  const int64_t span0 = f0 * p.hop - kNfft / 2 + wl - 1;  // global index of xs[0]
+  const int span = (nf - 1) * p.hop + p.win + 1;
 
-  for (int m = threadIdx.x; m < kBins; m += blockDim.x) {
+  // staging, one global round trip per phase: every load of a phase is issued
+  // into registers before any of them is stored
+  __shared__ int2 rng_s[kMaxMels];
+  constexpr int kXsPer = (kSpanMax + 64 * kFeWaves - 1) / (64 * kFeWaves);
+  constexpr int kFbPer = kMaxMels * kBand / (64 * kFeWaves);
+  constexpr int kWinPer = kMaxWin / (64 * kFeWaves);
+  float xr[kXsPer], wr[kWinPer];
+  const int mc = min(tid, p.n_mels - 1);
+  const int2 rr = make_int2(p.fb_range[2 * mc], p.fb_range[2 * mc + 1]);
+#pragma unroll
+  for (int u = 0; u < kWinPer; ++u) wr[u] = p.window[min(tid + u * 64 * kFeWaves, p.win - 1)];
+  // raw sample i from this call's input or the ring (0 outside [0, total)):
+  // unconditional loads from clamped addresses
+#pragma unroll
+  for (int u = 0; u < kXsPer; ++u) {
+    const int i = tid + u * 64 * kFeWaves;
+    const int64_t g = span0 + i;
+    const bool ok = i < span && g >= 0 && g < total;
+    const bool fresh = g >= s.sample_base;
+    const float xn = sample_in(ok && fresh ? g - s.sample_base : 0);
+    const float xo = ring[ok && !fresh ? (g & rmask) : 0];
+    const float x = fresh ? xn : xo;
+    xr[u] = ok ? x : 0.f;
+  }
+  if (tid < p.n_mels) rng_s[tid] = make_int2(max(rr.x, 0), min(rr.y, kBins));
+#pragma unroll
+  for (int u = 0; u < kWinPer; ++u) {
+    const int i = tid + u * 64 * kFeWaves;
+    if (i < p.win) win_s[i] = wr[u];
+  }
+#pragma unroll
+  for (int u = 0; u < kXsPer; ++u) {
+    const int i = tid + u * 64 * kFeWaves;
+    const int64_t g = span0 + i;
+    float x = xr[u];
+    if (p.dither != 0.f && g >= 0 && g < total) x += p.dither * dither_normal(g, s.noise_id, p.seed_lo, p.seed_hi);
+    if (i < span) xs[i] = x;
+  }
+  __syncthreads();
+  // band m's weights from its first bin (the bins past kBand are read from fb)
+  float fr[kFbPer];
+#pragma unroll
+  for (int u = 0; u < kFbPer; ++u) {
+    const int i = tid + u * 64 * kFeWaves;
+    const int m = i / kBand, k = rng_s[m].x + i % kBand;
+    fr[u] = (m < p.n_mels && k < rng_s[m].y) ? p.fb[(int64_t)m * kBins + k] : 0.f;
+  }
+  for (int m = tid; m < kBins; m += blockDim.x) {
     float sn, cs;
     if (m < kCplx) {
       sincospif((float)m / 128.0f, &sn, &cs);
@@ -132,37 +208,24 @@ __global__ void __launch_bounds__(64 * kFeWaves) fe_kernel(const FeK p) {
     sincospif((float)m / 256.0f, &sn, &cs);
     tw2[m] = make_float2(cs, -sn);
   }
+#pragma unroll
+  for (int u = 0; u < kFbPer; ++u) {
+    const int i = tid + u * 64 * kFeWaves;
+    fbw[i / kBand][i % kBand] = fr[u];
+  }
   __syncthreads();
 
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int j = blockIdx.x * kFeWaves + wave;
-  if (j >= s.n_frames) return;  // no barrier below this point
-  const int f = s.frame0 + j;
-  const int64_t base = (int64_t)f * p.hop - kNfft / 2;
-  const int wl = (kNfft - p.win) / 2;
-  const uint32_t k0 = p.seed_lo, k1 = p.seed_hi;
-
-  // raw sample i (0 <= i < total) from this call's input or the ring, dithered
-  auto xd = [&](int64_t i) -> float {
-    float x;
-    if (i >= s.sample_base) {
-      const int64_t o = i - s.sample_base;
-      x = p.pcm == PK_PCM_S16 ? (float)((const int16_t*)p.samples)[b * p.s_stride + o] * (1.0f / 32768.0f)
-                              : ((const float*)p.samples)[b * p.s_stride + o];
-    } else {
-      x = ring[i & rmask];
-    }
-    if (p.dither != 0.f) x += p.dither * dither_normal(i, s.noise_id, k0, k1);
-    return x;
-  };
+  const int wave = tid >> 6, lane = tid & 63;
+  if (wave >= nf) return;  // no barrier below this point
+  const int64_t f = f0 + wave;
+  const int64_t base = f * p.hop - kNfft / 2;
+  const int off = wave * p.hop - wl + 1;  // xs index of frame sample n is off + n
   // windowed, pre-emphasised frame sample n (0 <= n < 512)
   auto frame_val = [&](int n) -> float {
     if (n < wl || n >= wl + p.win) return 0.f;
     const int64_t i = base + n;
     if (i < 0 || i >= total) return 0.f;
-    const float cur = xd(i);
-    const float prev = i >= 1 ? xd(i - 1) : 0.f;
-    return (cur - p.preemph * prev) * p.window[n - wl];
+    return (xs[off + n] - p.preemph * xs[off + n - 1]) * win_s[n - wl];
   };
 
   // z[n] = v[2n] + i v[2n+1]; lane holds z[lane + 64 r]
@@ -206,10 +269,10 @@ __global__ void __launch_bounds__(64 * kFeWaves) fe_kernel(const FeK p) {
   wave_lds_sync();
   float* mrow = p.mel + ((int64_t)s.slot * p.mel_rows + (f & (p.mel_rows - 1))) * p.n_mels;
   for (int m = lane; m < p.n_mels; m += 64) {
-    const int lo = p.fb_range[2 * m], hi = p.fb_range[2 * m + 1];
-    const float* w = p.fb + (int64_t)m * kBins;
+    const int lo = rng_s[m].x, hi = rng_s[m].y;
     float acc = 0.f;
-    for (int kk = max(lo, 0); kk < min(hi, kBins); ++kk) acc += w[kk] * pwv[kk];
+    for (int kk = lo; kk < hi; ++kk)
+      acc += (kk - lo < kBand ? fbw[m][kk - lo] : p.fb[(int64_t)m * kBins + kk]) * pwv[kk];
     mrow[m] = logf(acc + p.guard);
   }
 }
@@ -268,13 +331,17 @@ struct SubK {
 
 constexpr int kSubWaves = 8;
 constexpr int kSubThreads = 64 * kSubWaves;
-constexpr int kMaxC = 256;
 constexpr int kCG = 64;  // channels per conv.0 / first depthwise group
 
 // output length of a 3x3 stride-2 conv padded (2, 1): (n + 2 + 1 - 3) / 2 + 1
 __host__ __device__ static inline int half_up(int n) { return n / 2 + 1; }
 
-template <typename ST, int QT>
+template <int A, int B>
+struct cmax {
+  static constexpr int v = A > B ? A : B;
+};
+
+template <typename ST, int QT, int C>
 struct SubGeom {
   static constexpr int VEC = 16 / sizeof(ST);
   static constexpr int XR = 15, XC = 8 * QT + 7;  // input rows / cols of the tile
@@ -282,21 +349,68 @@ struct SubGeom {
   static constexpr int A2R = 3, A2C = 2 * QT + 1;  // after the first depthwise conv
   static constexpr int M1 = A1R * A1C, T1 = (M1 + 15) / 16;
   static constexpr int M2 = A2R * A2C, T2 = (M2 + 15) / 16;
-  static constexpr int RS = kMaxC + VEC;  // padded LDS row (elements) of MFMA A operands
-  static constexpr int REG_A = (A1R * A1C * kCG > M2 * kMaxC ? A1R * A1C * kCG : M2 * kMaxC) > kMaxC * QT
-                                   ? (A1R * A1C * kCG > M2 * kMaxC ? A1R * A1C * kCG : M2 * kMaxC)
-                                   : kMaxC * QT;
-  static constexpr int REG_B = (T2 > 1 ? T2 : 1) * 16 * RS;
-  static constexpr int T1W = (T1 + kSubWaves - 1) / kSubWaves;  // conv.0 M tiles per wave
+  // LDS rows of per-position channel vectors are padded by one 16-byte chunk so
+  // the 16 positions of an MFMA fragment fall on distinct banks
+  static constexpr int RS = C + VEC;    // a2 (before and after the pointwise conv), a3
+  static constexpr int A1S = kCG + VEC;  // a1 (one channel group)
+  // regA: a1 [T1*16][A1S] -> a2 [T2*16][RS] -> output tile [C][QT]
+  static constexpr int REG_A = cmax<cmax<T1 * 16 * A1S, T2 * 16 * RS>::v, C * QT>::v;
+  // regB: a2 before the pointwise conv [T2*16][RS] -> a3 before it [16][RS]
+  static constexpr int REG_B = cmax<T2, 1>::v * 16 * RS;
+  static constexpr int T1W = (T1 + kSubWaves - 1) / kSubWaves;  // conv.0 position tiles per wave
+  static constexpr int KS = C / (4 * VEC);                      // K steps of a pointwise conv
+  static constexpr int NT = C / 16;                             // channel tiles of a pointwise conv
+  static constexpr int NPW = (NT + kSubWaves - 1) / kSubWaves;  // channel tiles per wave
+  static constexpr int CH = C / VEC;                            // 16-byte channel chunks
+  static constexpr int KP = 4 * VEC;                            // conv.0 taps padded to one K step
 };
 
-template <typename ST, int QT>
+// Weight rows W[n][k] of a pointwise conv ([C out][C in], as the module holds
+// them) for the wave's channel tiles: the MFMA A operand, lane l holding
+// W[tile*16 + l%16][kstep*4*VEC + VEC*(l/16) + e].
+template <int NPW, int KS, int C, typename ST>
+__device__ static inline void load_pw(u32x4 (&b)[NPW][KS], const ST* w, int wave, int lr, int lg) {
+  constexpr int VEC = 16 / sizeof(ST);
+#pragma unroll
+  for (int h = 0; h < NPW; ++h) {
+    const int n = (wave * NPW + h) * 16 + lr;
+    if (n >= C) continue;
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) b[h][kk] = ld16(w + (int64_t)n * C + kk * 4 * VEC + VEC * lg);
+  }
+}
+
+// four consecutive elements from fp32
+template <typename ST>
+__device__ static inline void store4(ST* dst, const float* v) {
+  if constexpr (sizeof(ST) == 4) {
+    *reinterpret_cast<u32x4*>(dst) = Tr<ST>::pack(v);
+  } else {
+    Chunk<ST> c;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) c.v[e] = to_st<ST>(v[e]);
+    const u32x4 w = __builtin_bit_cast(u32x4, c);
+    *reinterpret_cast<uint2*>(dst) = make_uint2(w.x, w.y);
+  }
+}
+
+// One output frame t of the stack for output columns [p0, p0 + QT) per
+// workgroup.  MFMA operands: the weights are A (rows = output channels), the
+// activations B (columns = positions), so lane l holds 4 consecutive channels
+// 4*(l/16) .. of position l%16 and writes them as one 8- or 16-byte chunk.
+// Depthwise convs run on 16-byte channel chunks per thread.
+template <typename ST, int QT, int C>
 __global__ void __launch_bounds__(kSubThreads) subsample_kernel(const SubK<ST> p) {
-  typedef SubGeom<ST, QT> G;
+  typedef SubGeom<ST, QT, C> G;
   constexpr int VEC = G::VEC;
+  static_assert(C <= kSubThreads && C % kCG == 0, "one bias per thread, whole channel groups");
   __shared__ __align__(16) ST xin[G::XR * G::XC];
-  __shared__ __align__(16) ST regA[G::REG_A];  // a1 (one group) -> a2 -> flattened output tile
-  __shared__ __align__(16) ST regB[G::REG_B];  // a2 before pw (all channels) -> a3 before pw
+  __shared__ __align__(16) ST regA[G::REG_A];
+  __shared__ __align__(16) ST regB[G::REG_B];
+  __shared__ __align__(16) ST w0p[C * G::KP];  // conv.0 weights [C][KP], taps 9.. zero
+  __shared__ __align__(16) ST w2t[9 * C];   // depthwise weights tap-major [tap][C]
+  __shared__ __align__(16) ST w5t[9 * C];
+  __shared__ __align__(16) float bsm[5][C];  // biases of conv.0/2/3/5/6, 0 where absent
 
   const int b = blockIdx.z;
   const pk_sub_stream s = p.streams[b];
@@ -308,7 +422,7 @@ __global__ void __launch_bounds__(kSubThreads) subsample_kernel(const SubK<ST> p
   const int t = s.drop + j;  // output frame of the stack
   const int L3 = half_up(half_up(half_up(s.rows)));
   if (t >= L3) return;
-  const int F = p.F, C = p.C;
+  const int F = p.F;
   const int F1 = half_up(F), F2 = half_up(F1), F3 = half_up(F2);
   const int p0 = blockIdx.y * QT;  // first output column of the tile
   if (p0 >= F3) return;
@@ -323,26 +437,75 @@ __global__ void __launch_bounds__(kSubThreads) subsample_kernel(const SubK<ST> p
     return;
   }
 
-  // ---- input tile: rows 8t-14 .., cols 8p0-14 .., masked by length, rounded
+  // every global load before the convolutions is issued into registers first
+  // (one round trip): the small weights, biases and the input tile (stored to
+  // LDS), then the first pointwise conv's weights (kept in registers).  The
+  // loads are unconditional, from clamped addresses, so none waits in a branch.
+  constexpr int kWPer = (C * 9 + kSubThreads - 1) / kSubThreads;
+  constexpr int kXPer = (G::XR * G::XC + kSubThreads - 1) / kSubThreads;
+  ST w0r[kWPer], w2r[kWPer], w5r[kWPer];
+#pragma unroll
+  for (int u = 0; u < kWPer; ++u) {
+    const int i = min(tid + u * kSubThreads, C * 9 - 1);
+    w0r[u] = p.w0[i];
+    w2r[u] = p.w2[i];
+    w5r[u] = p.w5[i];
+  }
+  ST brs[5];
+  {
+    const int c = min(tid, C - 1);
+    brs[0] = (p.b0 ? p.b0 : p.w0)[c];
+    brs[1] = (p.b2 ? p.b2 : p.w0)[c];
+    brs[2] = (p.b3 ? p.b3 : p.w0)[c];
+    brs[3] = (p.b5 ? p.b5 : p.w0)[c];
+    brs[4] = (p.b6 ? p.b6 : p.w0)[c];
+  }
+  // input tile: rows 8t-14 .., cols 8p0-14 .., masked by length
+  float xr[kXPer];
   {
     const int r0 = 8 * t - 14, c0 = 8 * p0 - 14;
     const float* inb = p.in + (int64_t)s.slot * p.in_rows * F;
     const int rmask = p.in_rows - 1;
-    for (int i = tid; i < G::XR * G::XC; i += kSubThreads) {
+#pragma unroll
+    for (int u = 0; u < kXPer; ++u) {
+      const int i = tid + u * kSubThreads;
       const int rr = i / G::XC, cc = i - rr * G::XC;
       const int gr = r0 + rr, gc = c0 + cc;
-      float v = 0.f;
-      if (gr >= 0 && gr < s.length && gc >= 0 && gc < F) {
-        const int row = p.in_ring ? ((s.row0 + gr) & rmask) : s.row0 + gr;
-        v = inb[(int64_t)row * F + gc];
-      }
-      xin[i] = to_st<ST>(v);
+      const bool ok = i < G::XR * G::XC && gr >= 0 && gr < s.length && gc >= 0 && gc < F;
+      const int row = p.in_ring ? ((s.row0 + gr) & rmask) : s.row0 + gr;
+      const float v = inb[ok ? (int64_t)row * F + gc : 0];
+      xr[u] = ok ? v : 0.f;
     }
+  }
+  u32x4 bq[G::NPW][G::KS];
+  load_pw<G::NPW, G::KS, C>(bq, p.w3, wave, lr, lg);
+  const float br[5] = {p.b0 ? from_st(brs[0]) : 0.f, p.b2 ? from_st(brs[1]) : 0.f, p.b3 ? from_st(brs[2]) : 0.f,
+                       p.b5 ? from_st(brs[3]) : 0.f, p.b6 ? from_st(brs[4]) : 0.f};
+  for (int i = tid; i < C * G::KP; i += kSubThreads) w0p[i] = to_st<ST>(0.f);  // tap padding
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < kWPer; ++u) {
+    const int i = tid + u * kSubThreads;
+    if (i < C * 9) {
+      const int c = i / 9, k = i - c * 9;
+      w0p[c * G::KP + k] = w0r[u];
+      w2t[k * C + c] = w2r[u];
+      w5t[k * C + c] = w5r[u];
+    }
+  }
+  if (tid < C) {
+#pragma unroll
+    for (int k = 0; k < 5; ++k) bsm[k][tid] = br[k];
+  }
+#pragma unroll
+  for (int u = 0; u < kXPer; ++u) {
+    const int i = tid + u * kSubThreads;
+    if (i < G::XR * G::XC) xin[i] = to_st<ST>(xr[u]);
   }
   __syncthreads();
 
-  // ---- conv.0 operands: A = the 9 taps of each position (one K chunk), per wave
-  // its M tiles m = wave + 8 u
+  // conv.0 B operand: the 9 taps of each position (one K chunk), per wave its
+  // position tiles wave + 8 u
   u32x4 a0[G::T1W];
 #pragma unroll
   for (int u = 0; u < G::T1W; ++u) {
@@ -360,150 +523,170 @@ __global__ void __launch_bounds__(kSubThreads) subsample_kernel(const SubK<ST> p
     }
     a0[u] = __builtin_bit_cast(u32x4, ch);
   }
+  // validity of the wave's conv.0 positions (rows 4t-6 .., cols 4p0-6 ..)
+  bool ok1[G::T1W];
+#pragma unroll
+  for (int u = 0; u < G::T1W; ++u) {
+    const int m = (wave + kSubWaves * u) * 16 + lr;
+    const int i = m / G::A1C, q = m - i * G::A1C;
+    const int gr = 4 * t - 6 + i, gq = 4 * p0 - 6 + q;
+    ok1[u] = m < G::M1 && gr >= 0 && gr < len1 && gq >= 0 && gq < F1;
+  }
 
   ST* a1 = regA;
   ST* a2p = regB;
+#pragma unroll 1
   for (int cg = 0; cg < C; cg += kCG) {
-    // conv.0 for channels cg .. cg+63 -> bias, mask, ReLU -> a1 [7][A1C][64]
-    u32x4 bw[kCG / 16];
+    // conv.0 for channels cg .. cg+63 -> bias, mask, ReLU -> a1 [T1*16][A1S]
+    u32x4 aw[kCG / 16];
 #pragma unroll
-    for (int nt = 0; nt < kCG / 16; ++nt) {
-      const int c = cg + nt * 16 + lr;
-      Chunk<ST> ch;
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        const int tap = VEC * lg + e;
-        ch.v[e] = tap < 9 ? p.w0[c * 9 + tap] : to_st<ST>(0.f);
-      }
-      bw[nt] = __builtin_bit_cast(u32x4, ch);
-    }
+    for (int nt = 0; nt < kCG / 16; ++nt)
+      aw[nt] = *reinterpret_cast<const u32x4*>(&w0p[(cg + nt * 16 + lr) * G::KP + VEC * lg]);
 #pragma unroll
     for (int u = 0; u < G::T1W; ++u) {
       const int mt = wave + kSubWaves * u;
       if (mt >= G::T1) break;
 #pragma unroll
       for (int nt = 0; nt < kCG / 16; ++nt) {
-        const int c = cg + nt * 16 + lr;
-        const float bias = p.b0 ? from_st(p.b0[c]) : 0.f;
-        f32x4_t d = MmaK<ST>::step(a0[u], bw[nt], f32x4_t{0.f, 0.f, 0.f, 0.f});
+        const f32x4_t d = MmaK<ST>::step(aw[nt], a0[u], f32x4_t{0.f, 0.f, 0.f, 0.f});
+        const float4 bias = *reinterpret_cast<const float4*>(&bsm[0][cg + nt * 16 + 4 * lg]);
+        float v[4] = {d[0] + bias.x, d[1] + bias.y, d[2] + bias.z, d[3] + bias.w};
 #pragma unroll
-        for (int ii = 0; ii < 4; ++ii) {
-          const int m = mt * 16 + 4 * lg + ii;
-          if (m >= G::M1) continue;
-          const int i = m / G::A1C, q = m - i * G::A1C;
-          const int gr = 4 * t - 6 + i, gq = 4 * p0 - 6 + q;
-          const bool ok = gr >= 0 && gr < len1 && gq >= 0 && gq < F1;
-          a1[m * kCG + nt * 16 + lr] = to_st<ST>(ok ? fmaxf(round_to<ST>(d[ii] + bias), 0.f) : 0.f);
-        }
+        for (int e = 0; e < 4; ++e) v[e] = ok1[u] ? fmaxf(round_to<ST>(v[e]), 0.f) : 0.f;
+        store4<ST>(&a1[(mt * 16 + lr) * G::A1S + nt * 16 + 4 * lg], v);
       }
     }
     __syncthreads();
-    // first depthwise conv for the group -> a2p [M2][RS] (before the pointwise conv)
-    {
-      const int c = cg + lane;
-      float w[9];
+    // first depthwise conv for the group -> a2p [M2][RS], one 16-byte chunk of
+    // channels per item
+    constexpr int kGC = kCG / VEC;  // chunks per group
+    for (int it = tid; it < G::M2 * kGC; it += kSubThreads) {
+      const int m = it / kGC, cc = (it - m * kGC) * VEC;
+      const int si = m / G::A2C, pp = m - si * G::A2C;
+      float acc[VEC];
+      {
+        const float4* bb = reinterpret_cast<const float4*>(&bsm[1][cg + cc]);
 #pragma unroll
-      for (int k = 0; k < 9; ++k) w[k] = from_st(p.w2[c * 9 + k]);
-      const float bias = p.b2 ? from_st(p.b2[c]) : 0.f;
-      for (int m = wave; m < G::M2; m += kSubWaves) {
-        const int si = m / G::A2C, pp = m - si * G::A2C;
-        float acc = bias;
-#pragma unroll
-        for (int kt = 0; kt < 3; ++kt)
-#pragma unroll
-          for (int kf = 0; kf < 3; ++kf)
-            acc += w[kt * 3 + kf] * from_st(a1[((2 * si + kt) * G::A1C + 2 * pp + kf) * kCG + lane]);
-        a2p[m * G::RS + c] = to_st<ST>(acc);
-      }
-    }
-    __syncthreads();
-  }
-
-  // ---- pointwise conv.3 (C x C): wave owns N tiles 2w, 2w+1 -> bias, mask, ReLU -> a2
-  ST* a2 = regA;
-  const int ntiles = C / 16;
-  const int ksteps = C / (4 * VEC);
-  {
-    f32x4_t acc[G::T2][2];
-#pragma unroll
-    for (int mt = 0; mt < G::T2; ++mt) acc[mt][0] = acc[mt][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    const int n0 = 2 * wave;
-    if (n0 < ntiles) {
-      for (int kk = 0; kk < ksteps; ++kk) {
-        const int k = kk * 4 * VEC + VEC * lg;
-        const u32x4 b0 = ld16(p.w3 + (int64_t)(n0 * 16 + lr) * C + k);
-        const u32x4 b1 = ld16(p.w3 + (int64_t)((n0 + 1) * 16 + lr) * C + k);
-#pragma unroll
-        for (int mt = 0; mt < G::T2; ++mt) {
-          const u32x4 a = *reinterpret_cast<const u32x4*>(a2p + (mt * 16 + lr) * G::RS + k);
-          acc[mt][0] = MmaK<ST>::step(a, b0, acc[mt][0]);
-          acc[mt][1] = MmaK<ST>::step(a, b1, acc[mt][1]);
+        for (int e = 0; e < VEC; e += 4) {
+          const float4 x = bb[e / 4];
+          acc[e] = x.x;
+          acc[e + 1] = x.y;
+          acc[e + 2] = x.z;
+          acc[e + 3] = x.w;
         }
       }
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int c = (n0 + h) * 16 + lr;
-        const float bias = p.b3 ? from_st(p.b3[c]) : 0.f;
-#pragma unroll
-        for (int mt = 0; mt < G::T2; ++mt)
-#pragma unroll
-          for (int ii = 0; ii < 4; ++ii) {
-            const int m = mt * 16 + 4 * lg + ii;
-            if (m >= G::M2) continue;
-            const int si = m / G::A2C, pp = m - si * G::A2C;
-            const int gs = 2 * t - 2 + si, gp = 2 * p0 - 2 + pp;
-            const bool ok = gs >= 0 && gs < len2 && gp >= 0 && gp < F2;
-            a2[m * kMaxC + c] = to_st<ST>(ok ? fmaxf(round_to<ST>(acc[mt][h][ii] + bias), 0.f) : 0.f);
-          }
-      }
-    }
-  }
-  __syncthreads();
-
-  // ---- second depthwise conv -> a3p [QT][RS]
-  ST* a3p = regB;
-  for (int c = lane; c < C; c += 64) {
-    float w[9];
-#pragma unroll
-    for (int k = 0; k < 9; ++k) w[k] = from_st(p.w5[c * 9 + k]);
-    const float bias = p.b5 ? from_st(p.b5[c]) : 0.f;
-    for (int q = wave; q < QT; q += kSubWaves) {
-      float acc = bias;
 #pragma unroll
       for (int kt = 0; kt < 3; ++kt)
 #pragma unroll
-        for (int kf = 0; kf < 3; ++kf)
-          acc += w[kt * 3 + kf] * from_st(a2[(kt * G::A2C + 2 * q + kf) * kMaxC + c]);
-      a3p[q * G::RS + c] = to_st<ST>(acc);
+        for (int kf = 0; kf < 3; ++kf) {
+          float a[VEC], w[VEC];
+          Tr<ST>::unpack(*reinterpret_cast<const u32x4*>(&a1[((2 * si + kt) * G::A1C + 2 * pp + kf) * G::A1S + cc]), a);
+          Tr<ST>::unpack(*reinterpret_cast<const u32x4*>(&w2t[(kt * 3 + kf) * C + cg + cc]), w);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) acc[e] += w[e] * a[e];
+        }
+      *reinterpret_cast<u32x4*>(&a2p[m * G::RS + cg + cc]) = Tr<ST>::pack(acc);
+    }
+    __syncthreads();
+  }
+
+  // pointwise conv.3 (C x C): wave owns channel tiles wave*NPW .. -> bias, mask,
+  // ReLU -> a2 [T2*16][RS] (rows past M2 are scratch)
+  ST* a2 = regA;
+  const bool pw_active = wave * G::NPW < G::NT;
+  {
+    f32x4_t acc[G::T2][G::NPW];
+#pragma unroll
+    for (int mt = 0; mt < G::T2; ++mt)
+#pragma unroll
+      for (int h = 0; h < G::NPW; ++h) acc[mt][h] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    if (pw_active) {
+#pragma unroll
+      for (int kk = 0; kk < G::KS; ++kk) {
+        const int k = kk * 4 * VEC + VEC * lg;
+#pragma unroll
+        for (int mt = 0; mt < G::T2; ++mt) {
+          const u32x4 x = *reinterpret_cast<const u32x4*>(a2p + (mt * 16 + lr) * G::RS + k);
+#pragma unroll
+          for (int h = 0; h < G::NPW; ++h) acc[mt][h] = MmaK<ST>::step(bq[h][kk], x, acc[mt][h]);
+        }
+      }
+    }
+    // the second pointwise conv's weights load while this epilogue and the
+    // second depthwise conv run
+    load_pw<G::NPW, G::KS, C>(bq, p.w6, wave, lr, lg);
+    if (pw_active) {
+#pragma unroll
+      for (int mt = 0; mt < G::T2; ++mt) {
+        const int m = mt * 16 + lr;
+        const int si = m / G::A2C, pp = m - si * G::A2C;
+        const int gs = 2 * t - 2 + si, gp = 2 * p0 - 2 + pp;
+        const bool ok = m < G::M2 && gs >= 0 && gs < len2 && gp >= 0 && gp < F2;
+#pragma unroll
+        for (int h = 0; h < G::NPW; ++h) {
+          const int c0 = (wave * G::NPW + h) * 16 + 4 * lg;
+          const float4 bias = *reinterpret_cast<const float4*>(&bsm[2][c0]);
+          float v[4] = {acc[mt][h][0] + bias.x, acc[mt][h][1] + bias.y, acc[mt][h][2] + bias.z,
+                        acc[mt][h][3] + bias.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = ok ? fmaxf(round_to<ST>(v[e]), 0.f) : 0.f;
+          store4<ST>(&a2[m * G::RS + c0], v);
+        }
+      }
     }
   }
   __syncthreads();
 
-  // ---- pointwise conv.6 + ReLU -> flattened tile [C][QT] in regA
-  ST* ot = regA;
-  {
-    const int n0 = 2 * wave;
-    if (n0 < ntiles) {
-      f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-      for (int kk = 0; kk < ksteps; ++kk) {
-        const int k = kk * 4 * VEC + VEC * lg;
-        const u32x4 b0 = ld16(p.w6 + (int64_t)(n0 * 16 + lr) * C + k);
-        const u32x4 b1 = ld16(p.w6 + (int64_t)((n0 + 1) * 16 + lr) * C + k);
-        const u32x4 a = *reinterpret_cast<const u32x4*>(a3p + lr * G::RS + k);
-        acc0 = MmaK<ST>::step(a, b0, acc0);
-        acc1 = MmaK<ST>::step(a, b1, acc1);
+  // second depthwise conv -> a3p [QT][RS]
+  ST* a3p = regB;
+  for (int it = tid; it < QT * G::CH; it += kSubThreads) {
+    const int q = it / G::CH, cc = (it - q * G::CH) * VEC;
+    float acc[VEC];
+    {
+      const float4* bb = reinterpret_cast<const float4*>(&bsm[3][cc]);
+#pragma unroll
+      for (int e = 0; e < VEC; e += 4) {
+        const float4 x = bb[e / 4];
+        acc[e] = x.x;
+        acc[e + 1] = x.y;
+        acc[e + 2] = x.z;
+        acc[e + 3] = x.w;
       }
+    }
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int c = (n0 + h) * 16 + lr;
-        const float bias = p.b6 ? from_st(p.b6[c]) : 0.f;
+    for (int kt = 0; kt < 3; ++kt)
 #pragma unroll
-        for (int ii = 0; ii < 4; ++ii) {
-          const int q = 4 * lg + ii;
-          if (q >= QT) continue;
-          const float v = (h ? acc1 : acc0)[ii];
-          ot[c * QT + q] = to_st<ST>(fmaxf(round_to<ST>(v + bias), 0.f));
-        }
+      for (int kf = 0; kf < 3; ++kf) {
+        float a[VEC], w[VEC];
+        Tr<ST>::unpack(*reinterpret_cast<const u32x4*>(&a2[(kt * G::A2C + 2 * q + kf) * G::RS + cc]), a);
+        Tr<ST>::unpack(*reinterpret_cast<const u32x4*>(&w5t[(kt * 3 + kf) * C + cc]), w);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[e] += w[e] * a[e];
+      }
+    *reinterpret_cast<u32x4*>(&a3p[q * G::RS + cc]) = Tr<ST>::pack(acc);
+  }
+  __syncthreads();
+
+  // pointwise conv.6 + ReLU -> flattened tile [C][QT] in regA
+  ST* ot = regA;
+  if (pw_active) {
+    f32x4_t acc[G::NPW];
+#pragma unroll
+    for (int h = 0; h < G::NPW; ++h) acc[h] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < G::KS; ++kk) {
+      const u32x4 x = *reinterpret_cast<const u32x4*>(a3p + lr * G::RS + kk * 4 * VEC + VEC * lg);
+#pragma unroll
+      for (int h = 0; h < G::NPW; ++h) acc[h] = MmaK<ST>::step(bq[h][kk], x, acc[h]);
+    }
+    if (lr < QT) {
+#pragma unroll
+      for (int h = 0; h < G::NPW; ++h) {
+        const int c0 = (wave * G::NPW + h) * 16 + 4 * lg;
+        const float4 bias = *reinterpret_cast<const float4*>(&bsm[4][c0]);
+        const float bv[4] = {bias.x, bias.y, bias.z, bias.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ot[(c0 + e) * QT + lr] = to_st<ST>(fmaxf(round_to<ST>(acc[h][e] + bv[e]), 0.f));
       }
     }
   }
@@ -519,7 +702,7 @@ __global__ void __launch_bounds__(kSubThreads) subsample_kernel(const SubK<ST> p
 
 static bool pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
 
-template <typename ST, int QT>
+template <typename ST, int QT, int C>
 static int launch_sub(const pk_sub_args* a, hipStream_t st) {
   SubK<ST> k;
   k.streams = a->streams;
@@ -539,13 +722,25 @@ static int launch_sub(const pk_sub_args* a, hipStream_t st) {
   k.in_rows = a->feat_rows;
   k.in_ring = a->feat_ring;
   k.F = a->n_mels;
-  k.C = a->channels;
+  k.C = C;
   k.out_rows = a->out_rows;
   k.max_out = a->max_out;
   const int F3 = half_up(half_up(half_up(a->n_mels)));
   const dim3 grid(a->max_out, (F3 + QT - 1) / QT, a->batch);
-  hipLaunchKernelGGL((subsample_kernel<ST, QT>), grid, dim3(kSubThreads), 0, st, k);
+  hipLaunchKernelGGL((subsample_kernel<ST, QT, C>), grid, dim3(kSubThreads), 0, st, k);
   return check_launch("pk_subsample");
+}
+
+template <typename ST, int QT>
+static int launch_sub_c(const pk_sub_args* a, hipStream_t st) {
+  switch (a->channels) {
+    case 64:
+      return launch_sub<ST, QT, 64>(a, st);
+    case 128:
+      return launch_sub<ST, QT, 128>(a, st);
+    default:
+      return launch_sub<ST, QT, 256>(a, st);
+  }
 }
 
 }  // namespace pk
@@ -561,7 +756,7 @@ extern "C" int pk_fe_step(const pk_fe_args* a, void* stream) {
   if (a->win_length < 1 || a->win_length > a->n_fft || (a->n_fft - a->win_length) % 2)
     return fail(PK_ERR_INVALID, "pk_fe_step: win_length %d must be in [1, n_fft] with n_fft - win even",
                 a->win_length);
-  if (a->hop < 1) return fail(PK_ERR_INVALID, "pk_fe_step: hop %d", a->hop);
+  if (a->hop < 1 || a->hop > kMaxHop) return fail(PK_ERR_INVALID, "pk_fe_step: hop %d not in [1, %d]", a->hop, kMaxHop);
   if (a->n_mels < 1 || a->n_mels > kMaxMels)
     return fail(PK_ERR_UNSUPPORTED, "pk_fe_step: n_mels %d not in [1, %d]", a->n_mels, kMaxMels);
   if (!pow2(a->ring_size) || !pow2(a->mel_ring_rows))
@@ -607,7 +802,10 @@ extern "C" int pk_fe_step(const pk_fe_args* a, void* stream) {
   k.seed_lo = (uint32_t)a->seed;
   k.seed_hi = (uint32_t)(a->seed >> 32);
   const int gx = a->max_frames > 0 ? (a->max_frames + kFeWaves - 1) / kFeWaves : 1;
-  hipLaunchKernelGGL(fe_kernel, dim3(gx, a->batch), dim3(64 * kFeWaves), 0, (hipStream_t)stream, k);
+  if (a->pcm_dtype == PK_PCM_S16)
+    hipLaunchKernelGGL(fe_kernel<PK_PCM_S16>, dim3(gx, a->batch), dim3(64 * kFeWaves), 0, (hipStream_t)stream, k);
+  else
+    hipLaunchKernelGGL(fe_kernel<PK_PCM_F32>, dim3(gx, a->batch), dim3(64 * kFeWaves), 0, (hipStream_t)stream, k);
   return check_launch("pk_fe_step");
 }
 
@@ -637,10 +835,10 @@ extern "C" int pk_subsample(const pk_sub_args* a, void* stream) {
   const int F3 = half_up(half_up(half_up(a->n_mels)));
   switch (a->dtype) {
     case PK_DTYPE_F16:
-      return F3 <= 11 ? launch_sub<_Float16, 11>(a, st) : launch_sub<_Float16, 9>(a, st);
+      return F3 <= 11 ? launch_sub_c<_Float16, 11>(a, st) : launch_sub_c<_Float16, 9>(a, st);
     case PK_DTYPE_BF16:
-      return F3 <= 11 ? launch_sub<bf16_t, 11>(a, st) : launch_sub<bf16_t, 9>(a, st);
+      return F3 <= 11 ? launch_sub_c<bf16_t, 11>(a, st) : launch_sub_c<bf16_t, 9>(a, st);
     default:
-      return launch_sub<float, 6>(a, st);
+      return launch_sub_c<float, 6>(a, st);
   }
 }
