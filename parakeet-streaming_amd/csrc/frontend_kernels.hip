@@ -443,13 +443,14 @@ __global__ void __launch_bounds__(kSubThreads) subsample_kernel(const SubK<ST> p
   // loads are unconditional, from clamped addresses, so none waits in a branch.
   constexpr int kWPer = (C * 9 + kSubThreads - 1) / kSubThreads;
   constexpr int kXPer = (G::XR * G::XC + kSubThreads - 1) / kSubThreads;
-  ST w0r[kWPer], w2r[kWPer], w5r[kWPer];
+  ST w0r[kWPer], w2r[kWPer], w5r[kWPer], brs0[kWPer];
 #pragma unroll
   for (int u = 0; u < kWPer; ++u) {
     const int i = min(tid + u * kSubThreads, C * 9 - 1);
     w0r[u] = p.w0[i];
     w2r[u] = p.w2[i];
     w5r[u] = p.w5[i];
+    brs0[u] = (p.b0 ? p.b0 : p.w0)[i / 9];  // conv.0 bias of the channel whose tap 0 this is
   }
   ST brs[5];
   {
@@ -489,6 +490,7 @@ __global__ void __launch_bounds__(kSubThreads) subsample_kernel(const SubK<ST> p
     if (i < C * 9) {
       const int c = i / 9, k = i - c * 9;
       w0p[c * G::KP + k] = w0r[u];
+      if (k == 0) w0p[c * G::KP + 9] = p.b0 ? brs0[u] : to_st<ST>(0.f);  // bias against the im2col's 1
       w2t[k * C + c] = w2r[u];
       w5t[k * C + c] = w5r[u];
     }
@@ -510,16 +512,15 @@ __global__ void __launch_bounds__(kSubThreads) subsample_kernel(const SubK<ST> p
 #pragma unroll
   for (int u = 0; u < G::T1W; ++u) {
     const int m = (wave + kSubWaves * u) * 16 + lr;
+    const int mm = min(m, G::M1 - 1);
+    const int i = mm / G::A1C, q = mm - i * G::A1C;
     Chunk<ST> ch;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
       const int tap = VEC * lg + e;
-      float v = 0.f;
-      if (tap < 9 && m < G::M1) {
-        const int i = m / G::A1C, q = m - i * G::A1C;
-        v = from_st(xin[(2 * i + tap / 3) * G::XC + 2 * q + tap % 3]);
-      }
-      ch.v[e] = to_st<ST>(v);
+      const int tc = min(tap, 8);
+      const ST v = xin[(2 * i + tc / 3) * G::XC + 2 * q + tc % 3];
+      ch.v[e] = (tap < 9 && m < G::M1) ? v : to_st<ST>(tap == 9 ? 1.f : 0.f);
     }
     a0[u] = __builtin_bit_cast(u32x4, ch);
   }
@@ -542,50 +543,62 @@ __global__ void __launch_bounds__(kSubThreads) subsample_kernel(const SubK<ST> p
 #pragma unroll
     for (int nt = 0; nt < kCG / 16; ++nt)
       aw[nt] = *reinterpret_cast<const u32x4*>(&w0p[(cg + nt * 16 + lr) * G::KP + VEC * lg]);
+    f32x4_t d[G::T1W][kCG / 16];
+#pragma unroll
+    for (int u = 0; u < G::T1W; ++u)
+#pragma unroll
+      for (int nt = 0; nt < kCG / 16; ++nt)
+        d[u][nt] = wave + kSubWaves * u < G::T1 ? MmaK<ST>::step(aw[nt], a0[u], f32x4_t{0.f, 0.f, 0.f, 0.f})
+                                                 : f32x4_t{0.f, 0.f, 0.f, 0.f};
+    // the bias came in through tap 9; ReLU before the one rounding to the
+    // storage type is the same as after it
 #pragma unroll
     for (int u = 0; u < G::T1W; ++u) {
       const int mt = wave + kSubWaves * u;
-      if (mt >= G::T1) break;
+      if (mt < G::T1) {
 #pragma unroll
-      for (int nt = 0; nt < kCG / 16; ++nt) {
-        const f32x4_t d = MmaK<ST>::step(aw[nt], a0[u], f32x4_t{0.f, 0.f, 0.f, 0.f});
-        const float4 bias = *reinterpret_cast<const float4*>(&bsm[0][cg + nt * 16 + 4 * lg]);
-        float v[4] = {d[0] + bias.x, d[1] + bias.y, d[2] + bias.z, d[3] + bias.w};
+        for (int nt = 0; nt < kCG / 16; ++nt) {
+          float v[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = ok1[u] ? fmaxf(round_to<ST>(v[e]), 0.f) : 0.f;
-        store4<ST>(&a1[(mt * 16 + lr) * G::A1S + nt * 16 + 4 * lg], v);
+          for (int e = 0; e < 4; ++e) v[e] = ok1[u] ? fmaxf(d[u][nt][e], 0.f) : 0.f;
+          store4<ST>(&a1[(mt * 16 + lr) * G::A1S + nt * 16 + 4 * lg], v);
+        }
       }
     }
     __syncthreads();
-    // first depthwise conv for the group -> a2p [M2][RS], one 16-byte chunk of
-    // channels per item
-    constexpr int kGC = kCG / VEC;  // chunks per group
-    for (int it = tid; it < G::M2 * kGC; it += kSubThreads) {
-      const int m = it / kGC, cc = (it - m * kGC) * VEC;
-      const int si = m / G::A2C, pp = m - si * G::A2C;
-      float acc[VEC];
-      {
-        const float4* bb = reinterpret_cast<const float4*>(&bsm[1][cg + cc]);
+    // first depthwise conv for the group -> a2p [M2][RS]: a thread owns one
+    // 16-byte chunk of channels (weights held in registers) and positions
+    // m, m + kPS, ...
+    {
+      constexpr int kGC = kCG / VEC;              // chunks per group
+      constexpr int kPS = kSubThreads / kGC;      // positions per sweep
+      const int cc = (tid % kGC) * VEC;
+      float w[9][VEC], bias[VEC];
 #pragma unroll
-        for (int e = 0; e < VEC; e += 4) {
-          const float4 x = bb[e / 4];
-          acc[e] = x.x;
-          acc[e + 1] = x.y;
-          acc[e + 2] = x.z;
-          acc[e + 3] = x.w;
+      for (int k = 0; k < 9; ++k) Tr<ST>::unpack(*reinterpret_cast<const u32x4*>(&w2t[k * C + cg + cc]), w[k]);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) bias[e] = bsm[1][cg + cc + e];
+#pragma unroll
+      for (int m0 = 0; m0 < G::M2; m0 += kPS) {
+        const int m = m0 + tid / kGC;
+        if (m < G::M2) {
+          const int si = m / G::A2C, pp = m - si * G::A2C;
+          float acc[VEC];
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) acc[e] = bias[e];
+#pragma unroll
+          for (int kt = 0; kt < 3; ++kt)
+#pragma unroll
+            for (int kf = 0; kf < 3; ++kf) {
+              float a[VEC];
+              Tr<ST>::unpack(
+                  *reinterpret_cast<const u32x4*>(&a1[((2 * si + kt) * G::A1C + 2 * pp + kf) * G::A1S + cc]), a);
+#pragma unroll
+              for (int e = 0; e < VEC; ++e) acc[e] += w[kt * 3 + kf][e] * a[e];
+            }
+          *reinterpret_cast<u32x4*>(&a2p[m * G::RS + cg + cc]) = Tr<ST>::pack(acc);
         }
       }
-#pragma unroll
-      for (int kt = 0; kt < 3; ++kt)
-#pragma unroll
-        for (int kf = 0; kf < 3; ++kf) {
-          float a[VEC], w[VEC];
-          Tr<ST>::unpack(*reinterpret_cast<const u32x4*>(&a1[((2 * si + kt) * G::A1C + 2 * pp + kf) * G::A1S + cc]), a);
-          Tr<ST>::unpack(*reinterpret_cast<const u32x4*>(&w2t[(kt * 3 + kf) * C + cg + cc]), w);
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) acc[e] += w[e] * a[e];
-        }
-      *reinterpret_cast<u32x4*>(&a2p[m * G::RS + cg + cc]) = Tr<ST>::pack(acc);
     }
     __syncthreads();
   }
@@ -629,7 +642,7 @@ __global__ void __launch_bounds__(kSubThreads) subsample_kernel(const SubK<ST> p
           float v[4] = {acc[mt][h][0] + bias.x, acc[mt][h][1] + bias.y, acc[mt][h][2] + bias.z,
                         acc[mt][h][3] + bias.w};
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = ok ? fmaxf(round_to<ST>(v[e]), 0.f) : 0.f;
+          for (int e = 0; e < 4; ++e) v[e] = ok ? fmaxf(v[e], 0.f) : 0.f;
           store4<ST>(&a2[m * G::RS + c0], v);
         }
       }
@@ -686,7 +699,7 @@ __global__ void __launch_bounds__(kSubThreads) subsample_kernel(const SubK<ST> p
         const float4 bias = *reinterpret_cast<const float4*>(&bsm[4][c0]);
         const float bv[4] = {bias.x, bias.y, bias.z, bias.w};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) ot[(c0 + e) * QT + lr] = to_st<ST>(fmaxf(round_to<ST>(acc[h][e] + bv[e]), 0.f));
+        for (int e = 0; e < 4; ++e) ot[(c0 + e) * QT + lr] = to_st<ST>(fmaxf(acc[h][e] + bv[e], 0.f));
       }
     }
   }
