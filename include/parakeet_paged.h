@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define PK_ABI_VERSION 5
+#define PK_ABI_VERSION 6
 
 enum pk_dtype { PK_DTYPE_F32 = 0, PK_DTYPE_F16 = 1, PK_DTYPE_BF16 = 2 };
 
@@ -419,6 +419,79 @@ typedef struct pk_sub_args {
   int32_t max_out;
 } pk_sub_args;
 int pk_subsample(const pk_sub_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * pk_rnnt_greedy_step -- one greedy RNNT decoding step for a batch of streams
+ * whose predictor state (LSTM h and c of every layer, and the predictor's joint
+ * projection) lives on the device in slots.  For each encoder frame t <
+ * lengths[b] and up to max_symbols decisions per frame:
+ *   logits = W_out relu(enc_proj[b, t] + pred_proj[slot]) + b_out, each rounded
+ *   to `dtype`; the decision is the first maximum.  A blank ends the frame; a
+ *   token is appended to tokens[b] and advances the predictor: x = embed[token],
+ *   per layer gates = W_ih x + W_hh h + b_ih + b_hh (i, f, g, o),
+ *   c' = sig(f) c + sig(i) tanh(g), h' = sig(o) tanh(c') (h', c' rounded to
+ *   `dtype`), then pred_proj = W_pred h'_top + b_pred.
+ * The whole step is issued from the host with no synchronisation; workgroups
+ * whose streams are done for the frame return at once.  Replaces
+ *   ModelRunner._decode_batch / _decode_frame_batch / _stack_states /
+ *       _unstack_states parakeet/engine/model_runner.py:347-484 (the per-symbol
+ *       `.all()` and `.tolist()` synchronisations and the state copies);
+ *   Predictor.forward parakeet/modules/decoder.py:44-50 and Joiner.forward
+ *       decoder.py:82-86 (dropout is the identity at inference);
+ *   with prime != 0: the predictor run on the blank start token from zero state
+ *       in ModelRunner.create_sequence model_runner.py:70-77 (no frames are read).
+ *
+ * slots      : int32 [batch] device, distinct, < num_slots.
+ * embed      : [vocab1][hidden] (nn.Embedding, vocab1 = vocabulary + blank).
+ * w_ih, w_hh : [layers][4*hidden][hidden]; b_ih, b_hh: [layers][4*hidden]
+ *              (nn.LSTM weight_ih_l*, ... stacked over layers).
+ * w_pred, b_pred: [joint][hidden], [joint]; w_out, b_out: [vocab1][joint], [vocab1].
+ * h, c       : [num_slots][layers][hidden]; pred_proj: [num_slots][joint].
+ * enc_proj   : [batch][frames][joint] Joiner.enc of the step's encoder frames,
+ *              element strides (stride_b, stride_t), rows 16-byte aligned.
+ * lengths    : int32 [batch] frames of each stream (<= max_frames).
+ * tokens     : int32 [batch][max_frames * max_symbols] out: the emitted tokens;
+ *              frame_counts: int32 [batch][max_frames] out: tokens per frame.
+ * workspace  : device bytes, at least pk_rnnt_workspace_bytes(...), 16-aligned.
+ * One dtype for every floating tensor; fp32 accumulation.  hidden must be 640
+ * (both reference models, config.py:19-21); joint a multiple of 64, <= 1024.
+ */
+typedef struct pk_rnnt_args {
+  int32_t dtype;
+  int32_t device;
+  int32_t batch;
+  const int32_t* slots;
+  int32_t num_slots;
+  int32_t layers;
+  int32_t hidden;
+  int32_t joint;
+  int32_t vocab1;
+  int32_t blank;
+  int32_t max_symbols;
+  int32_t prime;
+  const void* embed;
+  const void* w_ih;
+  const void* w_hh;
+  const void* b_ih;
+  const void* b_hh;
+  const void* w_pred;
+  const void* b_pred;
+  const void* w_out;
+  const void* b_out;
+  void* h;
+  void* c;
+  void* pred_proj;
+  const void* enc_proj;
+  int64_t enc_stride_b;
+  int64_t enc_stride_t;
+  const int32_t* lengths;
+  int32_t max_frames;
+  int32_t* tokens;
+  int32_t* frame_counts;
+  void* workspace;
+} pk_rnnt_args;
+int64_t pk_rnnt_workspace_bytes(int32_t dtype, int32_t batch, int32_t vocab1, int32_t layers, int32_t hidden);
+int pk_rnnt_greedy_step(const pk_rnnt_args* args, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Host page pool: FIFO free-page queue and per-slot page rings.  Thread safe

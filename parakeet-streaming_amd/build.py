@@ -65,7 +65,7 @@ def build(verbose: bool = False) -> Path:
     inc = [f"-I{INCLUDE}", f"-I{CSRC}"]
     objs: list[Path] = []
 
-    for name in ("paged_kernels.hip", "conv_kernels.hip", "frontend_kernels.hip"):
+    for name in ("paged_kernels.hip", "conv_kernels.hip", "frontend_kernels.hip", "decode_kernels.hip"):
         obj = BUILD_DIR / (Path(name).stem + ".o")
         _run([HIPCC, *HIP_FLAGS, *inc, "-x", "hip", "-c", str(CSRC / name), "-o", str(obj)], verbose)
         objs.append(obj)

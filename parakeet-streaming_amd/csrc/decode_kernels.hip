@@ -1,0 +1,476 @@
+// gfx950 kernels of batched RNNT greedy decoding with the predictor state of
+// every stream on the device (parakeet/engine/model_runner.py:306-447,
+// parakeet/modules/decoder.py:5-86).
+//
+// One decode step for a batch runs, for each encoder frame t and each symbol
+// s < max_symbols, four launches with no host synchronisation:
+//   joint_kernel     hid = relu(enc_proj[b, t] + pred_proj[slot]) (rounded to the
+//                    storage type), logits = W_out hid + b_out (rounded), and the
+//                    first maximum over a tile of 128 vocabulary rows: MFMA with
+//                    W_out rows as A (rows = vocabulary entries) and hid as B
+//                    (columns = 16 streams).  Workgroups whose streams are all
+//                    done for the frame return at once -- the reference's
+//                    "every decision blank" break, per workgroup.
+//   select_kernel    the first maximum over the tiles; a blank ends the stream's
+//                    frame, a token is appended and marks the stream for the
+//                    predictor update.
+//   lstm_kernel      per layer: gates = W_ih x + W_hh h + b_ih + b_hh as MFMA over
+//                    K = [x ; h] (x = embedding of the token, or the layer below),
+//                    then c' = sig(f) c + sig(i) tanh(g), h' = sig(o) tanh(c') for
+//                    16 hidden units x SPW streams per workgroup; streams not
+//                    marked keep their state.  Every workgroup reads all of a
+//                    stream's h, so h' goes to a per-batch scratch; c is read and
+//                    written by one thread per element, in place.
+//   pred_kernel      pred_proj[slot] = W_pred h'_top + b_pred for the marked
+//                    streams, and h' copied from the scratch into the slot state
+//                    (this launch runs after every read of the old h).
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "pk_common.h"
+#include "pk_device.h"
+
+namespace pk {
+
+template <typename ST>
+struct MmaR;
+template <>
+struct MmaR<_Float16> {
+  typedef _Float16 H8 __attribute__((ext_vector_type(8)));
+  __device__ static inline f32x4_t step(u32x4 a, u32x4 b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(H8, a), __builtin_bit_cast(H8, b), c, 0,
+                                                  0, 0);
+  }
+};
+template <>
+struct MmaR<bf16_t> {
+  typedef __bf16 H8 __attribute__((ext_vector_type(8)));
+  __device__ static inline f32x4_t step(u32x4 a, u32x4 b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(H8, a), __builtin_bit_cast(H8, b), c, 0,
+                                                   0, 0);
+  }
+};
+template <>
+struct MmaR<float> {
+  __device__ static inline f32x4_t step(u32x4 a, u32x4 b, f32x4_t c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.x), __uint_as_float(b.x), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.y), __uint_as_float(b.y), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.z), __uint_as_float(b.z), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.w), __uint_as_float(b.w), c, 0, 0, 0);
+    return c;
+  }
+};
+
+constexpr int kVT = 128;      // vocabulary rows per joint workgroup
+constexpr int kMaxDim = 1024;  // hidden / joint sizes held in LDS
+// per-stream words of the step workspace: flag, token, emitted count, pad
+constexpr int kWsHead = 4;
+
+struct DecK {
+  int32_t batch, num_slots, layers, H, J, V1, blank, max_symbols, t, s, vtiles, max_frames;
+  const int32_t* slots;
+  const int32_t* lengths;
+  const void* embed;
+  const void *w_ih, *w_hh, *b_ih, *b_hh;
+  const void *w_pred, *b_pred, *w_out, *b_out;
+  void* h;   // [num_slots][layers][H]
+  void* hn;  // [batch][layers][H] scratch: this iteration's new h
+  void* c;
+  void* pred_proj;  // [num_slots][J]
+  const void* enc;  // [batch][.. frames][J] enc projections
+  int64_t enc_sb, enc_st;
+  int32_t* tokens;        // [batch][max_frames * max_symbols]
+  int32_t* frame_counts;  // [batch][max_frames]
+  int32_t* ws;            // [batch][kWsHead + 2 * vtiles]
+  int32_t layer;
+  int32_t prime;
+};
+
+// stream state words in the workspace
+__device__ static inline int32_t* ws_of(const DecK& p, int b) { return p.ws + (int64_t)b * (kWsHead + 2 * p.vtiles); }
+
+// A stream decides at (t, s) while t is one of its frames and it has not yet
+// decided blank in frame t (word 0 of its workspace: 1 = blank seen).
+__device__ static inline bool active_at(const DecK& p, int b, const int32_t* w) {
+  return b < p.batch && p.t < p.lengths[b] && (p.s == 0 || w[0] == 0);
+}
+
+// ---------------------------------------------------------------------------
+template <typename ST>
+__global__ void __launch_bounds__(512) joint_kernel(const DecK p) {
+  constexpr int VEC = 16 / sizeof(ST);
+  __shared__ __align__(16) ST hid[16][kMaxDim + 8];
+  __shared__ float bv[8][16];
+  __shared__ int bi[8][16];
+  const int vt = blockIdx.x, b0 = blockIdx.y * 16;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
+  bool any = false;
+  for (int k = 0; k < 16; ++k) any |= active_at(p, b0 + k, ws_of(p, min(b0 + k, p.batch - 1)));
+  if (!any) return;  // uniform: every stream of the tile is done for this frame
+  // hid for the 16 streams (zero for streams not deciding)
+  const int J = p.J, nch = J / VEC;
+  for (int i = tid; i < 16 * nch; i += 512) {
+    const int k = i / nch, cc = (i - k * nch) * VEC;
+    const int b = b0 + k;
+    float out[VEC];
+    if (b < p.batch && active_at(p, b, ws_of(p, b))) {
+      float e[VEC], q[VEC];
+      Tr<ST>::unpack(ld16((const ST*)p.enc + b * p.enc_sb + (int64_t)p.t * p.enc_st + cc), e);
+      Tr<ST>::unpack(ld16((const ST*)p.pred_proj + (int64_t)p.slots[b] * J + cc), q);
+#pragma unroll
+      for (int u = 0; u < VEC; ++u) out[u] = fmaxf(round_to<ST>(e[u] + q[u]), 0.f);
+    } else {
+#pragma unroll
+      for (int u = 0; u < VEC; ++u) out[u] = 0.f;
+    }
+    *reinterpret_cast<u32x4*>(&hid[k][cc]) = Tr<ST>::pack(out);
+  }
+  __syncthreads();
+  // logits of rows vt*128 + 16*wave .. for the 16 streams
+  const int r = vt * kVT + wave * 16 + lr;
+  const ST* wrow = (const ST*)p.w_out + (int64_t)min(r, p.V1 - 1) * J;
+  f32x4_t d = {0.f, 0.f, 0.f, 0.f};
+  const int ks = J / (4 * VEC);
+  for (int kk = 0; kk < ks; ++kk) {
+    const int k = kk * 4 * VEC + VEC * lg;
+    d = MmaR<ST>::step(ld16(wrow + k), *reinterpret_cast<const u32x4*>(&hid[lr][k]), d);
+  }
+  // lane holds rows 4*lg + i (of the wave's 16) for stream lr
+  float best = -INFINITY;
+  int bidx = 0x7fffffff;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = vt * kVT + wave * 16 + 4 * lg + i;
+    if (row < p.V1) {
+      const float v = round_to<ST>(d[i] + from_st(((const ST*)p.b_out)[row]));
+      if (v > best) {  // rows ascend: the first maximum wins ties
+        best = v;
+        bidx = row;
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 16; m < 64; m <<= 1) {
+    const float ov = __shfl_xor(best, m);
+    const int oi = __shfl_xor(bidx, m);
+    if (ov > best || (ov == best && oi < bidx)) {
+      best = ov;
+      bidx = oi;
+    }
+  }
+  if (lg == 0) {
+    bv[wave][lr] = best;
+    bi[wave][lr] = bidx;
+  }
+  __syncthreads();
+  if (tid < 16 && b0 + tid < p.batch) {
+    float v = bv[0][tid];
+    int ix = bi[0][tid];
+    for (int w = 1; w < 8; ++w)
+      if (bv[w][tid] > v || (bv[w][tid] == v && bi[w][tid] < ix)) {
+        v = bv[w][tid];
+        ix = bi[w][tid];
+      }
+    int32_t* ws = ws_of(p, b0 + tid);
+    ws[kWsHead + 2 * vt] = __float_as_int(v);
+    ws[kWsHead + 2 * vt + 1] = ix;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// word 0: blank seen in the current frame; 1: token decided (-1: no update);
+// 2: tokens emitted this step
+__global__ void __launch_bounds__(256) select_kernel(const DecK p) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= p.batch) return;
+  int32_t* ws = ws_of(p, b);
+  if (p.t == 0 && p.s == 0) ws[2] = 0;
+  if (p.s == 0) {
+    ws[0] = 0;
+    if (p.t < p.max_frames) p.frame_counts[(int64_t)b * p.max_frames + p.t] = 0;
+  }
+  if (!active_at(p, b, ws)) {
+    ws[1] = -1;
+    return;
+  }
+  float v = __int_as_float(ws[kWsHead]);
+  int ix = ws[kWsHead + 1];
+  for (int k = 1; k < p.vtiles; ++k) {
+    const float ov = __int_as_float(ws[kWsHead + 2 * k]);
+    const int oi = ws[kWsHead + 2 * k + 1];
+    if (ov > v || (ov == v && oi < ix)) {
+      v = ov;
+      ix = oi;
+    }
+  }
+  if (ix == p.blank || ix < 0 || ix >= p.V1) {
+    ws[0] = 1;
+    ws[1] = -1;
+    return;
+  }
+  ws[1] = ix;
+  const int n = ws[2];
+  p.tokens[(int64_t)b * p.max_frames * p.max_symbols + n] = ix;
+  ws[2] = n + 1;
+  p.frame_counts[(int64_t)b * p.max_frames + p.t] += 1;
+}
+
+// ---------------------------------------------------------------------------
+template <typename ST>
+struct LstmCfg {
+  static constexpr int SPW = sizeof(ST) == 4 ? 16 : 32;  // streams per workgroup
+  static constexpr int WAVES = 4 * (SPW / 16);           // 4 gates x stream tiles
+  static constexpr int KMAX = 2 * kMaxDim;
+};
+
+template <typename ST>
+__global__ void __launch_bounds__(LstmCfg<ST>::WAVES * 64) lstm_kernel(const DecK p) {
+  typedef LstmCfg<ST> Cfg;
+  constexpr int VEC = 16 / sizeof(ST), SPW = Cfg::SPW;
+  constexpr int RS = 2 * 640 + VEC;  // [x ; h] row of one stream (hidden 640 in LDS)
+  __shared__ __align__(16) ST inp[SPW][RS];
+  __shared__ float gsm[4][SPW][17];
+  __shared__ int32_t tok_s[SPW];
+  const int H = p.H, L = p.layers, layer = p.layer;
+  const int u0 = blockIdx.x * 16, b0 = blockIdx.y * SPW;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
+  // which streams update: the select's token (prime: every stream, token blank)
+  if (tid < SPW) {
+    const int b = b0 + tid;
+    int tk = -1;
+    if (b < p.batch) tk = p.prime ? p.blank : ws_of(p, b)[1];
+    tok_s[tid] = tk;
+  }
+  __syncthreads();
+  bool any = false;
+  for (int k = 0; k < SPW; ++k) any |= tok_s[k] >= 0;
+  const int nch = H / VEC;
+  if (!any) return;  // uniform: no stream of the tile updates
+  // [x ; h] of each stream: x = embedding row of the token (layer 0) or the new
+  // h of the layer below; h = this layer's current h
+  for (int i = tid; i < SPW * 2 * nch; i += Cfg::WAVES * 64) {
+    const int k = i / (2 * nch), cc = (i - k * 2 * nch) * VEC;
+    const int b = b0 + k;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (b < p.batch && tok_s[k] >= 0) {
+      const int64_t slot = p.slots[b];
+      if (cc < H) {
+        if (layer == 0)
+          v = ld16((const ST*)p.embed + (int64_t)tok_s[k] * H + cc);
+        else
+          v = ld16((const ST*)p.hn + ((int64_t)b * L + layer - 1) * H + cc);
+      } else if (!p.prime) {  // a stream's first step starts from zero state
+        v = ld16((const ST*)p.h + (slot * L + layer) * H + cc - H);
+      }
+    }
+    *reinterpret_cast<u32x4*>(&inp[k][cc]) = v;
+  }
+  __syncthreads();
+  // gate gi rows gi*H + u0 .. +16 for stream tile sb
+  const int gi = wave & 3, sb = wave >> 2;
+  const int64_t row = (int64_t)layer * 4 * H + gi * H + u0 + lr;
+  const ST* wi = (const ST*)p.w_ih + row * H;
+  const ST* wh = (const ST*)p.w_hh + row * H;
+  f32x4_t d = {0.f, 0.f, 0.f, 0.f};
+  const int ks = H / (4 * VEC);
+  for (int kk = 0; kk < ks; ++kk) {
+    const int k = kk * 4 * VEC + VEC * lg;
+    d = MmaR<ST>::step(ld16(wi + k), *reinterpret_cast<const u32x4*>(&inp[sb * 16 + lr][k]), d);
+  }
+  for (int kk = 0; kk < ks; ++kk) {
+    const int k = kk * 4 * VEC + VEC * lg;
+    d = MmaR<ST>::step(ld16(wh + k), *reinterpret_cast<const u32x4*>(&inp[sb * 16 + lr][H + k]), d);
+  }
+  // lane: units u0 + 4*lg + i of gate gi, stream sb*16 + lr
+#pragma unroll
+  for (int i = 0; i < 4; ++i) gsm[gi][sb * 16 + lr][4 * lg + i] = d[i];
+  __syncthreads();
+  // cell update: thread -> (stream, unit)
+  for (int i = tid; i < SPW * 16; i += Cfg::WAVES * 64) {
+    const int k = i / 16, u = i % 16, b = b0 + k;
+    if (b >= p.batch || tok_s[k] < 0) continue;
+    const int64_t so = ((int64_t)p.slots[b] * L + layer) * H + u0 + u;
+    const int64_t bo = (int64_t)layer * 4 * H + u0 + u;
+    float g4[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      g4[q] = gsm[q][k][u] + from_st(((const ST*)p.b_ih)[bo + q * H]) + from_st(((const ST*)p.b_hh)[bo + q * H]);
+    const float ig = 1.f / (1.f + __expf(-g4[0])), fg = 1.f / (1.f + __expf(-g4[1]));
+    const float gg = tanhf(g4[2]), og = 1.f / (1.f + __expf(-g4[3]));
+    const float c0 = p.prime ? 0.f : from_st(((const ST*)p.c)[so]);
+    const float c1 = fg * c0 + ig * gg;
+    ((ST*)p.c)[so] = to_st<ST>(c1);
+    ((ST*)p.hn)[((int64_t)b * L + layer) * H + u0 + u] = to_st<ST>(og * tanhf(c1));
+  }
+}
+
+// ---------------------------------------------------------------------------
+template <typename ST>
+__global__ void __launch_bounds__(256) pred_kernel(const DecK p) {
+  constexpr int VEC = 16 / sizeof(ST);
+  __shared__ __align__(16) ST hs[16][kMaxDim + 8];
+  __shared__ int32_t tok_s[16];
+  const int H = p.H, J = p.J, L = p.layers;
+  const int j0 = blockIdx.x * 64, b0 = blockIdx.y * 16;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
+  if (tid < 16) {
+    const int b = b0 + tid;
+    tok_s[tid] = b < p.batch ? (p.prime ? 0 : ws_of(p, b)[1]) : -1;
+  }
+  __syncthreads();
+  bool any = false;
+  for (int k = 0; k < 16; ++k) any |= tok_s[k] >= 0;
+  if (!any) return;
+  const int nch = H / VEC;
+  for (int i = tid; i < 16 * nch; i += 256) {
+    const int k = i / nch, cc = (i - k * nch) * VEC, b = b0 + k;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (b < p.batch && tok_s[k] >= 0) v = ld16((const ST*)p.hn + ((int64_t)b * L + L - 1) * H + cc);
+    *reinterpret_cast<u32x4*>(&hs[k][cc]) = v;
+  }
+  // the new h of every layer into the slot state (one column of workgroups)
+  if (blockIdx.x == 0) {
+    for (int i = tid; i < 16 * L * nch; i += 256) {
+      const int k = i / (L * nch), r = i - k * L * nch, b = b0 + k;
+      if (b < p.batch && tok_s[k] >= 0) {
+        const int l = r / nch, cc = (r - l * nch) * VEC;
+        st16((ST*)p.h + ((int64_t)p.slots[b] * L + l) * H + cc, ld16((const ST*)p.hn + ((int64_t)b * L + l) * H + cc));
+      }
+    }
+  }
+  __syncthreads();
+  const int j = j0 + wave * 16 + lr;
+  if (j0 + wave * 16 >= J) return;  // uniform per wave; no barrier below
+  const ST* wrow = (const ST*)p.w_pred + (int64_t)j * H;
+  f32x4_t d = {0.f, 0.f, 0.f, 0.f};
+  for (int kk = 0; kk < H / (4 * VEC); ++kk) {
+    const int k = kk * 4 * VEC + VEC * lg;
+    d = MmaR<ST>::step(ld16(wrow + k), *reinterpret_cast<const u32x4*>(&hs[lr][k]), d);
+  }
+  // lane: outputs j0 + 16 wave + 4 lg + i for stream lr
+  const int b = b0 + lr;
+  if (b < p.batch && tok_s[lr] >= 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int jj = j0 + wave * 16 + 4 * lg + i;
+      ((ST*)p.pred_proj)[(int64_t)p.slots[b] * J + jj] =
+          to_st<ST>(d[i] + from_st(((const ST*)p.b_pred)[jj]));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+static int64_t ws_int_bytes(int batch, int vocab1) {
+  const int64_t b = (int64_t)batch * (kWsHead + 2 * ((vocab1 + kVT - 1) / kVT)) * 4;
+  return (b + 255) / 256 * 256;
+}
+
+template <typename ST>
+static int run_step(const pk_rnnt_args* a, hipStream_t st) {
+  DecK k{};
+  k.batch = a->batch;
+  k.num_slots = a->num_slots;
+  k.layers = a->layers;
+  k.H = a->hidden;
+  k.J = a->joint;
+  k.V1 = a->vocab1;
+  k.blank = a->blank;
+  k.max_symbols = a->max_symbols;
+  k.vtiles = (a->vocab1 + kVT - 1) / kVT;
+  k.max_frames = a->max_frames;
+  k.slots = a->slots;
+  k.lengths = a->lengths;
+  k.embed = a->embed;
+  k.w_ih = a->w_ih;
+  k.w_hh = a->w_hh;
+  k.b_ih = a->b_ih;
+  k.b_hh = a->b_hh;
+  k.w_pred = a->w_pred;
+  k.b_pred = a->b_pred;
+  k.w_out = a->w_out;
+  k.b_out = a->b_out;
+  k.c = a->c;
+  k.pred_proj = a->pred_proj;
+  k.enc = a->enc_proj;
+  k.enc_sb = a->enc_stride_b;
+  k.enc_st = a->enc_stride_t;
+  k.tokens = a->tokens;
+  k.frame_counts = a->frame_counts;
+  k.ws = (int32_t*)a->workspace;
+  k.hn = (char*)a->workspace + ws_int_bytes(a->batch, a->vocab1);
+  k.h = a->h;
+  k.prime = a->prime;
+  const dim3 gj(k.vtiles, (a->batch + 15) / 16), gs((a->batch + 255) / 256);
+  const dim3 gl(a->hidden / 16, (a->batch + LstmCfg<ST>::SPW - 1) / LstmCfg<ST>::SPW);
+  const dim3 gp((a->joint + 63) / 64, (a->batch + 15) / 16);
+  auto predictor = [&]() {
+    for (int l = 0; l < a->layers; ++l) {
+      k.layer = l;
+      hipLaunchKernelGGL(lstm_kernel<ST>, gl, dim3(LstmCfg<ST>::WAVES * 64), 0, st, k);
+    }
+    hipLaunchKernelGGL(pred_kernel<ST>, gp, dim3(256), 0, st, k);
+  };
+  if (a->prime) {
+    k.t = k.s = 0;
+    predictor();
+  } else {
+    for (int t = 0; t < a->max_frames; ++t)
+      for (int s = 0; s < a->max_symbols; ++s) {
+        k.t = t;
+        k.s = s;
+        hipLaunchKernelGGL(joint_kernel<ST>, gj, dim3(512), 0, st, k);
+        hipLaunchKernelGGL(select_kernel, gs, dim3(256), 0, st, k);
+        predictor();
+      }
+  }
+  return check_launch("pk_rnnt_greedy_step");
+}
+
+}  // namespace pk
+
+using namespace pk;
+
+extern "C" int64_t pk_rnnt_workspace_bytes(int32_t dtype, int32_t batch, int32_t vocab1, int32_t layers,
+                                           int32_t hidden) {
+  if (batch < 0 || vocab1 < 1 || layers < 1 || hidden < 1) return -1;
+  const int es = dtype == PK_DTYPE_F32 ? 4 : 2;
+  return ws_int_bytes(batch, vocab1) + (int64_t)batch * layers * hidden * es;
+}
+
+extern "C" int pk_rnnt_greedy_step(const pk_rnnt_args* a, void* stream) {
+  clear_error();
+  if (!a) return fail(PK_ERR_INVALID, "pk_rnnt_greedy_step: args is NULL");
+  if (a->dtype != PK_DTYPE_F32 && a->dtype != PK_DTYPE_F16 && a->dtype != PK_DTYPE_BF16)
+    return fail(PK_ERR_INVALID, "pk_rnnt_greedy_step: dtype %d", a->dtype);
+  if (a->batch < 0 || a->max_frames < 0 || a->max_symbols < 1 || a->layers < 1 || a->num_slots < 1)
+    return fail(PK_ERR_INVALID, "pk_rnnt_greedy_step: bad batch/max_frames/max_symbols/layers/num_slots");
+  if (a->hidden != 640 || a->joint < 64 || a->joint > kMaxDim || a->joint % 64)
+    return fail(PK_ERR_UNSUPPORTED, "pk_rnnt_greedy_step: hidden %d (built: 640), joint %d (multiple of 64, <= %d)",
+                a->hidden, a->joint, kMaxDim);
+  if (a->vocab1 < 2 || a->blank < 0 || a->blank >= a->vocab1)
+    return fail(PK_ERR_INVALID, "pk_rnnt_greedy_step: vocab1 %d, blank %d", a->vocab1, a->blank);
+  if (a->batch == 0 || (!a->prime && a->max_frames == 0)) return PK_OK;
+  if (a->batch > 65535 * 16) return fail(PK_ERR_UNSUPPORTED, "pk_rnnt_greedy_step: batch %d", a->batch);
+  if (!a->slots || !a->embed || !a->w_ih || !a->w_hh || !a->b_ih || !a->b_hh || !a->w_pred || !a->b_pred ||
+      !a->w_out || !a->b_out || !a->h || !a->c || !a->pred_proj || !a->workspace ||
+      (!a->prime && (!a->enc_proj || !a->lengths || !a->tokens || !a->frame_counts)))
+    return fail(PK_ERR_INVALID, "pk_rnnt_greedy_step: NULL pointer");
+  const void* vecs[] = {a->embed, a->w_ih, a->w_hh, a->w_pred, a->w_out, a->h, a->c, a->pred_proj, a->enc_proj};
+  for (const void* v : vecs)
+    if (v && !aligned16(v)) return fail(PK_ERR_INVALID, "pk_rnnt_greedy_step: weights and state must be 16-byte aligned");
+  if (!aligned16(a->workspace)) return fail(PK_ERR_INVALID, "pk_rnnt_greedy_step: workspace must be 16-byte aligned");
+  if (!a->prime && (a->enc_stride_b % 8 || a->enc_stride_t % 8))
+    return fail(PK_ERR_INVALID, "pk_rnnt_greedy_step: enc_proj strides must keep 16-byte rows");
+  DeviceGuard dg(a->device);
+  if (!dg.ok) return fail(PK_ERR_HIP, "pk_rnnt_greedy_step: cannot select device %d", a->device);
+  switch (a->dtype) {
+    case PK_DTYPE_F16:
+      return run_step<_Float16>(a, (hipStream_t)stream);
+    case PK_DTYPE_BF16:
+      return run_step<bf16_t>(a, (hipStream_t)stream);
+    default:
+      return run_step<float>(a, (hipStream_t)stream);
+  }
+}

@@ -15,7 +15,7 @@ from pathlib import Path
 LIB_NAME = "libparakeet_paged.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -254,6 +254,43 @@ class SubArgs(ctypes.Structure):
     ]
 
 
+class RnntArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", c_int32),
+        ("device", c_int32),
+        ("batch", c_int32),
+        ("slots", c_void_p),
+        ("num_slots", c_int32),
+        ("layers", c_int32),
+        ("hidden", c_int32),
+        ("joint", c_int32),
+        ("vocab1", c_int32),
+        ("blank", c_int32),
+        ("max_symbols", c_int32),
+        ("prime", c_int32),
+        ("embed", c_void_p),
+        ("w_ih", c_void_p),
+        ("w_hh", c_void_p),
+        ("b_ih", c_void_p),
+        ("b_hh", c_void_p),
+        ("w_pred", c_void_p),
+        ("b_pred", c_void_p),
+        ("w_out", c_void_p),
+        ("b_out", c_void_p),
+        ("h", c_void_p),
+        ("c", c_void_p),
+        ("pred_proj", c_void_p),
+        ("enc_proj", c_void_p),
+        ("enc_stride_b", c_int64),
+        ("enc_stride_t", c_int64),
+        ("lengths", c_void_p),
+        ("max_frames", c_int32),
+        ("tokens", c_void_p),
+        ("frame_counts", c_void_p),
+        ("workspace", c_void_p),
+    ]
+
+
 # name -> (restype, argtypes); exactly the functions include/parakeet_paged.h declares
 SIGNATURES = {
     "pk_kv_append": (c_int, [POINTER(KvAppendArgs), c_void_p]),
@@ -263,6 +300,8 @@ SIGNATURES = {
     "pk_conv_step": (c_int, [POINTER(ConvArgs), c_void_p]),
     "pk_fe_step": (c_int, [POINTER(FeArgs), c_void_p]),
     "pk_subsample": (c_int, [POINTER(SubArgs), c_void_p]),
+    "pk_rnnt_workspace_bytes": (c_int64, [c_int32, c_int32, c_int32, c_int32, c_int32]),
+    "pk_rnnt_greedy_step": (c_int, [POINTER(RnntArgs), c_void_p]),
     "pk_pool_create": (
         c_int,
         [c_int32, c_int32, c_int32, c_int32, c_int32, POINTER(c_int32), POINTER(c_void_p)],

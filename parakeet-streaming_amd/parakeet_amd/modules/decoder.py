@@ -1,0 +1,193 @@
+"""Batched RNNT greedy decoding on the GPU, the predictor state of every stream
+kept on the device by slot.
+
+* :class:`Predictor`, :class:`Joiner` -- the parameter structure of
+  parakeet/modules/decoder.py:5-86 (same constructors and state-dict names), so
+  a reference checkpoint loads.  Their per-call forwards are not the decoding
+  path here: the greedy loop runs in :class:`GreedyDecoder`.
+* :class:`GreedyDecoder` -- ModelRunner._decode_batch / _decode_frame_batch
+  (parakeet/engine/model_runner.py:347-447) for a batch: one ``enc`` GEMM for the
+  step's frames, then ``pk_rnnt_greedy_step`` issues the whole per-frame,
+  per-symbol loop with no host synchronisation; the tokens come back in one copy.
+  ``reset_slot`` is create_sequence's predictor start state (model_runner.py:70-77).
+
+There is no CPU path: without the HIP library the calls raise.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+from torch import Tensor, nn
+from torch.nn import functional as F
+
+from .. import _lib, ops
+from .._lib import RnntArgs, check, lib
+
+
+class Predictor(nn.Module):
+    """decoder.py:5-42: embedding (blank = padding row) and an LSTM."""
+
+    def __init__(self, pred_dim: int, hidden_dim: int, num_layers: int, vocab_size: int):
+        super().__init__()
+        self.prediction = nn.ModuleDict(
+            {
+                "embed": nn.Embedding(vocab_size + 1, pred_dim, padding_idx=vocab_size),
+                "dec_rnn": nn.LSTM(input_size=pred_dim, hidden_size=hidden_dim, num_layers=num_layers),
+            }
+        )
+        self.pred_dim = pred_dim
+        self.num_layers = num_layers
+
+    def init_state(self, batch_size: int):
+        p = next(self.parameters())
+        z = torch.zeros(self.num_layers, batch_size, self.pred_dim, device=p.device, dtype=p.dtype)
+        return (z, z.clone())
+
+
+class Joiner(nn.Module):
+    """decoder.py:53-80: enc / pred projections, ReLU, dropout, output layer."""
+
+    def __init__(self, encoder_dim, pred_dim, joint_dim, dropout: float = 0.2, num_classes: int = 1024):
+        super().__init__()
+        self._vocab_size = num_classes
+        self._num_classes = num_classes + 1
+        self.encoder_dim, self.pred_dim, self.joint_dim, self.dropout = encoder_dim, pred_dim, joint_dim, dropout
+        self.pred = nn.Linear(pred_dim, joint_dim)
+        self.enc = nn.Linear(encoder_dim, joint_dim)
+        self.joint_net = nn.Sequential(nn.ReLU(inplace=True), nn.Dropout(p=dropout), nn.Linear(joint_dim, num_classes + 1))
+
+
+class GreedyDecoder:
+    """Greedy RNNT decoding of many streams at once (model_runner.py:306-447).
+
+    ``predictor`` / ``joiner``: modules with the reference's parameter names
+    (this package's or the reference's own).  State per slot on ``device``: LSTM h
+    and c [slots, layers, hidden] and the predictor's joint projection
+    [slots, joint], in the modules' dtype."""
+
+    def __init__(self, predictor: nn.Module, joiner: nn.Module, blank_id: int, num_slots: int, max_symbols: int = 5):
+        self.pred, self.joiner = predictor, joiner
+        self.blank, self.max_symbols = int(blank_id), int(max_symbols)
+        self.num_slots = S = int(num_slots)
+        lstm = predictor.prediction["dec_rnn"]
+        embed = predictor.prediction["embed"]
+        self.layers, self.hidden = lstm.num_layers, lstm.hidden_size
+        w = embed.weight
+        self.device, self.dtype = w.device, w.dtype
+        if self.device.type != "cuda":
+            raise RuntimeError("GreedyDecoder runs on a HIP device (there is no CPU implementation)")
+        self.vocab1 = int(w.shape[0])
+        self.joint = int(joiner.pred.weight.shape[0])
+        if not 0 <= self.blank < self.vocab1:
+            raise ValueError(f"blank id {self.blank} outside the vocabulary of {self.vocab1}")
+        self.refresh_weights()
+        L, H, J = self.layers, self.hidden, self.joint
+        self.h = torch.zeros((S, L, H), dtype=self.dtype, device=self.device)
+        self.c = torch.zeros((S, L, H), dtype=self.dtype, device=self.device)
+        self.pred_proj = torch.zeros((S, J), dtype=self.dtype, device=self.device)
+        self._ws: dict[int, torch.Tensor] = {}
+
+    def refresh_weights(self) -> None:
+        """Contiguous copies of the parameters in the layouts the kernels read
+        (LSTM weights stacked over layers); call after loading new weights."""
+        lstm = self.pred.prediction["dec_rnn"]
+        L = self.layers
+        with torch.no_grad():
+            g = lambda n: torch.stack([getattr(lstm, f"{n}_l{k}") for k in range(L)]).contiguous()
+            self.w_ih, self.w_hh, self.b_ih, self.b_hh = g("weight_ih"), g("weight_hh"), g("bias_ih"), g("bias_hh")
+            self.embed = self.pred.prediction["embed"].weight.detach().contiguous()
+            j = self.joiner
+            self.w_pred, self.b_pred = j.pred.weight.detach().contiguous(), j.pred.bias.detach().contiguous()
+            self.w_enc, self.b_enc = j.enc.weight.detach(), j.enc.bias.detach()
+            out = j.joint_net[-1]
+            self.w_out, self.b_out = out.weight.detach().contiguous(), out.bias.detach().contiguous()
+        if self.w_ih.shape[2] != self.hidden:
+            raise NotImplementedError("the predictor's embedding size must equal its hidden size (config.py:19)")
+        for t in (self.w_ih, self.w_hh, self.b_ih, self.b_hh, self.embed, self.w_pred, self.b_pred, self.w_out, self.b_out):
+            if t.dtype != self.dtype or t.device != self.device:
+                raise ValueError("predictor and joiner parameters must share one dtype and device")
+
+    def _workspace(self, batch: int) -> torch.Tensor:
+        n = int(lib().pk_rnnt_workspace_bytes(ops.dtype_code(self.dtype), batch, self.vocab1, self.layers, self.hidden))
+        ws = self._ws.get(batch)
+        if ws is None or ws.numel() < n:
+            ws = torch.empty(max(n, 256), dtype=torch.uint8, device=self.device)
+            self._ws[batch] = ws
+        return ws
+
+    def _args(self, slots: Tensor, prime: bool) -> RnntArgs:
+        a = RnntArgs()
+        a.dtype = ops.dtype_code(self.dtype)
+        a.device = self.device.index if self.device.index is not None else torch.cuda.current_device()
+        a.batch, a.slots, a.num_slots = int(slots.numel()), slots.data_ptr(), self.num_slots
+        a.layers, a.hidden, a.joint, a.vocab1 = self.layers, self.hidden, self.joint, self.vocab1
+        a.blank, a.max_symbols, a.prime = self.blank, self.max_symbols, int(prime)
+        a.embed, a.w_ih, a.w_hh = self.embed.data_ptr(), self.w_ih.data_ptr(), self.w_hh.data_ptr()
+        a.b_ih, a.b_hh = self.b_ih.data_ptr(), self.b_hh.data_ptr()
+        a.w_pred, a.b_pred = self.w_pred.data_ptr(), self.b_pred.data_ptr()
+        a.w_out, a.b_out = self.w_out.data_ptr(), self.b_out.data_ptr()
+        a.h, a.c, a.pred_proj = self.h.data_ptr(), self.c.data_ptr(), self.pred_proj.data_ptr()
+        a.workspace = self._workspace(a.batch).data_ptr()
+        return a
+
+    def _slots(self, slots) -> Tensor:
+        s = np.ascontiguousarray(np.asarray(slots, dtype=np.int32).reshape(-1))
+        if len(np.unique(s)) != len(s) or (len(s) and (s.min() < 0 or s.max() >= self.num_slots)):
+            raise ValueError(f"slots must be distinct and in [0, {self.num_slots})")
+        return torch.from_numpy(s).to(self.device)
+
+    def reset_slot(self, slots) -> None:
+        """A new stream on each of ``slots``: the predictor run on the blank start
+        token from zero state (model_runner.py:70-77)."""
+        st = self._slots(slots)
+        if st.numel() == 0:
+            return
+        a = self._args(st, prime=True)
+        check(lib().pk_rnnt_greedy_step(ctypes.byref(a), ops._stream(self.device)), "pk_rnnt_greedy_step")
+
+    def decode(self, slots, enc_out: Tensor, lengths=None, frame_tokens: bool = False):
+        """Greedy decoding of one step's encoder frames.
+
+        enc_out: [B, T, D] encoder output (frames of stream b in enc_out[b, :lengths[b]]);
+        lengths: frames per stream (None: all T).  Returns the emitted tokens of
+        each stream (``frame_tokens=True``: a list per frame)."""
+        st = self._slots(slots)
+        B = int(st.numel())
+        if enc_out.dim() != 3 or enc_out.shape[0] != B:
+            raise ValueError(f"enc_out must be [{B}, T, D]")
+        T = int(enc_out.shape[1])
+        if lengths is None:
+            lens = np.full(B, T, dtype=np.int32)
+        else:
+            lens = np.asarray(torch.as_tensor(lengths).cpu(), dtype=np.int32).reshape(-1)
+            if lens.shape != (B,) or (B and (lens.min() < 0 or lens.max() > T)):
+                raise ValueError(f"lengths must be [{B}] in [0, {T}]")
+        if B == 0 or T == 0:
+            return [[] for _ in range(B)]
+        with torch.no_grad():
+            e = F.linear(enc_out.to(self.dtype), self.w_enc, self.b_enc).contiguous()  # Joiner.enc (decoder.py:83)
+        tokens = torch.empty((B, T * self.max_symbols), dtype=torch.int32, device=self.device)
+        counts = torch.empty((B, T), dtype=torch.int32, device=self.device)
+        lens_d = torch.from_numpy(lens).to(self.device)
+        a = self._args(st, prime=False)
+        a.enc_proj, a.enc_stride_b, a.enc_stride_t = e.data_ptr(), e.stride(0), e.stride(1)
+        a.lengths, a.max_frames = lens_d.data_ptr(), T
+        a.tokens, a.frame_counts = tokens.data_ptr(), counts.data_ptr()
+        check(lib().pk_rnnt_greedy_step(ctypes.byref(a), ops._stream(self.device)), "pk_rnnt_greedy_step")
+        tok, cnt = tokens.cpu().numpy(), counts.cpu().numpy()  # the step's one synchronisation
+        out = []
+        for b in range(B):
+            n = cnt[b, : lens[b]]
+            flat = tok[b, : int(n.sum())].tolist()
+            if frame_tokens:
+                edges = np.concatenate([[0], np.cumsum(n)])
+                out.append([flat[edges[i] : edges[i + 1]] for i in range(len(n))])
+            else:
+                out.append(flat)
+        return out
+
+
+__all__ = ["Predictor", "Joiner", "GreedyDecoder"]

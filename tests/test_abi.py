@@ -61,6 +61,7 @@ def test_every_declared_symbol_is_exported_and_bound():
         ("pk_fe_args", _lib.FeArgs),
         ("pk_sub_stream", _lib.SubStream),
         ("pk_sub_args", _lib.SubArgs),
+        ("pk_rnnt_args", _lib.RnntArgs),
     ],
 )
 def test_struct_layout_matches_header(cname, pyclass):
@@ -77,6 +78,7 @@ def test_null_args_rejected_without_gpu():
     assert lib.pk_conv_step(None, None) == _lib.PK_ERR_INVALID
     assert lib.pk_fe_step(None, None) == _lib.PK_ERR_INVALID
     assert lib.pk_subsample(None, None) == _lib.PK_ERR_INVALID
+    assert lib.pk_rnnt_greedy_step(None, None) == _lib.PK_ERR_INVALID
 
 
 def test_mask_args_validated_before_launch():
@@ -138,3 +140,21 @@ def test_front_end_args_validated_before_launch():
     assert L.pk_subsample(ctypes.byref(s), None) == _lib.PK_ERR_INVALID
     s.feat_rows, s.dtype = 32, 9
     assert L.pk_subsample(ctypes.byref(s), None) == _lib.PK_ERR_INVALID
+
+
+def test_rnnt_args_validated_before_launch():
+    L = _lib.lib()
+    a = _lib.RnntArgs()
+    a.dtype, a.batch, a.num_slots, a.layers, a.hidden, a.joint = _lib.DTYPE_F16, 4, 8, 1, 640, 640
+    a.vocab1, a.blank, a.max_symbols, a.max_frames = 1027, 1026, 5, 2
+    assert L.pk_rnnt_greedy_step(ctypes.byref(a), None) == _lib.PK_ERR_INVALID  # NULL tensors
+    assert "NULL" in _lib.last_error()
+    a.hidden = 512
+    assert L.pk_rnnt_greedy_step(ctypes.byref(a), None) == _lib.PK_ERR_UNSUPPORTED
+    a.hidden, a.blank = 640, 1027  # blank outside the vocabulary
+    assert L.pk_rnnt_greedy_step(ctypes.byref(a), None) == _lib.PK_ERR_INVALID
+    a.blank, a.joint = 1026, 600  # joint not a multiple of 64
+    assert L.pk_rnnt_greedy_step(ctypes.byref(a), None) == _lib.PK_ERR_UNSUPPORTED
+    # workspace: per-stream words (4 + 2 x 9 vocabulary tiles) rounded to 256 B, then h'
+    assert L.pk_rnnt_workspace_bytes(_lib.DTYPE_F16, 128, 1027, 1, 640) == 11264 + 128 * 640 * 2
+    assert L.pk_rnnt_workspace_bytes(_lib.DTYPE_F32, 1, 1025, 2, 640) == 256 + 2 * 640 * 4

@@ -1,0 +1,133 @@
+"""Batched RNNT greedy decoding on the GPU (pk_rnnt_greedy_step) against the
+oracle (oracle/rnnt.py, pinned in test_oracle_rnnt.py).
+
+Decisions are argmaxes, so an implementation with other rounding may break a
+near-tie the other way.  The bar is per decision: the oracle replays the GPU's
+decisions (tokens per frame, then blank) at the same rounding points, and every
+decision's logit must be within 4 eps (|max logit| + rms(logits)) of the
+oracle's maximum, eps = 2^-10 fp16, 2^-7 bf16, 2^-17 fp32; at most 2% of the
+decisions may differ from the oracle's own argmax.  Predictor state after
+reset_slot: |got - ref| <= 4 eps (|ref| + rms).  Streams are independent of the
+batch they are decoded in (bit-exact), and slots outside a batch are untouched.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import rnnt
+from parakeet_amd.modules.decoder import GreedyDecoder, Joiner, Predictor
+
+pytestmark = pytest.mark.gpu
+
+EPS = {torch.float16: 2.0**-10, torch.bfloat16: 2.0**-7, torch.float32: 2.0**-17}
+
+
+def _model(vocab, enc_dim, layers, dt, cuda, seed, blank_bias=1.5, out_scale=4.0):
+    torch.manual_seed(seed)
+    pred = Predictor(640, 640, layers, vocab)
+    joint = Joiner(enc_dim, 640, 640, num_classes=vocab)
+    with torch.no_grad():
+        joint.joint_net[2].weight.mul_(out_scale)
+        joint.joint_net[2].bias[vocab] += blank_bias
+    pred = pred.to(dt).to(cuda).eval().requires_grad_(False)
+    joint = joint.to(dt).to(cuda).eval().requires_grad_(False)
+    P = rnnt.RnntParams(pred.state_dict(), joint.state_dict(), layers)
+    return pred, joint, P
+
+
+def _tol(dt):
+    return lambda lg: 4 * EPS[dt] * (np.abs(lg).max() + np.sqrt((lg**2).mean()))
+
+
+@pytest.mark.parametrize(
+    "dt,layers,vocab,enc_dim,blank_bias",  # the bias gives a mix of tokens and blanks
+    [(torch.float16, 1, 1026, 512, 1.5), (torch.bfloat16, 2, 1024, 1024, 3.5), (torch.float32, 1, 1026, 512, 1.5)],
+)
+def test_greedy_decode_matches_oracle_replay(cuda, dt, layers, vocab, enc_dim, blank_bias):
+    pred, joint, P = _model(vocab, enc_dim, layers, dt, cuda, seed=layers + enc_dim, blank_bias=blank_bias)
+    S, B = 20, 12
+    dec = GreedyDecoder(pred, joint, blank_id=vocab, num_slots=S)
+    rng = np.random.default_rng(7)
+    slots = rng.permutation(S)[:B]
+    dec.reset_slot(slots)
+    oracles = [rnnt.StreamDecoder(P, vocab, dtype=dt) for _ in range(B)]
+    n_dec = n_diff = n_tok = n_blankframes = 0
+    for step in range(4):
+        T = 3
+        lengths = rng.integers(0, T + 1, B)
+        if step == 0:
+            lengths[:] = T
+        enc = torch.randn(B, T, enc_dim, generator=torch.Generator().manual_seed(step)).to(dt).to(cuda)
+        got = dec.decode(slots, enc, lengths, frame_tokens=True)
+        for b in range(B):
+            frames = enc[b, : lengths[b]].double().cpu().numpy()
+            n, worst, differ = oracles[b].replay(frames, got[b], _tol(dt))
+            n_dec += n
+            n_diff += differ
+            n_tok += sum(len(t) for t in got[b])
+            n_blankframes += sum(len(t) < 5 for t in got[b])
+    assert n_tok > 20 and n_blankframes > 5, (n_tok, n_blankframes)  # both tokens and blanks occurred
+    assert n_diff <= 0.02 * n_dec, f"{n_diff} of {n_dec} decisions differ from the oracle's argmax"
+
+
+def test_reset_slot_gives_the_start_state(cuda):
+    dt = torch.float16
+    pred, joint, P = _model(1026, 512, 2, dt, cuda, seed=3)
+    dec = GreedyDecoder(pred, joint, blank_id=1026, num_slots=6)
+    dec.reset_slot([4, 1])
+    ref_out, ref_h, ref_c = rnnt.init_state(P, 1026, dt)
+    for s in (4, 1):
+        for got, ref in ((dec.h[s], ref_h), (dec.c[s], ref_c)):
+            g = got.double().cpu().numpy()
+            rms = np.sqrt((ref**2).mean())
+            assert (np.abs(g - ref) <= 4 * EPS[dt] * (np.abs(ref) + rms)).all()
+        pp = dec.pred_proj[s].double().cpu().numpy()
+        ref_pp = rnnt.pred_proj(P, ref_out, dt)
+        assert (np.abs(pp - ref_pp) <= 4 * EPS[dt] * (np.abs(ref_pp) + np.sqrt((ref_pp**2).mean()))).all()
+    assert not dec.h[[0, 2, 3, 5]].any()  # other slots untouched
+
+
+def test_streams_are_independent_of_the_batch(cuda):
+    """A stream's tokens and state do not depend on its position in the batch or
+    its slot (bit for bit; the batch size is kept so the enc GEMM is the same
+    kernel); slots outside the batch do not move."""
+    dt = torch.float16
+    pred, joint, _ = _model(1026, 512, 1, dt, cuda, seed=5)
+    a = GreedyDecoder(pred, joint, blank_id=1026, num_slots=8)
+    b = GreedyDecoder(pred, joint, blank_id=1026, num_slots=8)
+    a.reset_slot(range(8))
+    b.reset_slot(range(8))
+    sa = np.array([0, 2, 4, 6, 7])
+    perm = np.array([3, 0, 4, 1, 2])
+    sb = np.array([5, 1, 3, 7, 0])  # stream i of a lives on slot sb[i] in b, at batch position inv[i]
+    inv = np.argsort(perm)
+    g = torch.Generator().manual_seed(9)
+    for step in range(3):
+        enc = torch.randn(5, 2, 512, generator=g).to(dt).to(cuda)
+        lengths = np.array([2, 1, 2, 0, 2])
+        ta = a.decode(sa, enc, lengths)
+        before = b.h[[2, 4, 6]].clone()
+        tb = b.decode(sb[perm], enc[torch.from_numpy(perm).to(cuda)], lengths[perm])
+        assert [tb[inv[i]] for i in range(5)] == ta
+        for i in range(5):
+            assert torch.equal(a.h[sa[i]], b.h[sb[i]]) and torch.equal(a.c[sa[i]], b.c[sb[i]])
+            assert torch.equal(a.pred_proj[sa[i]], b.pred_proj[sb[i]])
+        assert torch.equal(b.h[[2, 4, 6]], before)
+
+
+@pytest.mark.parametrize("blank_bias,expect", [(-50.0, "cap"), (50.0, "none")])
+def test_symbol_cap_and_all_blank(cuda, blank_bias, expect):
+    """A blank that never wins: every frame stops at max_symbols tokens
+    (model_runner.py:422); a blank that always wins: no tokens."""
+    dt = torch.float16
+    pred, joint, _ = _model(1026, 512, 1, dt, cuda, seed=6, blank_bias=blank_bias)
+    dec = GreedyDecoder(pred, joint, blank_id=1026, num_slots=4, max_symbols=5)
+    dec.reset_slot(range(4))
+    enc = torch.randn(4, 3, 512, generator=torch.Generator().manual_seed(1)).to(dt).to(cuda)
+    got = dec.decode(range(4), enc, [3, 2, 1, 0], frame_tokens=True)
+    for b, L in enumerate([3, 2, 1, 0]):
+        assert len(got[b]) == L
+        for toks in got[b]:
+            assert len(toks) == (5 if expect == "cap" else 0)
+            assert all(0 <= k < 1026 for k in toks)
