@@ -246,26 +246,59 @@ def front_end_cpu_baseline(sub_sd: dict, budget_s: float, seed: int) -> dict:
     return {"chunks_per_s": chunks / el, "chunks": chunks, "seconds": el}
 
 
+def decode_cpu_baseline(pred, joint, vocab: int, budget_s: float) -> dict:
+    """The oracle's greedy decoding (float64 numpy, one host core) of one stream
+    on 2-frame steps, for about ``budget_s`` seconds, scaled to 128 streams."""
+    import numpy as np
+    import torch
+
+    from oracle import rnnt
+    from threadpoolctl import threadpool_limits
+
+    P = rnnt.RnntParams(pred.state_dict(), joint.state_dict(), 1)
+    sd = rnnt.StreamDecoder(P, vocab)
+    g = np.random.default_rng(13)
+    n, toks, t0 = 0, 0, time.perf_counter()
+    with threadpool_limits(limits=1):
+        while time.perf_counter() - t0 < budget_s:
+            toks += len(sd.decode(g.standard_normal((2, P.w_enc.shape[1]))))
+            n += 1
+    el = time.perf_counter() - t0
+    return {
+        "value": round(n / el / 128, 4),
+        "unit": "decode steps/s (128 streams x 2 frames)",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{n} two-frame steps of one stream through the oracle's greedy loop (float64 numpy), "
+        f"{toks} tokens, in {el:.1f} s, scaled to 128 streams per step",
+    }
+
+
 def encoder_bench(args, device) -> int:
     """``--config e2e``: one streaming step of a random-init small FastConformer
-    from pcm16 -- 128 streams, each fed a 160 ms chunk (2560 samples) per step:
-    the batched front end (pk_fe_step: sample ring, dither, pre-emphasis, FFT,
-    Slaney mel, log; pk_subsample: the 8x convolution stack over each stream's
-    [9 cached + 16 new] mel window; the ``out`` GEMM; model_runner.py:181-252),
-    then the encoder (17 layers, d_model 512, 8 heads, feed-forward x4,
-    depthwise conv kernel 9, left context 70, 2 frames per step: torch
-    projections and feed-forward GEMMs, pk_paged_relpos_attn, pk_conv_step,
-    pk_streaming_mask; encoder.py:229-267), fp16.  Input: int16 pcm of 3
-    random sinusoids (100-4000 Hz) plus noise at 20 dB SNR, resident on the GPU.
-    Also times the front-end kernels and the conv step alone per launch."""
+    from pcm16 to tokens -- 128 streams, each fed a 160 ms chunk (2560 samples)
+    per step: the batched front end (pk_fe_step: sample ring, dither,
+    pre-emphasis, FFT, Slaney mel, log; pk_subsample: the 8x convolution stack
+    over each stream's [9 cached + 16 new] mel window; the ``out`` GEMM;
+    model_runner.py:181-252), the encoder (17 layers, d_model 512, 8 heads,
+    feed-forward x4, depthwise conv kernel 9, left context 70, 2 frames per step:
+    torch projections and feed-forward GEMMs, pk_paged_relpos_attn, pk_conv_step,
+    pk_streaming_mask; encoder.py:229-267), then greedy RNNT decoding
+    (pk_rnnt_greedy_step: up to 5 symbols a frame, predictor state per slot on
+    the device; model_runner.py:306-447) with one token copy per step; fp16.
+    Input: int16 pcm of 3 random sinusoids (100-4000 Hz) plus noise at 20 dB
+    SNR, resident on the GPU.  Also times the front-end kernels, the decode step
+    and the conv step alone."""
     import numpy as np
     import torch
 
     from parakeet_amd import ops
+    from parakeet_amd.modules.decoder import GreedyDecoder, Joiner, Predictor
     from parakeet_amd.modules.encoder import ConformerEncoder
     from parakeet_amd.modules.frontend import ConvSubsampling, FeatureExtractor, PreEncoder
 
     B, D, H, Ly, K, left, right = 128, 512, 8, 17, 9, 70, 1
+    vocab, out_scale, blank_bias = 1026, 4.0, 3.0
     n_mels, C = 80, 256
     T = right + 1
     hop, chunk = 160, 2560
@@ -284,8 +317,20 @@ def encoder_bench(args, device) -> int:
         for mod in sub.conv:
             if isinstance(mod, torch.nn.Conv2d):
                 mod.weight.normal_(0.0, mod.weight[0].numel() ** -0.5)
+    # predictor and joiner (config.py:19-22), default init with the output layer
+    # scaled and the blank logit biased so frames end on blank or on tokens
+    # (the token rate is reported below)
+    pred = Predictor(640, 640, 1, vocab)
+    joint = Joiner(D, 640, 640, num_classes=vocab)
+    with torch.no_grad():
+        joint.joint_net[2].weight.mul_(out_scale)
+        joint.joint_net[2].bias[vocab] += blank_bias
     enc = enc.to(dt).to(device).eval().requires_grad_(False)
     sub = sub.to(dt).to(device).eval().requires_grad_(False)
+    pred = pred.to(dt).to(device).eval().requires_grad_(False)
+    joint = joint.to(dt).to(device).eval().requires_grad_(False)
+    dec = GreedyDecoder(pred, joint, blank_id=vocab, num_slots=B)
+    dec.reset_slot(np.arange(B))
     fx = FeatureExtractor(n_mels=n_mels, seed=6, device=device)
     pre = PreEncoder(fx, sub, num_slots=B, device=device)
     slots = np.arange(B)
@@ -298,15 +343,19 @@ def encoder_bench(args, device) -> int:
     pcm = torch.from_numpy(synth_pcm(B, n_total, seed=7)).to(device)
     length = torch.full((B,), T, dtype=torch.int64, device=device)
     pos = 0
+    n_tokens = n_frames = 0
 
     def step():
-        nonlocal pos
+        nonlocal pos, n_tokens, n_frames
         n = 1440 if pos == 0 else chunk
         rows, counts, first = pre.step(slots, pcm[:, pos : pos + n], n, False)
         pos += n
         if not (counts == T).all():
             raise RuntimeError(f"front end gave {counts.min()}..{counts.max()} frames per stream, expected {T}")
-        enc(rows.view(B, T, D), state, length=length)
+        out, _ = enc(rows.view(B, T, D), state, length=length)
+        toks = dec.decode(slots, out.transpose(1, 2), graph=True)
+        n_tokens += sum(len(t) for t in toks)
+        n_frames += B * T
 
     gc.collect()
     gc.freeze()
@@ -325,6 +374,23 @@ def encoder_bench(args, device) -> int:
         wall = time.perf_counter() - t0
         ms = start.elapsed_time(stop) / K_steps
         log(f"timed {K_steps} steps from pcm16")
+        tok_rate = n_tokens / max(n_frames, 1)
+        # the decode step alone on encoder frames of the same shape (the step's
+        # launches are issued by the library, then one token copy)
+        enc_frames = torch.randn(B, T, D, generator=torch.Generator().manual_seed(12)).to(dt).to(device)
+        dec.decode(slots, enc_frames, graph=True)
+        torch.cuda.synchronize()
+        a_ev, b_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        dec_reps = 20
+        t1 = time.perf_counter()
+        a_ev.record()
+        for _ in range(dec_reps):
+            dec.decode(slots, enc_frames, graph=True)
+        b_ev.record()
+        torch.cuda.synchronize()
+        dec_wall_ms = 1000.0 * (time.perf_counter() - t1) / dec_reps
+        dec_ms = a_ev.elapsed_time(b_ev) / dec_reps
+        log("timed the decode step")
 
         # the front-end kernels alone on the last step's records (re-running a
         # step's records recomputes the same frames into the same ring rows)
@@ -360,8 +426,9 @@ def encoder_bench(args, device) -> int:
     # first depthwise + pointwise rows 2..6, second depthwise + pointwise rows 2..3
     sub_macs = B * (11 * F1 * C * 9 + 5 * F2 * C * 9 + 5 * F2 * C * C + 2 * F3 * C * 9 + 2 * F3 * C * C)
     sub_tflops = 2 * sub_macs / (sub_us * 1e-6) / 1e12
-    cpu = None
+    cpu = dec_cpu = None
     if not args.no_cpu_baseline:
+        dec_cpu = decode_cpu_baseline(pred, joint, vocab, min(args.cpu_baseline_seconds, 10.0))
         sd = {k: v.detach().double().cpu().numpy() for k, v in sub.state_dict().items()}
         cb = front_end_cpu_baseline(sd, min(args.cpu_baseline_seconds, 10.0), seed=8)
         cpu = {
@@ -373,7 +440,7 @@ def encoder_bench(args, device) -> int:
             f"ConvSubsampling (float64 numpy) in {cb['seconds']:.1f} s, scaled to 128 streams per step",
         }
     result = {
-        "metric": "streaming encoder steps/sec from pcm16 (small FastConformer: front end + 17 layers) at 1 GPU",
+        "metric": "streaming steps/sec from pcm16 to tokens (small FastConformer: front end + 17 layers + greedy RNNT) at 1 GPU",
         "value": round(1000.0 / ms, 2),
         "unit": "steps/s",
         "n_gpus": 1,
@@ -384,10 +451,11 @@ def encoder_bench(args, device) -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp16",
-        "data": "synthetic pcm16 (3 random sinusoids 100-4000 Hz + noise at 20 dB SNR), random-init weights, pos biases N(0,0.02)",
+        "data": "synthetic pcm16 (3 random sinusoids 100-4000 Hz + noise at 20 dB SNR), random-init weights, pos biases N(0,0.02), joint output x4 with blank logit bias +3",
         "config": {
             "workload": "small FastConformer step from pcm16: 160 ms per stream -> log-mel (80) -> 8x conv "
-            "subsampling -> 17 layers x (FF/2, paged rel-pos MHA, conv module with per-stream cache, FF/2, LN), "
+            "subsampling -> 17 layers x (FF/2, paged rel-pos MHA, conv module with per-stream cache, FF/2, LN) "
+            "-> greedy RNNT (LSTM 640, joint 640, 1027 classes, up to 5 symbols a frame), "
             "128 streams all live, 2 encoder frames per step",
             "layers": Ly,
             "d_model": D,
@@ -416,6 +484,13 @@ def encoder_bench(args, device) -> int:
                 "kernel": "subsample_kernel",
             },
             "cpu_baseline": cpu,
+        },
+        "decode": {
+            "step_ms": round(dec_ms, 4),
+            "step_wall_ms": round(dec_wall_ms, 4),
+            "tokens_per_frame": round(tok_rate, 3),
+            "decisions_max_per_step": B * T * 5,
+            "cpu_baseline": dec_cpu,
         },
         "conv_step": {
             "kernel": "conv_step_kernel (GLU, pad mask, causal depthwise conv with cache, LayerNorm, SiLU)",

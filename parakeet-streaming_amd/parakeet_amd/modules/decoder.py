@@ -89,6 +89,7 @@ class GreedyDecoder:
         self.c = torch.zeros((S, L, H), dtype=self.dtype, device=self.device)
         self.pred_proj = torch.zeros((S, J), dtype=self.dtype, device=self.device)
         self._ws: dict[int, torch.Tensor] = {}
+        self._graphs: dict[tuple[int, int, int], dict] = {}
 
     def refresh_weights(self) -> None:
         """Contiguous copies of the parameters in the layouts the kernels read
@@ -133,11 +134,14 @@ class GreedyDecoder:
         a.workspace = self._workspace(a.batch).data_ptr()
         return a
 
-    def _slots(self, slots) -> Tensor:
+    def _check_slots(self, slots) -> np.ndarray:
         s = np.ascontiguousarray(np.asarray(slots, dtype=np.int32).reshape(-1))
         if len(np.unique(s)) != len(s) or (len(s) and (s.min() < 0 or s.max() >= self.num_slots)):
             raise ValueError(f"slots must be distinct and in [0, {self.num_slots})")
-        return torch.from_numpy(s).to(self.device)
+        return s
+
+    def _slots(self, slots) -> Tensor:
+        return torch.from_numpy(self._check_slots(slots)).to(self.device)
 
     def reset_slot(self, slots) -> None:
         """A new stream on each of ``slots``: the predictor run on the blank start
@@ -148,14 +152,71 @@ class GreedyDecoder:
         a = self._args(st, prime=True)
         check(lib().pk_rnnt_greedy_step(ctypes.byref(a), ops._stream(self.device)), "pk_rnnt_greedy_step")
 
-    def decode(self, slots, enc_out: Tensor, lengths=None, frame_tokens: bool = False):
+    def _graph_for(self, B: int, T: int, D: int) -> dict:
+        """A HIP graph of one decode step for B streams and T frames: the enc GEMM
+        and every launch of pk_rnnt_greedy_step, over persistent input and output
+        buffers (recorded once, replayed per step)."""
+        key = (B, T, D)
+        g = self._graphs.get(key)
+        if g is not None:
+            return g
+        dev = self.device
+        W = T * self.max_symbols + T  # per stream: tokens, then counts per frame
+        meta = torch.zeros(2 * B, dtype=torch.int32, device=dev)  # slots | lengths
+        out = torch.zeros((B, W), dtype=torch.int32, device=dev)
+        g = {
+            "meta": meta,
+            "meta_h": torch.zeros(2 * B, dtype=torch.int32, pin_memory=True),
+            "slots": meta[:B],
+            "lens": meta[B:],
+            "enc": torch.zeros((B, T, D), dtype=self.dtype, device=dev),
+            "e": torch.empty((B, T, self.joint), dtype=self.dtype, device=dev),
+            "out": out,
+            "out_h": torch.zeros((B, W), dtype=torch.int32, pin_memory=True),
+            "tokens": out[:, : T * self.max_symbols],
+            "counts": out[:, T * self.max_symbols :],
+        }
+        a = self._args(g["slots"], prime=False)
+        a.enc_proj, a.enc_stride_b, a.enc_stride_t = g["e"].data_ptr(), g["e"].stride(0), g["e"].stride(1)
+        a.lengths, a.max_frames = g["lens"].data_ptr(), T
+        a.tokens, a.frame_counts = g["tokens"].data_ptr(), g["counts"].data_ptr()
+        # rows of `out` hold T*max_symbols tokens then T counts: the kernels index
+        # tokens with row length T*max_symbols and counts with row length T, so
+        # they get their own buffers and the graph copies them into `out`
+        g["tok_buf"] = torch.empty((B, T * self.max_symbols), dtype=torch.int32, device=dev)
+        g["cnt_buf"] = torch.empty((B, T), dtype=torch.int32, device=dev)
+        a.tokens, a.frame_counts = g["tok_buf"].data_ptr(), g["cnt_buf"].data_ptr()
+        g["args"] = a
+
+        def run():
+            torch.addmm(self.b_enc, g["enc"].view(B * T, D), self.w_enc.t(), out=g["e"].view(B * T, self.joint))
+            check(lib().pk_rnnt_greedy_step(ctypes.byref(a), ops._stream(dev)), "pk_rnnt_greedy_step")
+            g["tokens"].copy_(g["tok_buf"])
+            g["counts"].copy_(g["cnt_buf"])
+
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            run()  # warm the GEMM outside the capture; every length is 0, so no state moves
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            run()
+        torch.cuda.current_stream(dev).wait_stream(side)
+        g["graph"] = graph
+        self._graphs[key] = g
+        return g
+
+    def decode(self, slots, enc_out: Tensor, lengths=None, frame_tokens: bool = False, graph: bool = False):
         """Greedy decoding of one step's encoder frames.
 
         enc_out: [B, T, D] encoder output (frames of stream b in enc_out[b, :lengths[b]]);
         lengths: frames per stream (None: all T).  Returns the emitted tokens of
-        each stream (``frame_tokens=True``: a list per frame)."""
-        st = self._slots(slots)
-        B = int(st.numel())
+        each stream (``frame_tokens=True``: a list per frame).  ``graph=True``
+        replays a recorded step over persistent buffers: one upload of slots and
+        lengths, one copy of the tokens back (the pinned upload buffer is reused
+        by the next call, after this call's blocking copy)."""
+        sl = self._check_slots(slots)
+        B = len(sl)
         if enc_out.dim() != 3 or enc_out.shape[0] != B:
             raise ValueError(f"enc_out must be [{B}, T, D]")
         T = int(enc_out.shape[1])
@@ -167,6 +228,18 @@ class GreedyDecoder:
                 raise ValueError(f"lengths must be [{B}] in [0, {T}]")
         if B == 0 or T == 0:
             return [[] for _ in range(B)]
+        if graph:
+            g = self._graph_for(B, T, int(enc_out.shape[2]))
+            mh = g["meta_h"].numpy()
+            mh[:B] = sl
+            mh[B:] = lens
+            g["meta"].copy_(g["meta_h"], non_blocking=True)
+            g["enc"].copy_(enc_out)
+            g["graph"].replay()
+            g["out_h"].copy_(g["out"])  # the step's one synchronisation
+            o = g["out_h"].numpy()
+            return self._split(o[:, : T * self.max_symbols], o[:, T * self.max_symbols :], lens, frame_tokens)
+        st = torch.from_numpy(sl).to(self.device)
         with torch.no_grad():
             e = F.linear(enc_out.to(self.dtype), self.w_enc, self.b_enc).contiguous()  # Joiner.enc (decoder.py:83)
         tokens = torch.empty((B, T * self.max_symbols), dtype=torch.int32, device=self.device)
@@ -177,7 +250,16 @@ class GreedyDecoder:
         a.lengths, a.max_frames = lens_d.data_ptr(), T
         a.tokens, a.frame_counts = tokens.data_ptr(), counts.data_ptr()
         check(lib().pk_rnnt_greedy_step(ctypes.byref(a), ops._stream(self.device)), "pk_rnnt_greedy_step")
+        return self._collect(tokens, counts, lens, frame_tokens)
+
+    @staticmethod
+    def _collect(tokens: Tensor, counts: Tensor, lens: np.ndarray, frame_tokens: bool):
         tok, cnt = tokens.cpu().numpy(), counts.cpu().numpy()  # the step's one synchronisation
+        return GreedyDecoder._split(tok, cnt, lens, frame_tokens)
+
+    @staticmethod
+    def _split(tok: np.ndarray, cnt: np.ndarray, lens: np.ndarray, frame_tokens: bool):
+        B = len(lens)
         out = []
         for b in range(B):
             n = cnt[b, : lens[b]]

@@ -131,3 +131,25 @@ def test_symbol_cap_and_all_blank(cuda, blank_bias, expect):
         for toks in got[b]:
             assert len(toks) == (5 if expect == "cap" else 0)
             assert all(0 <= k < 1026 for k in toks)
+
+
+def test_graph_replay_matches_direct_launches(cuda):
+    """The recorded decode step replayed over persistent buffers gives the same
+    tokens and state as the direct launches, step after step, with other work in
+    between (a graph of the enc GEMM and every launch of the step)."""
+    dt = torch.float16
+    pred, joint, _ = _model(1026, 512, 1, dt, cuda, seed=8)
+    a = GreedyDecoder(pred, joint, blank_id=1026, num_slots=10)
+    b = GreedyDecoder(pred, joint, blank_id=1026, num_slots=10)
+    slots = np.array([7, 1, 4, 9, 2, 0])
+    a.reset_slot(slots)
+    b.reset_slot(slots)
+    g = torch.Generator().manual_seed(4)
+    for step in range(5):
+        enc = torch.randn(6, 2, 512, generator=g).to(dt).to(cuda)
+        lengths = np.array([2, 2, 1, 0, 2, 1]) if step % 2 else None
+        ta = a.decode(slots, enc, lengths)
+        tb = b.decode(slots, enc, lengths, graph=True)
+        assert ta == tb, f"step {step}"
+        assert torch.equal(a.h, b.h) and torch.equal(a.c, b.c) and torch.equal(a.pred_proj, b.pred_proj)
+        torch.cuda.synchronize()
