@@ -3,25 +3,23 @@
 // parakeet/modules/decoder.py:5-86).
 //
 // One decode step for a batch runs, for each encoder frame t and each symbol
-// s < max_symbols, four launches with no host synchronisation:
+// s < max_symbols, 2 + layers launches with no host synchronisation:
 //   joint_kernel     hid = relu(enc_proj[b, t] + pred_proj[slot]) (rounded to the
 //                    storage type), logits = W_out hid + b_out (rounded), and the
 //                    first maximum over a tile of 128 vocabulary rows: MFMA with
-//                    W_out rows as A (rows = vocabulary entries) and hid as B
-//                    (columns = 16 streams).  Workgroups whose streams are all
-//                    done for the frame return at once -- the reference's
-//                    "every decision blank" break, per workgroup.
-//   select_kernel    the first maximum over the tiles; a blank ends the stream's
-//                    frame, a token is appended and marks the stream for the
-//                    predictor update.
-//   lstm_kernel      per layer: gates = W_ih x + W_hh h + b_ih + b_hh as MFMA over
-//                    K = [x ; h] (x = embedding of the token, or the layer below),
-//                    then c' = sig(f) c + sig(i) tanh(g), h' = sig(o) tanh(c') for
-//                    16 hidden units x SPW streams per workgroup; streams not
-//                    marked keep their state.  Every workgroup reads all of a
-//                    stream's h, so h' goes to a per-batch scratch; c is read and
-//                    written by one thread per element, in place.
-//   pred_kernel      pred_proj[slot] = W_pred h'_top + b_pred for the marked
+//                    the weight rows as A and the 16 streams as B columns.
+//                    Workgroups whose streams are all done for the frame return
+//                    at once -- the reference's "every decision blank" break.
+//   lstm_kernel      layer 0 first takes the first maximum over the tiles (the
+//                    decision; column 0 of the grid records it: a blank ends the
+//                    stream's frame, a token is appended); per layer: gates =
+//                    W_ih x + W_hh h + b_ih + b_hh as MFMA over K = [x ; h] (x =
+//                    embedding of the token, or the layer below), then c' = sig(f)
+//                    c + sig(i) tanh(g), h' = sig(o) tanh(c') for 16 hidden units x
+//                    SPW streams per workgroup; other streams keep their state.
+//                    Every workgroup reads all of a stream's h, so h' goes to a
+//                    per-batch scratch; c is owned by one thread per element.
+//   pred_kernel      pred_proj[slot] = W_pred h'_top + b_pred for the updated
 //                    streams, and h' copied from the scratch into the slot state
 //                    (this launch runs after every read of the old h).
 
@@ -180,21 +178,15 @@ __global__ void __launch_bounds__(512) joint_kernel(const DecK p) {
 }
 
 // ---------------------------------------------------------------------------
-// word 0: blank seen in the current frame; 1: token decided (-1: no update);
-// 2: tokens emitted this step
-__global__ void __launch_bounds__(256) select_kernel(const DecK p) {
-  const int b = blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= p.batch) return;
-  int32_t* ws = ws_of(p, b);
-  if (p.t == 0 && p.s == 0) ws[2] = 0;
-  if (p.s == 0) {
-    ws[0] = 0;
-    if (p.t < p.max_frames) p.frame_counts[(int64_t)b * p.max_frames + p.t] = 0;
-  }
-  if (!active_at(p, b, ws)) {
-    ws[1] = -1;
-    return;
-  }
+// Stream b's decision at (t, s): the first maximum over the vocabulary tiles'
+// partial maxima; -1 when the stream is not deciding or decides blank.
+// Workspace words: 0 = blank seen in the current frame, 1 = token that updates
+// the predictor this iteration (-1: none), 2 = tokens emitted this step.
+__device__ static inline int decide(const DecK& p, int b, bool* act_out) {
+  const int32_t* ws = ws_of(p, b);
+  const bool act = active_at(p, b, ws);
+  *act_out = act;
+  if (!act) return -1;
   float v = __int_as_float(ws[kWsHead]);
   int ix = ws[kWsHead + 1];
   for (int k = 1; k < p.vtiles; ++k) {
@@ -205,14 +197,28 @@ __global__ void __launch_bounds__(256) select_kernel(const DecK p) {
       ix = oi;
     }
   }
-  if (ix == p.blank || ix < 0 || ix >= p.V1) {
+  return (ix == p.blank || ix < 0 || ix >= p.V1) ? -1 : ix;
+}
+
+// The record of stream b's decision (one writer per stream).  Other
+// workgroups of the same launch may read word 0 before or after this write:
+// an update needs a token, and a stream that just decided blank has none
+// either way.
+__device__ static inline void record(const DecK& p, int b, bool act, int tok) {
+  int32_t* ws = ws_of(p, b);
+  if (p.t == 0 && p.s == 0) ws[2] = 0;
+  if (p.s == 0) {
+    ws[0] = 0;
+    if (p.t < p.max_frames) p.frame_counts[(int64_t)b * p.max_frames + p.t] = 0;
+  }
+  ws[1] = tok;
+  if (!act) return;
+  if (tok < 0) {
     ws[0] = 1;
-    ws[1] = -1;
     return;
   }
-  ws[1] = ix;
   const int n = ws[2];
-  p.tokens[(int64_t)b * p.max_frames * p.max_symbols + n] = ix;
+  p.tokens[(int64_t)b * p.max_frames * p.max_symbols + n] = tok;
   ws[2] = n + 1;
   p.frame_counts[(int64_t)b * p.max_frames + p.t] += 1;
 }
@@ -236,11 +242,22 @@ __global__ void __launch_bounds__(LstmCfg<ST>::WAVES * 64) lstm_kernel(const Dec
   const int H = p.H, L = p.layers, layer = p.layer;
   const int u0 = blockIdx.x * 16, b0 = blockIdx.y * SPW;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
-  // which streams update: the select's token (prime: every stream, token blank)
+  // which streams update: layer 0 decides (prime: every stream, token blank),
+  // the layers above read layer 0's record
   if (tid < SPW) {
     const int b = b0 + tid;
     int tk = -1;
-    if (b < p.batch) tk = p.prime ? p.blank : ws_of(p, b)[1];
+    if (b < p.batch) {
+      if (p.prime) {
+        tk = p.blank;
+      } else if (layer == 0) {
+        bool act;
+        tk = decide(p, b, &act);
+        if (blockIdx.x == 0) record(p, b, act, tk);
+      } else {
+        tk = ws_of(p, b)[1];
+      }
+    }
     tok_s[tid] = tk;
   }
   __syncthreads();
@@ -402,28 +419,29 @@ static int run_step(const pk_rnnt_args* a, hipStream_t st) {
   k.hn = (char*)a->workspace + ws_int_bytes(a->batch, a->vocab1);
   k.h = a->h;
   k.prime = a->prime;
-  const dim3 gj(k.vtiles, (a->batch + 15) / 16), gs((a->batch + 255) / 256);
+  const dim3 gj(k.vtiles, (a->batch + 15) / 16);
   const dim3 gl(a->hidden / 16, (a->batch + LstmCfg<ST>::SPW - 1) / LstmCfg<ST>::SPW);
   const dim3 gp((a->joint + 63) / 64, (a->batch + 15) / 16);
-  auto predictor = [&]() {
+  auto lstm = [&]() {
     for (int l = 0; l < a->layers; ++l) {
       k.layer = l;
       hipLaunchKernelGGL(lstm_kernel<ST>, gl, dim3(LstmCfg<ST>::WAVES * 64), 0, st, k);
     }
-    hipLaunchKernelGGL(pred_kernel<ST>, gp, dim3(256), 0, st, k);
   };
-  if (a->prime) {
-    k.t = k.s = 0;
-    predictor();
-  } else {
+  auto pred = [&]() { hipLaunchKernelGGL(pred_kernel<ST>, gp, dim3(256), 0, st, k); };
+  k.t = k.s = 0;
+  if (!a->prime) {
     for (int t = 0; t < a->max_frames; ++t)
       for (int s = 0; s < a->max_symbols; ++s) {
         k.t = t;
         k.s = s;
         hipLaunchKernelGGL(joint_kernel<ST>, gj, dim3(512), 0, st, k);
-        hipLaunchKernelGGL(select_kernel, gs, dim3(256), 0, st, k);
-        predictor();
+        lstm();
+        pred();
       }
+  } else {
+    lstm();
+    pred();
   }
   return check_launch("pk_rnnt_greedy_step");
 }
