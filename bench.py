@@ -294,7 +294,7 @@ def encoder_bench(args, device) -> int:
 
     from parakeet_amd import ops
     from parakeet_amd.modules.decoder import GreedyDecoder, Joiner, Predictor
-    from parakeet_amd.modules.encoder import ConformerEncoder
+    from parakeet_amd.modules.encoder import ConformerEncoder, EncoderStepGraph
     from parakeet_amd.modules.frontend import ConvSubsampling, FeatureExtractor, PreEncoder
 
     B, D, H, Ly, K, left, right = 128, 512, 8, 17, 9, 70, 1
@@ -342,6 +342,9 @@ def encoder_bench(args, device) -> int:
     log(f"synthesising {B} x {n_total} pcm16 samples")
     pcm = torch.from_numpy(synth_pcm(B, n_total, seed=7)).to(device)
     length = torch.full((B,), T, dtype=torch.int64, device=device)
+    # the encoder step recorded once and replayed (the host page work and the
+    # rows upload stay outside the recording), or issued op by op from Python
+    enc_step = None if args.eager_encoder else EncoderStepGraph(enc, state, length)
     pos = 0
     n_tokens = n_frames = 0
 
@@ -352,7 +355,10 @@ def encoder_bench(args, device) -> int:
         pos += n
         if not (counts == T).all():
             raise RuntimeError(f"front end gave {counts.min()}..{counts.max()} frames per stream, expected {T}")
-        out, _ = enc(rows.view(B, T, D), state, length=length)
+        if enc_step is not None:
+            out = enc_step(rows.view(B, T, D))
+        else:
+            out, _ = enc(rows.view(B, T, D), state, length=length)
         toks = dec.decode(slots, out.transpose(1, 2), graph=True)
         n_tokens += sum(len(t) for t in toks)
         n_frames += B * T
@@ -467,6 +473,9 @@ def encoder_bench(args, device) -> int:
             "n_mels": n_mels,
             "subsampling_channels": C,
             "parallelism": "single GPU",
+            "encoder_launch": "eager: torch ops issued from Python"
+            if args.eager_encoder
+            else f"one HIP graph replay per step ({Ly} layers)",
         },
         "front_end": {
             "fe_kernel_us": round(fe_us, 3),
@@ -516,6 +525,7 @@ def main() -> int:
     ap.add_argument("--no-kernel-events", action="store_true")
     ap.add_argument("--kernel-event-steps", type=int, default=50, help="eager steps timed per kernel for the roofline")
     ap.add_argument("--graph", action="store_true", help="replay every step's launches from one HIP graph (grid sized for all slots)")
+    ap.add_argument("--eager-encoder", action="store_true", help="e2e: issue the encoder's ops from Python instead of replaying a recorded step")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB", help="only run a device copy of MIB MiB (counter calibration)")
     ap.add_argument("--cpu-baseline-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")

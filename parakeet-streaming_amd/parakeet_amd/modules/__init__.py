@@ -1,6 +1,6 @@
 from .attention import ConformerAttention, PositionalEncoding
 from .cache import ModelCache, StreamingState
-from .encoder import ConformerEncoder, ConformerLayer
+from .encoder import ConformerEncoder, ConformerLayer, EncoderStepGraph
 
 __all__ = [
     "ConformerAttention",
@@ -9,4 +9,5 @@ __all__ = [
     "StreamingState",
     "ConformerEncoder",
     "ConformerLayer",
+    "EncoderStepGraph",
 ]

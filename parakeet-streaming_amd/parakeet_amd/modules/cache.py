@@ -19,6 +19,7 @@ forward) needs no extra call.  The conv cache stays dense per slot.
 
 from __future__ import annotations
 
+from contextlib import contextmanager
 from dataclasses import dataclass
 
 import numpy as np
@@ -126,6 +127,7 @@ class ModelCache:
         self._rows = torch.zeros((n, 1 + self.max_pages), dtype=torch.int32, device=dev)
         self._seen: set[int] = set()
         self._step_open = False
+        self._recording = False
 
     def _derive(self, slots: np.ndarray) -> "ModelCache":
         view = ModelCache.__new__(ModelCache)
@@ -180,6 +182,11 @@ class ModelCache:
     def _begin_layer(self, layer_idx: int) -> None:
         if not 0 <= layer_idx < self.num_layers:
             raise IndexError(f"layer {layer_idx} out of range [0, {self.num_layers})")
+        if self._recording:
+            if layer_idx in self._seen:
+                raise RuntimeError(f"paged cache: layer {layer_idx} updated twice in one recorded step")
+            self._seen.add(layer_idx)
+            return
         if not self._step_open or layer_idx in self._seen:
             if self._step_open and len(self._seen) != self.num_layers:
                 raise RuntimeError(
@@ -200,6 +207,32 @@ class ModelCache:
             self._rows.copy_(torch.from_numpy(rows))
         self._seen = set()
         self._step_open = True
+
+    def open_step(self) -> None:
+        """Opens the next step now -- the host page work for the batch and the
+        upload of its rows -- instead of on the first layer update.  For callers
+        that replay a recorded step, whose launches read the rows uploaded here."""
+        if self._step_open and self._seen and len(self._seen) != self.num_layers:
+            raise RuntimeError(
+                f"paged cache: a new step began after layers {sorted(self._seen)} of {self.num_layers}"
+            )
+        self._open_step()
+
+    @contextmanager
+    def recording(self):
+        """While recording a step (HIP graph capture), layer updates never open a
+        step: the recording must hold no host work, and each replay follows an
+        ``open_step()``."""
+        if self._recording:
+            raise RuntimeError("paged cache: already recording")
+        seen = self._seen
+        self._seen = set()
+        self._recording = True
+        try:
+            yield self
+        finally:
+            self._recording = False
+            self._seen = seen
 
     def paged(self) -> ops.PagedKV:
         """Device view (pools + this batch's rows) for the kernels."""

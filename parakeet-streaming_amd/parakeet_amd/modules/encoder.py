@@ -7,7 +7,10 @@
   a per-stream Python loop with two device->host syncs per stream
   (encoder.py:167-227);
 * ``forward`` keeps the layer loop and the state advance (encoder.py:229-267);
-  the attention of every layer runs on the paged cache.
+  the attention of every layer runs on the paged cache;
+* ``EncoderStepGraph`` replays a recorded step for a fixed batch: the about 20
+  launches per layer that ``forward`` issues from Python become one HIP graph
+  replay, with the host page work and one upload per step left outside it.
 
 The convolution module's GLU / depthwise conv / LayerNorm / SiLU runs as one HIP
 launch with each stream's conv state updated in place (convolution.py:107-162,
@@ -257,4 +260,66 @@ class ConformerEncoder(nn.Module):
         return x.transpose(1, 2), state
 
 
-__all__ = ["ConformerEncoder", "ConformerLayer", "ConformerConvolution", "ConformerFeedForward", "CausalConv1d"]
+class EncoderStepGraph:
+    """``encoder(x, state, length)`` for a fixed batch, recorded once in a HIP
+    graph and replayed every step (the call ModelRunner._encode_step makes,
+    parakeet/engine/model_runner.py:285-291, with whole chunks).
+
+    Every launch of a step reads the same device memory each step: the page
+    pools, the batch's block-table rows, the state counters, the conv state, the
+    position table and the weights; only their contents change.  A call runs
+    ``state.cache.open_step()`` (the host page work and the one upload of the
+    batch's rows), copies ``x`` into a fixed input buffer and replays.  The first
+    call runs the step eagerly -- its real work, which also initialises the
+    libraries' handles -- and then records the step without running it.
+
+    ``length`` is the per-stream frame count of every step ([B] int64; the engine
+    feeds whole chunks, parakeet/engine/sequence.py:137-146).  The returned
+    [B, D, T] tensor is a fixed buffer that the next call overwrites.
+    """
+
+    def __init__(self, encoder: ConformerEncoder, state: StreamingState, length: Tensor):
+        cache = state.cache
+        if not isinstance(cache, ModelCache):
+            raise TypeError("state.cache must be the paged ModelCache")
+        for name in ("processed_frames", "cache_lengths"):
+            if not isinstance(getattr(state, name), Tensor):
+                raise TypeError(f"state.{name} must be a device tensor (a recorded step advances it on the device)")
+        B = cache.batch_size
+        dev = cache.k_pages.device
+        if not isinstance(length, Tensor) or tuple(length.shape) != (B,):
+            raise ValueError(f"length must be a [{B}] tensor")
+        self.encoder = encoder
+        self.state = state
+        self.length = length.to(device=dev, dtype=torch.int64).clone()
+        self.shape = (B, cache.chunk, encoder.embed_dim)
+        self.x: Tensor | None = None
+        self.out: Tensor | None = None
+        self.graph: torch.cuda.CUDAGraph | None = None
+
+    def __call__(self, x: Tensor) -> Tensor:
+        if tuple(x.shape) != self.shape:
+            raise ValueError(f"x must be {self.shape}, got {tuple(x.shape)}")
+        cache = self.state.cache
+        cache.open_step()
+        if self.graph is None:
+            self.x = x.detach().clone()
+            out, _ = self.encoder(self.x, self.state, length=self.length)
+            graph = torch.cuda.CUDAGraph()
+            with cache.recording(), torch.cuda.graph(graph):
+                self.out, _ = self.encoder(self.x, self.state, length=self.length)
+            self.graph = graph
+            return out
+        self.x.copy_(x)
+        self.graph.replay()
+        return self.out
+
+
+__all__ = [
+    "ConformerEncoder",
+    "ConformerLayer",
+    "ConformerConvolution",
+    "ConformerFeedForward",
+    "CausalConv1d",
+    "EncoderStepGraph",
+]

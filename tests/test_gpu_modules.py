@@ -255,3 +255,47 @@ def test_encoder_streaming_matches_dense_reference(cuda):
         assert state.cache_lengths.cpu().tolist() == cl.tolist()
     print(f"  worst max-abs error {worst:.3e}", flush=True)
     torch.cuda.synchronize()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_encoder_step_graph_matches_eager_steps(cuda, dtype):
+    """EncoderStepGraph (one recorded step replayed per call) against the eager
+    forward on a second state with the same weights: outputs, state counters,
+    conv state and the pages of every layer agree bit for bit, step after step
+    (eviction included), with the eager path's launches between the replays."""
+    print(f"\n[encoder graph] 2 layers {dtype} replay vs eager", flush=True)
+    from parakeet_amd.modules.encoder import EncoderStepGraph
+
+    left, right, D, H, Ly, B, K = 10, 1, 128, 2, 2, 5, 9
+    T = right + 1
+    torch.manual_seed(5)
+    enc = ConformerEncoder(
+        feat_in=80, hidden_size=D, ff_expansion_factor=2, num_layers=Ly, num_heads=H,
+        subsampling_factor=8, pos_emb_max_len=64, conv_kernel_size=K, att_context_size=[left, right],
+        subsampling_conv_channels=32, use_bias=False, page_size=4,
+    )
+    for layer in enc.layers:
+        _init_attention(layer.self_attn, D, seed=20 + layer.layer_idx)
+    enc = enc.to(cuda).to(dtype).eval().requires_grad_(False)
+    eager = enc.init_streaming_state(batch_size=B, device=cuda, dtype=dtype)
+    replay = enc.init_streaming_state(batch_size=B, device=cuda, dtype=dtype)
+    length = torch.full((B,), T, dtype=torch.int64, device=cuda)
+    graph = EncoderStepGraph(enc, replay, length)
+    g = torch.Generator().manual_seed(6)
+    with torch.no_grad():
+        for step in range(12):  # the window fills after 5 steps; pages are evicted from then on
+            x = torch.randn(B, T, D, generator=g).to(dtype).to(cuda)
+            ref, _ = enc(x, eager, length=length)
+            got = graph(x)
+            assert torch.equal(got, ref), f"step {step}: max diff {(got.float() - ref.float()).abs().max():.3e}"
+            assert torch.equal(replay.processed_frames, eager.processed_frames)
+            assert torch.equal(replay.cache_lengths, eager.cache_lengths)
+            assert torch.equal(replay.cache.conv_frames, eager.cache.conv_frames)
+            for layer in range(Ly):
+                kr, vr = replay.cache.window(layer)
+                ke, ve = eager.cache.window(layer)
+                assert torch.equal(kr, ke) and torch.equal(vr, ve), f"step {step} layer {layer}"
+    assert graph.graph is not None
+    assert replay.processed_frames.tolist() == [12 * T] * B
+    torch.cuda.synchronize()
