@@ -14,6 +14,14 @@ Modules (each function cites the reference file:line it restates):
 * ``relpos``      -- sinusoid table, pos slice, rel_shift (parakeet/modules/attention.py:23-83)
 * ``attention``   -- ConformerAttention core (parakeet/modules/attention.py:85-125)
 * ``dense_path``  -- torch-CPU fp32 dense encoder-attention step (the CPU baseline)
+* ``conv``        -- ConformerConvolution's GLU / causal depthwise conv with the
+                     conv cache / LayerNorm / SiLU (parakeet/modules/convolution.py:37-52,107-162)
+* ``frontend``    -- log-mel features with dither and the streaming push, 8x
+                     convolution subsampling, the pre-encode cache and drop
+                     (parakeet/modules/feature_extractor.py, subsample.py;
+                     parakeet/engine/model_runner.py:181-252)
+* ``rnnt``        -- Predictor / Joiner and the greedy per-frame loop
+                     (parakeet/modules/decoder.py:5-86; model_runner.py:347-447)
 
 How each is pinned (the reference ships no tests, fixtures or golden vectors):
 see tests/test_oracle_*.py -- closed forms, brute force on tiny inputs, library
