@@ -299,3 +299,99 @@ def test_encoder_step_graph_matches_eager_steps(cuda, dtype):
     assert graph.graph is not None
     assert replay.processed_frames.tolist() == [12 * T] * B
     torch.cuda.synchronize()
+
+
+@pytest.mark.gpu
+def test_engine_loop_with_scheduler_matches_per_stream_reference(cuda):
+    """The reference's _encode_step call pattern (parakeet/engine/model_runner.py:
+    254-304) on the drop-ins: Scheduler.init_state_pool, acquire_state_slot,
+    pack_states -> encoder(batch, state, length) -> unpack_states,
+    release_state_slot (scheduler.py:68-201), with streams arriving and leaving,
+    batches of varying slot subsets in varying order, and slots reused by new
+    streams.  Every stream's output of every step equals the float64 reference
+    encoder (oracle attention over a dense shift cache, oracle conv step, oracle
+    masks) run on that stream alone from its own start: streams are independent,
+    so that is what the reference's batched pack / unpack computes."""
+    print("\n[engine loop] scheduler + paged encoder vs per-stream dense reference", flush=True)
+    from parakeet_amd.engine.scheduler import Scheduler
+
+    left, right, D, H, Ly, K, S = 6, 1, 128, 2, 2, 9, 4
+    T = right + 1
+    torch.manual_seed(7)
+    enc = ConformerEncoder(
+        feat_in=80, hidden_size=D, ff_expansion_factor=2, num_layers=Ly, num_heads=H,
+        subsampling_factor=8, pos_emb_max_len=64, conv_kernel_size=K, att_context_size=[left, right],
+        subsampling_conv_channels=32, use_bias=False, page_size=4,
+    )
+    for layer in enc.layers:
+        _init_attention(layer.self_attn, D, seed=30 + layer.layer_idx)
+    ref = copy.deepcopy(enc).double()
+    for layer in ref.layers:
+        layer.self_attn.forward = _oracle_attention(layer.self_attn, left, H)
+        layer.conv.forward = _oracle_conv(layer.conv)
+
+    def ref_masks(current_len, cache_lengths, processed_frames, device, lengths):
+        pad, att = om.create_streaming_masks(
+            current_len, cache_lengths.numpy(), processed_frames.numpy(), lengths.numpy(), (left, right)
+        )
+        return torch.from_numpy(pad), torch.from_numpy(att)
+
+    ref._create_streaming_masks = ref_masks
+    enc = enc.to(cuda)
+    sch = Scheduler(max_active=S)
+    sch.init_state_pool(enc, cuda, torch.float32, pool_size=S, page_size=4)
+
+    class Seq:
+        def __init__(self, slot, steps):
+            self.status = None
+            self.encoder_state = slot
+            self.steps = steps
+            self.done = 0
+            self.dense = _DenseCache(1, Ly, left, right, D, K)
+            self.proc = 0
+            self.cl = 0
+
+    rng = np.random.default_rng(12)
+    g = torch.Generator().manual_seed(13)
+    live: list[Seq] = []
+    slot_users: dict[int, int] = {}
+    compared = worst = 0.0
+    with torch.no_grad():
+        for step in range(40):
+            while rng.random() < 0.6:  # arrivals until the pool is full
+                slot = sch.acquire_state_slot()
+                if slot is None:
+                    break
+                live.append(Seq(slot, int(rng.integers(3, 12))))
+                slot_users[slot] = slot_users.get(slot, 0) + 1
+            ready = [s for s in live if rng.random() < 0.8]
+            rng.shuffle(ready)
+            if ready:
+                B = len(ready)
+                x = torch.randn(B, T, D, generator=g)
+                state, index = sch.pack_states(ready)
+                out, state = enc(x.to(cuda), state, length=torch.full((B,), T, dtype=torch.int64, device=cuda))
+                sch.unpack_states(state, index)
+                out = out.double().cpu()
+                for b, s in enumerate(ready):
+                    rstate = StreamingState(
+                        s.dense, torch.tensor([s.proc], dtype=torch.int64), torch.tensor([s.cl], dtype=torch.int64)
+                    )
+                    rout, _ = ref(x[b : b + 1].double(), rstate, length=torch.full((1,), T, dtype=torch.int64))
+                    err = float((out[b] - rout[0]).abs().max())
+                    worst = max(worst, err)
+                    assert err <= 2e-4, f"step {step} slot {s.encoder_state}: max abs err {err:.3e}"
+                    s.proc += T
+                    s.cl = min(s.cl + T, left)
+                    s.done += 1
+                    compared += 1
+                pf = sch.pool_state.processed_frames.cpu().tolist()
+                for s in live:
+                    assert pf[s.encoder_state] == s.proc
+            for s in [s for s in live if s.done >= s.steps]:  # departures
+                sch.release_state_slot(s.encoder_state)
+                live.remove(s)
+    assert compared >= 60, compared
+    assert max(slot_users.values()) >= 2, "no slot was reused by a new stream"
+    print(f"  {int(compared)} stream-steps, worst max-abs error {worst:.3e}", flush=True)
+    torch.cuda.synchronize()
