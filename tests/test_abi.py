@@ -158,3 +158,24 @@ def test_rnnt_args_validated_before_launch():
     # workspace: per-stream words (4 + 2 x 9 vocabulary tiles) rounded to 256 B, then h'
     assert L.pk_rnnt_workspace_bytes(_lib.DTYPE_F16, 128, 1027, 1, 640) == 11264 + 128 * 640 * 2
     assert L.pk_rnnt_workspace_bytes(_lib.DTYPE_F32, 1, 1025, 2, 640) == 256 + 2 * 640 * 4
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    """With the HIP library absent, the product path raises instead of falling
+    back to anything else: the page pool, the cache and the kernel wrappers all
+    go through lib()."""
+    import torch
+
+    from parakeet_amd import _lib, ops
+    from parakeet_amd.modules.cache import ModelCache
+    from parakeet_amd.pool import PagePool
+
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "libparakeet_paged.so")
+    monkeypatch.setattr(_lib, "_lib", None)
+    with pytest.raises(RuntimeError, match="missing"):
+        PagePool(2, 16, 70, 2)
+    with pytest.raises(RuntimeError, match="missing"):
+        ModelCache(1, (70, 1), 64, 9, batch_size=2)
+    # host tensors are refused before the library is even looked up
+    with pytest.raises(RuntimeError, match="no CPU implementation|missing"):
+        ops.streaming_mask(torch.zeros(2, dtype=torch.int64), torch.zeros(2, dtype=torch.int64), 2, chunk=2, left=70, chunk_size=2)
