@@ -441,7 +441,9 @@ int pk_subsample(const pk_sub_args* args, void* stream);
  *   with prime != 0: the predictor run on the blank start token from zero state
  *       in ModelRunner.create_sequence model_runner.py:70-77 (no frames are read).
  *
- * slots      : int32 [batch] device, distinct, < num_slots.
+ * slots      : int32 [batch] device, distinct, < num_slots (a stream whose slot
+ *              is out of range is treated as absent: no tokens, zero counts,
+ *              no state read or written).
  * embed      : [vocab1][hidden] (nn.Embedding, vocab1 = vocabulary + blank).
  * w_ih, w_hh : [layers][4*hidden][hidden]; b_ih, b_hh: [layers][4*hidden]
  *              (nn.LSTM weight_ih_l*, ... stacked over layers).

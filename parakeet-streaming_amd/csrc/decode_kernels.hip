@@ -89,10 +89,18 @@ struct DecK {
 // stream state words in the workspace
 __device__ static inline int32_t* ws_of(const DecK& p, int b) { return p.ws + (int64_t)b * (kWsHead + 2 * p.vtiles); }
 
+// Stream b is in the batch and its slot addresses the state arrays.  A slot
+// outside them is a caller error the host wrapper rejects; the kernels treat such
+// a stream as absent (no tokens, no state read or written) rather than address
+// outside the state.
+__device__ static inline bool stream_ok(const DecK& p, int b) {
+  return b < p.batch && (uint32_t)p.slots[b] < (uint32_t)p.num_slots;
+}
+
 // A stream decides at (t, s) while t is one of its frames and it has not yet
 // decided blank in frame t (word 0 of its workspace: 1 = blank seen).
 __device__ static inline bool active_at(const DecK& p, int b, const int32_t* w) {
-  return b < p.batch && p.t < p.lengths[b] && (p.s == 0 || w[0] == 0);
+  return stream_ok(p, b) && p.t < p.lengths[b] && (p.s == 0 || w[0] == 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -249,8 +257,8 @@ __global__ void __launch_bounds__(LstmCfg<ST>::WAVES * 64) lstm_kernel(const Dec
     int tk = -1;
     if (b < p.batch) {
       if (p.prime) {
-        tk = p.blank;
-      } else if (layer == 0) {
+        tk = stream_ok(p, b) ? p.blank : -1;
+      } else if (layer == 0) {  // a stream with a bad slot is never active: no token, zero counts
         bool act;
         tk = decide(p, b, &act);
         if (blockIdx.x == 0) record(p, b, act, tk);
@@ -334,7 +342,7 @@ __global__ void __launch_bounds__(256) pred_kernel(const DecK p) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
   if (tid < 16) {
     const int b = b0 + tid;
-    tok_s[tid] = b < p.batch ? (p.prime ? 0 : ws_of(p, b)[1]) : -1;
+    tok_s[tid] = stream_ok(p, b) ? (p.prime ? 0 : ws_of(p, b)[1]) : -1;
   }
   __syncthreads();
   bool any = false;

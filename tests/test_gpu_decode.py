@@ -153,3 +153,30 @@ def test_graph_replay_matches_direct_launches(cuda):
         assert ta == tb, f"step {step}"
         assert torch.equal(a.h, b.h) and torch.equal(a.c, b.c) and torch.equal(a.pred_proj, b.pred_proj)
         torch.cuda.synchronize()
+
+
+def test_out_of_range_slot_is_skipped_by_the_kernels(cuda):
+    """A slot id outside the state arrays (a caller error the host wrapper
+    rejects) reaching the kernels through the C ABI: the kernels treat that
+    stream as absent -- no tokens, zero frame counts, no state read or written
+    -- and the batch's other streams decode exactly as they would next to a
+    valid stream (same batch size, so the same enc GEMM)."""
+    dt = torch.float16
+    pred, joint, _ = _model(1026, 512, 1, dt, cuda, seed=11)
+    a = GreedyDecoder(pred, joint, blank_id=1026, num_slots=4)
+    b = GreedyDecoder(pred, joint, blank_id=1026, num_slots=4)
+    a.reset_slot(range(4))
+    b.reset_slot(range(4))
+    a._check_slots = lambda slots: np.ascontiguousarray(np.asarray(slots, dtype=np.int32).reshape(-1))
+    enc = torch.randn(3, 3, 512, generator=torch.Generator().manual_seed(2)).to(dt).to(cuda)
+    before = (a.h.clone(), a.c.clone(), a.pred_proj.clone())
+    got = a.decode([0, 4, 2], enc, frame_tokens=True)
+    ref = b.decode([0, 1, 2], enc, frame_tokens=True)
+    assert got[1] == [[], [], []]
+    assert got[0] == ref[0] and got[2] == ref[2]
+    for s in (0, 2):
+        assert torch.equal(a.h[s], b.h[s]) and torch.equal(a.c[s], b.c[s]) and torch.equal(a.pred_proj[s], b.pred_proj[s])
+    for s in (1, 3):
+        assert torch.equal(a.h[s], before[0][s]) and torch.equal(a.c[s], before[1][s])
+        assert torch.equal(a.pred_proj[s], before[2][s])
+    torch.cuda.synchronize()
