@@ -177,31 +177,43 @@ def test_subsampling_matches_oracle(cuda, dt, Fm, C):
     _close_sub(y.double().cpu().numpy().reshape(-1, D), ref_y, dt, "out")
 
 
+# (n_mels, d_model, first chunk, next chunk, frames per step, sample ring,
+# mel ring, steps): the small model's chunking (right context 1: 9 then 16 mel
+# frames) and the large model's (right context 13: 105 then 112 mel frames,
+# 128 mels; config.py:5-31, model_runner.py:53-56) with rings sized for it
+PRE_CONFIGS = {
+    "small": (80, 512, 1440, 2560, 2, 8192, 64, 6),
+    "large": (128, 1024, 16800, 17920, 14, 32768, 256, 5),
+}
+
+
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
-def test_pre_encoder_stream_matches_oracle(cuda, dt):
-    """_run_pre_encode (model_runner.py:181-252) for 6 streams over 6 steps:
-    starts staggered, the reference's chunking (1440 samples, then 2560), one
-    stream finishing with a short final push.  Windows and row counts are
+@pytest.mark.parametrize("cfg", sorted(PRE_CONFIGS))
+def test_pre_encoder_stream_matches_oracle(cuda, dt, cfg):
+    """_run_pre_encode (model_runner.py:181-252) for 6 streams: starts
+    staggered, the reference's chunking (first chunk, then the next-chunk size),
+    one stream finishing with a short final push.  Windows and row counts are
     exact; rows match the oracle's subsampling of the GPU's own window."""
-    Fm, C, D = 80, 256, 512
+    Fm, D, n_first, n_next, T_out, ring, mrows, steps = PRE_CONFIGS[cfg]
+    C = 256
     fx = FeatureExtractor(n_mels=Fm, dither=1e-5, seed=3, device=cuda)
     m = _module(C, Fm, D, dt, cuda, seed=11)
-    pre = PreEncoder(fx, m, num_slots=8, device=cuda)
+    pre = PreEncoder(fx, m, num_slots=8, device=cuda, ring_size=ring, mel_rows=mrows)
     p = fe.FeParams(n_mels=Fm, dither=1e-5)
     sd = _sd(m)
     slots = np.array([5, 1, 7, 0, 2, 6])
     for s in slots:
         pre.reset_slot(s)
     start_step = [0, 0, 1, 2, 2, 3]
-    sigs = [_pcm(1440 + 6 * 2560, seed=20 + i) for i in range(6)]
+    sigs = [_pcm(n_first + steps * n_next, seed=20 + i) for i in range(6)]
     states = [fe.PreEncodeState(fe.FeState(p, noise_id=int(pre.noise_id[s]), seed=3), sd, store_dtype=dt) for s in slots]
     pos = [0] * 6
-    for step in range(6):
+    for step in range(steps):
         live = [i for i in range(6) if step >= start_step[i]]
         n_new, final = [], []
         for i in live:
             k = step - start_step[i]
-            n = 1440 if k == 0 else 2560
+            n = n_first if k == 0 else n_next
             if i == 3 and k == 2:
                 n, fin = 1000, True
             else:
@@ -210,7 +222,7 @@ def test_pre_encoder_stream_matches_oracle(cuda, dt):
                 n = 0
             n_new.append(n)
             final.append(fin)
-        pcm = np.zeros((len(live), 2560), dtype=np.int16)
+        pcm = np.zeros((len(live), n_next), dtype=np.int16)
         for r, i in enumerate(live):
             pcm[r, : n_new[r]] = sigs[i][pos[i] : pos[i] + n_new[r]]
         rows, counts, first = pre.step(slots[live], torch.from_numpy(pcm).to(cuda), np.array(n_new), np.array(final))
@@ -235,7 +247,7 @@ def test_pre_encoder_stream_matches_oracle(cuda, dt):
                 ref = ref[2:] if had_cache else ref
                 assert counts[r] == ref.shape[0]
                 if not final[r]:
-                    assert counts[r] == 2  # 1 + 8 frames first, then 16 (model_runner.py:53-56)
+                    assert counts[r] == T_out  # 1 + 8R frames first, then 8 + 8R (model_runner.py:53-56)
                 flat_ref = ref @ sd["out.weight"].T + sd["out.bias"]
                 got = rows[first[r] : first[r] + counts[r]]
                 _close_sub(got, flat_ref, dt, f"stream {i} step {step}")
