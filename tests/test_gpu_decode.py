@@ -41,10 +41,15 @@ def _tol(dt):
 
 
 @pytest.mark.parametrize(
-    "dt,layers,vocab,enc_dim,blank_bias",  # the bias gives a mix of tokens and blanks
-    [(torch.float16, 1, 1026, 512, 1.5), (torch.bfloat16, 2, 1024, 1024, 3.5), (torch.float32, 1, 1026, 512, 1.5)],
+    "dt,layers,vocab,enc_dim,blank_bias,T",  # the bias gives a mix of tokens and blanks
+    [
+        (torch.float16, 1, 1026, 512, 1.5, 3),
+        (torch.bfloat16, 2, 1024, 1024, 3.5, 3),
+        (torch.float32, 1, 1026, 512, 1.5, 3),
+        (torch.bfloat16, 2, 1024, 1024, 3.5, 14),  # the large model's 14 frames a step (config.py:25-31)
+    ],
 )
-def test_greedy_decode_matches_oracle_replay(cuda, dt, layers, vocab, enc_dim, blank_bias):
+def test_greedy_decode_matches_oracle_replay(cuda, dt, layers, vocab, enc_dim, blank_bias, T):
     pred, joint, P = _model(vocab, enc_dim, layers, dt, cuda, seed=layers + enc_dim, blank_bias=blank_bias)
     S, B = 20, 12
     dec = GreedyDecoder(pred, joint, blank_id=vocab, num_slots=S)
@@ -54,7 +59,6 @@ def test_greedy_decode_matches_oracle_replay(cuda, dt, layers, vocab, enc_dim, b
     oracles = [rnnt.StreamDecoder(P, vocab, dtype=dt) for _ in range(B)]
     n_dec = n_diff = n_tok = n_blankframes = 0
     for step in range(4):
-        T = 3
         lengths = rng.integers(0, T + 1, B)
         if step == 0:
             lengths[:] = T
