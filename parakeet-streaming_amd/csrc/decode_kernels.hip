@@ -103,6 +103,41 @@ __device__ static inline bool active_at(const DecK& p, int b, const int32_t* w) 
   return stream_ok(p, b) && p.t < p.lengths[b] && (p.s == 0 || w[0] == 0);
 }
 
+// Weight chunks loaded ahead of their MFMAs: 20 k-steps of a 16-bit row (10 of
+// fp32) per round trip, within the registers a decode wave has to spare.
+template <typename ST>
+struct KChunk {
+  static constexpr int CH = sizeof(ST) == 4 ? 10 : 20;
+};
+
+// d += the wave's 16 weight rows (A, from global memory) times 16 columns held
+// in LDS (B) over nk k-steps of 4*VEC elements.  Rows are read from `wa` for
+// k-steps [0, ka) and from `wb` (at k-step - ka) after it; the LDS column runs
+// contiguously over all nk k-steps.  The weight chunks of CH k-steps are issued
+// together before their MFMAs (the index clamped, so every load is valid), so a
+// wave waits for one L2 round trip per CH k-steps rather than one per k-step.
+// The k-steps accumulate in order, as a plain loop would.
+template <typename ST>
+__device__ static inline f32x4_t mma_rows(const ST* wa, const ST* wb, int ka, int nk, const ST* col, int lg,
+                                          f32x4_t d) {
+  constexpr int VEC = 16 / sizeof(ST), CH = KChunk<ST>::CH;
+  for (int k0 = 0; k0 < nk; k0 += CH) {
+    u32x4 w[CH];
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int kk = min(k0 + u, nk - 1);
+      const ST* src = kk < ka ? wa + kk * 4 * VEC : wb + (kk - ka) * 4 * VEC;
+      w[u] = ld16(src + VEC * lg);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the chunk's loads all issue before its first MFMA
+#pragma unroll
+    for (int u = 0; u < CH; ++u)
+      if (k0 + u < nk)
+        d = MmaR<ST>::step(w[u], *reinterpret_cast<const u32x4*>(col + (k0 + u) * 4 * VEC + VEC * lg), d);
+  }
+  return d;
+}
+
 // ---------------------------------------------------------------------------
 template <typename ST>
 __global__ void __launch_bounds__(512) joint_kernel(const DecK p) {
@@ -110,39 +145,57 @@ __global__ void __launch_bounds__(512) joint_kernel(const DecK p) {
   __shared__ __align__(16) ST hid[16][kMaxDim + 8];
   __shared__ float bv[8][16];
   __shared__ int bi[8][16];
+  __shared__ int32_t act_s[16], slot_s[16];
   const int vt = blockIdx.x, b0 = blockIdx.y * 16;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
+  if (tid < 16) {
+    const int b = b0 + tid;
+    const bool a = active_at(p, b, ws_of(p, min(b, p.batch - 1)));
+    act_s[tid] = a;
+    slot_s[tid] = a ? p.slots[b] : 0;
+  }
+  __syncthreads();
   bool any = false;
-  for (int k = 0; k < 16; ++k) any |= active_at(p, b0 + k, ws_of(p, min(b0 + k, p.batch - 1)));
+  for (int k = 0; k < 16; ++k) any |= act_s[k] != 0;
   if (!any) return;  // uniform: every stream of the tile is done for this frame
-  // hid for the 16 streams (zero for streams not deciding)
+  // hid for the 16 streams (zero for streams not deciding): every load is issued
+  // first, from an address that is valid for any stream, then masked
   const int J = p.J, nch = J / VEC;
-  for (int i = tid; i < 16 * nch; i += 512) {
+  constexpr int IT = (16 * kMaxDim / VEC + 511) / 512;
+  u32x4 er[IT], qr[IT];
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int i = min(tid + it * 512, 16 * nch - 1);
     const int k = i / nch, cc = (i - k * nch) * VEC;
-    const int b = b0 + k;
-    float out[VEC];
-    if (b < p.batch && active_at(p, b, ws_of(p, b))) {
-      float e[VEC], q[VEC];
-      Tr<ST>::unpack(ld16((const ST*)p.enc + b * p.enc_sb + (int64_t)p.t * p.enc_st + cc), e);
-      Tr<ST>::unpack(ld16((const ST*)p.pred_proj + (int64_t)p.slots[b] * J + cc), q);
+    const int b = min(b0 + k, p.batch - 1);
+    er[it] = ld16((const ST*)p.enc + b * p.enc_sb + (int64_t)p.t * p.enc_st + cc);
+    qr[it] = ld16((const ST*)p.pred_proj + (int64_t)slot_s[k] * J + cc);
+  }
 #pragma unroll
-      for (int u = 0; u < VEC; ++u) out[u] = fmaxf(round_to<ST>(e[u] + q[u]), 0.f);
-    } else {
+  for (int it = 0; it < IT; ++it) {
+    const int i = tid + it * 512;
+    if (i < 16 * nch) {
+      const int k = i / nch, cc = (i - k * nch) * VEC;
+      float out[VEC];
+      if (act_s[k]) {
+        float e[VEC], q[VEC];
+        Tr<ST>::unpack(er[it], e);
+        Tr<ST>::unpack(qr[it], q);
 #pragma unroll
-      for (int u = 0; u < VEC; ++u) out[u] = 0.f;
+        for (int u = 0; u < VEC; ++u) out[u] = fmaxf(round_to<ST>(e[u] + q[u]), 0.f);
+      } else {
+#pragma unroll
+        for (int u = 0; u < VEC; ++u) out[u] = 0.f;
+      }
+      *reinterpret_cast<u32x4*>(&hid[k][cc]) = Tr<ST>::pack(out);
     }
-    *reinterpret_cast<u32x4*>(&hid[k][cc]) = Tr<ST>::pack(out);
   }
   __syncthreads();
   // logits of rows vt*128 + 16*wave .. for the 16 streams
   const int r = vt * kVT + wave * 16 + lr;
   const ST* wrow = (const ST*)p.w_out + (int64_t)min(r, p.V1 - 1) * J;
-  f32x4_t d = {0.f, 0.f, 0.f, 0.f};
   const int ks = J / (4 * VEC);
-  for (int kk = 0; kk < ks; ++kk) {
-    const int k = kk * 4 * VEC + VEC * lg;
-    d = MmaR<ST>::step(ld16(wrow + k), *reinterpret_cast<const u32x4*>(&hid[lr][k]), d);
-  }
+  const f32x4_t d = mma_rows<ST>(wrow, wrow, ks, ks, &hid[lr][0], lg, f32x4_t{0.f, 0.f, 0.f, 0.f});
   // lane holds rows 4*lg + i (of the wave's 16) for stream lr
   float best = -INFINITY;
   int bidx = 0x7fffffff;
@@ -195,14 +248,22 @@ __device__ static inline int decide(const DecK& p, int b, bool* act_out) {
   const bool act = active_at(p, b, ws);
   *act_out = act;
   if (!act) return -1;
-  float v = __int_as_float(ws[kWsHead]);
-  int ix = ws[kWsHead + 1];
-  for (int k = 1; k < p.vtiles; ++k) {
-    const float ov = __int_as_float(ws[kWsHead + 2 * k]);
-    const int oi = ws[kWsHead + 2 * k + 1];
-    if (ov > v || (ov == v && oi < ix)) {
-      v = ov;
-      ix = oi;
+  // tiles in ascending order; the (max, index) pairs of 8 tiles are loaded
+  // together ahead of their compares
+  float v = 0.f;
+  int ix = -1;
+  for (int k0 = 0; k0 < p.vtiles; k0 += 8) {
+    int2 m[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) m[u] = *reinterpret_cast<const int2*>(ws + kWsHead + 2 * min(k0 + u, p.vtiles - 1));
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float ov = __int_as_float(m[u].x);
+      const int oi = m[u].y;
+      if (k0 + u < p.vtiles && (k0 + u == 0 || ov > v || (ov == v && oi < ix))) {
+        v = ov;
+        ix = oi;
+      }
     }
   }
   return (ix == p.blank || ix < 0 || ix >= p.V1) ? -1 : ix;
@@ -246,8 +307,9 @@ __global__ void __launch_bounds__(LstmCfg<ST>::WAVES * 64) lstm_kernel(const Dec
   constexpr int RS = 2 * 640 + VEC;  // [x ; h] row of one stream (hidden 640 in LDS)
   __shared__ __align__(16) ST inp[SPW][RS];
   __shared__ float gsm[4][SPW][17];
-  __shared__ int32_t tok_s[SPW];
-  const int H = p.H, L = p.layers, layer = p.layer;
+  __shared__ int32_t tok_s[SPW], slot_s[SPW];
+  constexpr int H = 640;  // the hidden size the host accepts
+  const int L = p.layers, layer = p.layer;
   const int u0 = blockIdx.x * 16, b0 = blockIdx.y * SPW;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
   // which streams update: layer 0 decides (prime: every stream, token blank),
@@ -267,47 +329,49 @@ __global__ void __launch_bounds__(LstmCfg<ST>::WAVES * 64) lstm_kernel(const Dec
       }
     }
     tok_s[tid] = tk;
+    slot_s[tid] = tk >= 0 ? p.slots[b] : 0;  // a stream that updates has a valid slot
   }
   __syncthreads();
   bool any = false;
   for (int k = 0; k < SPW; ++k) any |= tok_s[k] >= 0;
-  const int nch = H / VEC;
+  constexpr int nch = H / VEC;
   if (!any) return;  // uniform: no stream of the tile updates
   // [x ; h] of each stream: x = embedding row of the token (layer 0) or the new
-  // h of the layer below; h = this layer's current h
-  for (int i = tid; i < SPW * 2 * nch; i += Cfg::WAVES * 64) {
+  // h of the layer below; h = this layer's current h (zero on a stream's first
+  // step).  Every load is issued first, from an address valid for any stream,
+  // then masked.
+  constexpr int NTH = Cfg::WAVES * 64, IT = (SPW * 2 * nch + NTH - 1) / NTH;
+  u32x4 xr[IT];
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int i = min(tid + it * NTH, SPW * 2 * nch - 1);
     const int k = i / (2 * nch), cc = (i - k * 2 * nch) * VEC;
-    const int b = b0 + k;
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (b < p.batch && tok_s[k] >= 0) {
-      const int64_t slot = p.slots[b];
-      if (cc < H) {
-        if (layer == 0)
-          v = ld16((const ST*)p.embed + (int64_t)tok_s[k] * H + cc);
-        else
-          v = ld16((const ST*)p.hn + ((int64_t)b * L + layer - 1) * H + cc);
-      } else if (!p.prime) {  // a stream's first step starts from zero state
-        v = ld16((const ST*)p.h + (slot * L + layer) * H + cc - H);
-      }
+    const int b = min(b0 + k, p.batch - 1);
+    const ST* src;
+    if (cc < H)
+      src = layer == 0 ? (const ST*)p.embed + (int64_t)max(tok_s[k], 0) * H + cc
+                       : (const ST*)p.hn + ((int64_t)b * L + layer - 1) * H + cc;
+    else
+      src = (const ST*)p.h + ((int64_t)slot_s[k] * L + layer) * H + cc - H;
+    xr[it] = ld16(src);
+  }
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int i = tid + it * NTH;
+    if (i < SPW * 2 * nch) {
+      const int k = i / (2 * nch), cc = (i - k * 2 * nch) * VEC;
+      const bool keep = tok_s[k] >= 0 && (cc < H || !p.prime);
+      *reinterpret_cast<u32x4*>(&inp[k][cc]) = keep ? xr[it] : u32x4{0u, 0u, 0u, 0u};
     }
-    *reinterpret_cast<u32x4*>(&inp[k][cc]) = v;
   }
   __syncthreads();
-  // gate gi rows gi*H + u0 .. +16 for stream tile sb
+  // gate gi rows gi*H + u0 .. +16 for stream tile sb: K = [x ; h] against
+  // [W_ih | W_hh]
   const int gi = wave & 3, sb = wave >> 2;
   const int64_t row = (int64_t)layer * 4 * H + gi * H + u0 + lr;
-  const ST* wi = (const ST*)p.w_ih + row * H;
-  const ST* wh = (const ST*)p.w_hh + row * H;
-  f32x4_t d = {0.f, 0.f, 0.f, 0.f};
-  const int ks = H / (4 * VEC);
-  for (int kk = 0; kk < ks; ++kk) {
-    const int k = kk * 4 * VEC + VEC * lg;
-    d = MmaR<ST>::step(ld16(wi + k), *reinterpret_cast<const u32x4*>(&inp[sb * 16 + lr][k]), d);
-  }
-  for (int kk = 0; kk < ks; ++kk) {
-    const int k = kk * 4 * VEC + VEC * lg;
-    d = MmaR<ST>::step(ld16(wh + k), *reinterpret_cast<const u32x4*>(&inp[sb * 16 + lr][H + k]), d);
-  }
+  constexpr int ks = H / (4 * VEC);
+  const f32x4_t d = mma_rows<ST>((const ST*)p.w_ih + row * H, (const ST*)p.w_hh + row * H, ks, 2 * ks,
+                                 &inp[sb * 16 + lr][0], lg, f32x4_t{0.f, 0.f, 0.f, 0.f});
   // lane: units u0 + 4*lg + i of gate gi, stream sb*16 + lr
 #pragma unroll
   for (int i = 0; i < 4; ++i) gsm[gi][sb * 16 + lr][4 * lg + i] = d[i];
@@ -316,7 +380,7 @@ __global__ void __launch_bounds__(LstmCfg<ST>::WAVES * 64) lstm_kernel(const Dec
   for (int i = tid; i < SPW * 16; i += Cfg::WAVES * 64) {
     const int k = i / 16, u = i % 16, b = b0 + k;
     if (b >= p.batch || tok_s[k] < 0) continue;
-    const int64_t so = ((int64_t)p.slots[b] * L + layer) * H + u0 + u;
+    const int64_t so = ((int64_t)slot_s[k] * L + layer) * H + u0 + u;
     const int64_t bo = (int64_t)layer * 4 * H + u0 + u;
     float g4[4];
 #pragma unroll
@@ -336,32 +400,61 @@ template <typename ST>
 __global__ void __launch_bounds__(256) pred_kernel(const DecK p) {
   constexpr int VEC = 16 / sizeof(ST);
   __shared__ __align__(16) ST hs[16][kMaxDim + 8];
-  __shared__ int32_t tok_s[16];
-  const int H = p.H, J = p.J, L = p.layers;
+  __shared__ int32_t tok_s[16], slot_s[16];
+  constexpr int H = 640;  // the hidden size the host accepts
+  const int J = p.J, L = p.layers;
   const int j0 = blockIdx.x * 64, b0 = blockIdx.y * 16;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
   if (tid < 16) {
     const int b = b0 + tid;
-    tok_s[tid] = stream_ok(p, b) ? (p.prime ? 0 : ws_of(p, b)[1]) : -1;
+    const int tk = stream_ok(p, b) ? (p.prime ? 0 : ws_of(p, b)[1]) : -1;
+    tok_s[tid] = tk;
+    slot_s[tid] = tk >= 0 ? p.slots[b] : 0;
   }
   __syncthreads();
   bool any = false;
   for (int k = 0; k < 16; ++k) any |= tok_s[k] >= 0;
   if (!any) return;
-  const int nch = H / VEC;
-  for (int i = tid; i < 16 * nch; i += 256) {
-    const int k = i / nch, cc = (i - k * nch) * VEC, b = b0 + k;
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (b < p.batch && tok_s[k] >= 0) v = ld16((const ST*)p.hn + ((int64_t)b * L + L - 1) * H + cc);
-    *reinterpret_cast<u32x4*>(&hs[k][cc]) = v;
+  // the top layer's new h of the 16 streams: loads first (valid addresses for
+  // any stream), then masked into LDS
+  constexpr int nch = H / VEC, IT = (16 * nch + 255) / 256;
+  u32x4 hr[IT];
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int i = min(tid + it * 256, 16 * nch - 1);
+    const int k = i / nch, cc = (i - k * nch) * VEC, b = min(b0 + k, p.batch - 1);
+    hr[it] = ld16((const ST*)p.hn + ((int64_t)b * L + L - 1) * H + cc);
   }
-  // the new h of every layer into the slot state (one column of workgroups)
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int i = tid + it * 256;
+    if (i < 16 * nch) {
+      const int k = i / nch, cc = (i - k * nch) * VEC;
+      *reinterpret_cast<u32x4*>(&hs[k][cc]) = tok_s[k] >= 0 ? hr[it] : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  // the new h of every layer into the slot state (one column of workgroups),
+  // IT chunks per thread at a time: loads, then stores
   if (blockIdx.x == 0) {
-    for (int i = tid; i < 16 * L * nch; i += 256) {
-      const int k = i / (L * nch), r = i - k * L * nch, b = b0 + k;
-      if (b < p.batch && tok_s[k] >= 0) {
+    for (int i0 = 0; i0 < 16 * L * nch; i0 += 256 * IT) {
+      u32x4 v[IT];
+#pragma unroll
+      for (int it = 0; it < IT; ++it) {
+        const int i = min(i0 + tid + it * 256, 16 * L * nch - 1);
+        const int k = i / (L * nch), r = i - k * L * nch, b = min(b0 + k, p.batch - 1);
         const int l = r / nch, cc = (r - l * nch) * VEC;
-        st16((ST*)p.h + ((int64_t)p.slots[b] * L + l) * H + cc, ld16((const ST*)p.hn + ((int64_t)b * L + l) * H + cc));
+        v[it] = ld16((const ST*)p.hn + ((int64_t)b * L + l) * H + cc);
+      }
+#pragma unroll
+      for (int it = 0; it < IT; ++it) {
+        const int i = i0 + tid + it * 256;
+        if (i < 16 * L * nch) {
+          const int k = i / (L * nch), r = i - k * L * nch;
+          if (tok_s[k] >= 0) {
+            const int l = r / nch, cc = (r - l * nch) * VEC;
+            st16((ST*)p.h + ((int64_t)slot_s[k] * L + l) * H + cc, v[it]);
+          }
+        }
       }
     }
   }
@@ -369,18 +462,14 @@ __global__ void __launch_bounds__(256) pred_kernel(const DecK p) {
   const int j = j0 + wave * 16 + lr;
   if (j0 + wave * 16 >= J) return;  // uniform per wave; no barrier below
   const ST* wrow = (const ST*)p.w_pred + (int64_t)j * H;
-  f32x4_t d = {0.f, 0.f, 0.f, 0.f};
-  for (int kk = 0; kk < H / (4 * VEC); ++kk) {
-    const int k = kk * 4 * VEC + VEC * lg;
-    d = MmaR<ST>::step(ld16(wrow + k), *reinterpret_cast<const u32x4*>(&hs[lr][k]), d);
-  }
+  constexpr int ks = H / (4 * VEC);
+  const f32x4_t d = mma_rows<ST>(wrow, wrow, ks, ks, &hs[lr][0], lg, f32x4_t{0.f, 0.f, 0.f, 0.f});
   // lane: outputs j0 + 16 wave + 4 lg + i for stream lr
-  const int b = b0 + lr;
-  if (b < p.batch && tok_s[lr] >= 0) {
+  if (tok_s[lr] >= 0) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int jj = j0 + wave * 16 + 4 * lg + i;
-      ((ST*)p.pred_proj)[(int64_t)p.slots[b] * J + jj] =
+      ((ST*)p.pred_proj)[(int64_t)slot_s[lr] * J + jj] =
           to_st<ST>(d[i] + from_st(((const ST*)p.b_pred)[jj]));
     }
   }
