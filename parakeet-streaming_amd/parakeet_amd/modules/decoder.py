@@ -259,17 +259,23 @@ class GreedyDecoder:
 
     @staticmethod
     def _split(tok: np.ndarray, cnt: np.ndarray, lens: np.ndarray, frame_tokens: bool):
+        """Per-stream token lists from the step's [B, frames * max_symbols] tokens
+        and [B, frames] counts (frames past a stream's length count nothing); the
+        counts and offsets are computed for the whole batch at once."""
         B = len(lens)
-        out = []
-        for b in range(B):
-            n = cnt[b, : lens[b]]
-            flat = tok[b, : int(n.sum())].tolist()
-            if frame_tokens:
-                edges = np.concatenate([[0], np.cumsum(n)])
-                out.append([flat[edges[i] : edges[i + 1]] for i in range(len(n))])
-            else:
-                out.append(flat)
-        return out
+        if B == 0:
+            return []
+        T = cnt.shape[1]
+        n = np.where(np.arange(T)[None, :] < np.asarray(lens)[:, None], cnt, 0).astype(np.int64)
+        tot = n.sum(1)
+        # the emitted tokens only, stream after stream, as one list
+        flat = tok[np.arange(tok.shape[1])[None, :] < tot[:, None]].tolist()
+        off = np.concatenate([[0], np.cumsum(tot)])
+        if not frame_tokens:
+            o = off.tolist()
+            return [flat[o[b] : o[b + 1]] for b in range(B)]
+        edges = (off[:-1, None] + np.concatenate([np.zeros((B, 1), dtype=np.int64), np.cumsum(n, axis=1)], axis=1)).tolist()
+        return [[flat[e[i] : e[i + 1]] for i in range(int(l))] for e, l in zip(edges, lens)]
 
 
 __all__ = ["Predictor", "Joiner", "GreedyDecoder"]
