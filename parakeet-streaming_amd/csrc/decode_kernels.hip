@@ -110,30 +110,47 @@ struct KChunk {
   static constexpr int CH = sizeof(ST) == 4 ? 10 : 20;
 };
 
-// d += the wave's 16 weight rows (A, from global memory) times 16 columns held
-// in LDS (B) over nk k-steps of 4*VEC elements.  Rows are read from `wa` for
+// The wave's 16 weight rows (A, from global memory) against 16 columns held in
+// LDS (B), over nk k-steps of 4*VEC elements.  Rows are read from `wa` for
 // k-steps [0, ka) and from `wb` (at k-step - ka) after it; the LDS column runs
-// contiguously over all nk k-steps.  The weight chunks of CH k-steps are issued
-// together before their MFMAs (the index clamped, so every load is valid), so a
-// wave waits for one L2 round trip per CH k-steps rather than one per k-step.
-// The k-steps accumulate in order, as a plain loop would.
+// contiguously over all nk k-steps.  Weights move in chunks of CH k-steps whose
+// loads are all issued before the chunk's first MFMA (the index clamped, so
+// every load is valid): a wave waits for one L2 round trip per CH k-steps rather
+// than one per k-step.  The k-steps accumulate in order, as a plain loop would.
 template <typename ST>
-__device__ static inline f32x4_t mma_rows(const ST* wa, const ST* wb, int ka, int nk, const ST* col, int lg,
-                                          f32x4_t d) {
+__device__ static inline void load_chunk(u32x4 (&w)[KChunk<ST>::CH], const ST* wa, const ST* wb, int ka, int nk,
+                                         int k0, int lg) {
   constexpr int VEC = 16 / sizeof(ST), CH = KChunk<ST>::CH;
-  for (int k0 = 0; k0 < nk; k0 += CH) {
+#pragma unroll
+  for (int u = 0; u < CH; ++u) {
+    const int kk = min(k0 + u, nk - 1);
+    const ST* src = kk < ka ? wa + kk * 4 * VEC : wb + (kk - ka) * 4 * VEC;
+    w[u] = ld16(src + VEC * lg);
+  }
+}
+
+template <typename ST>
+__device__ static inline f32x4_t mma_chunk(const u32x4 (&w)[KChunk<ST>::CH], const ST* col, int k0, int nk, int lg,
+                                           f32x4_t d) {
+  constexpr int VEC = 16 / sizeof(ST), CH = KChunk<ST>::CH;
+#pragma unroll
+  for (int u = 0; u < CH; ++u)
+    if (k0 + u < nk) d = MmaR<ST>::step(w[u], *reinterpret_cast<const u32x4*>(col + (k0 + u) * 4 * VEC + VEC * lg), d);
+  return d;
+}
+
+// d += the product, with the first chunk's weights already loaded into w0 (its
+// loads issued early, so their round trip overlaps the caller's other loads).
+template <typename ST>
+__device__ static inline f32x4_t mma_rows(const u32x4 (&w0)[KChunk<ST>::CH], const ST* wa, const ST* wb, int ka,
+                                          int nk, const ST* col, int lg, f32x4_t d) {
+  constexpr int CH = KChunk<ST>::CH;
+  d = mma_chunk<ST>(w0, col, 0, nk, lg, d);
+  for (int k0 = CH; k0 < nk; k0 += CH) {
     u32x4 w[CH];
-#pragma unroll
-    for (int u = 0; u < CH; ++u) {
-      const int kk = min(k0 + u, nk - 1);
-      const ST* src = kk < ka ? wa + kk * 4 * VEC : wb + (kk - ka) * 4 * VEC;
-      w[u] = ld16(src + VEC * lg);
-    }
+    load_chunk<ST>(w, wa, wb, ka, nk, k0, lg);
     __builtin_amdgcn_sched_barrier(0);  // the chunk's loads all issue before its first MFMA
-#pragma unroll
-    for (int u = 0; u < CH; ++u)
-      if (k0 + u < nk)
-        d = MmaR<ST>::step(w[u], *reinterpret_cast<const u32x4*>(col + (k0 + u) * 4 * VEC + VEC * lg), d);
+    d = mma_chunk<ST>(w, col, k0, nk, lg, d);
   }
   return d;
 }
@@ -158,9 +175,19 @@ __global__ void __launch_bounds__(512) joint_kernel(const DecK p) {
   bool any = false;
   for (int k = 0; k < 16; ++k) any |= act_s[k] != 0;
   if (!any) return;  // uniform: every stream of the tile is done for this frame
+  // the weight rows' first chunk and the biases of the lane's 4 rows: loads
+  // that depend on nothing, issued ahead of the staging loads
+  const int J = p.J, nch = J / VEC, ks = J / (4 * VEC);
+  const int r = vt * kVT + wave * 16 + lr;
+  const ST* wrow = (const ST*)p.w_out + (int64_t)min(r, p.V1 - 1) * J;
+  u32x4 w0[KChunk<ST>::CH];
+  load_chunk<ST>(w0, wrow, wrow, ks, ks, 0, lg);
+  float bias[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) bias[i] = from_st(((const ST*)p.b_out)[min(vt * kVT + wave * 16 + 4 * lg + i, p.V1 - 1)]);
+  __builtin_amdgcn_sched_barrier(0);
   // hid for the 16 streams (zero for streams not deciding): every load is issued
   // first, from an address that is valid for any stream, then masked
-  const int J = p.J, nch = J / VEC;
   constexpr int IT = (16 * kMaxDim / VEC + 511) / 512;
   u32x4 er[IT], qr[IT];
 #pragma unroll
@@ -192,10 +219,7 @@ __global__ void __launch_bounds__(512) joint_kernel(const DecK p) {
   }
   __syncthreads();
   // logits of rows vt*128 + 16*wave .. for the 16 streams
-  const int r = vt * kVT + wave * 16 + lr;
-  const ST* wrow = (const ST*)p.w_out + (int64_t)min(r, p.V1 - 1) * J;
-  const int ks = J / (4 * VEC);
-  const f32x4_t d = mma_rows<ST>(wrow, wrow, ks, ks, &hid[lr][0], lg, f32x4_t{0.f, 0.f, 0.f, 0.f});
+  const f32x4_t d = mma_rows<ST>(w0, wrow, wrow, ks, ks, &hid[lr][0], lg, f32x4_t{0.f, 0.f, 0.f, 0.f});
   // lane holds rows 4*lg + i (of the wave's 16) for stream lr
   float best = -INFINITY;
   int bidx = 0x7fffffff;
@@ -203,7 +227,7 @@ __global__ void __launch_bounds__(512) joint_kernel(const DecK p) {
   for (int i = 0; i < 4; ++i) {
     const int row = vt * kVT + wave * 16 + 4 * lg + i;
     if (row < p.V1) {
-      const float v = round_to<ST>(d[i] + from_st(((const ST*)p.b_out)[row]));
+      const float v = round_to<ST>(d[i] + bias[i]);
       if (v > best) {  // rows ascend: the first maximum wins ties
         best = v;
         bidx = row;
@@ -336,6 +360,16 @@ __global__ void __launch_bounds__(LstmCfg<ST>::WAVES * 64) lstm_kernel(const Dec
   for (int k = 0; k < SPW; ++k) any |= tok_s[k] >= 0;
   constexpr int nch = H / VEC;
   if (!any) return;  // uniform: no stream of the tile updates
+  // gate gi rows gi*H + u0 .. +16 for stream tile sb: K = [x ; h] against
+  // [W_ih | W_hh]; the first weight chunk is issued ahead of the staging loads
+  const int gi = wave & 3, sb = wave >> 2;
+  const int64_t row = (int64_t)layer * 4 * H + gi * H + u0 + lr;
+  constexpr int ks = H / (4 * VEC);
+  const ST* wi = (const ST*)p.w_ih + row * H;
+  const ST* wh = (const ST*)p.w_hh + row * H;
+  u32x4 w0[KChunk<ST>::CH];
+  load_chunk<ST>(w0, wi, wh, ks, 2 * ks, 0, lg);
+  __builtin_amdgcn_sched_barrier(0);
   // [x ; h] of each stream: x = embedding row of the token (layer 0) or the new
   // h of the layer below; h = this layer's current h (zero on a stream's first
   // step).  Every load is issued first, from an address valid for any stream,
@@ -365,13 +399,7 @@ __global__ void __launch_bounds__(LstmCfg<ST>::WAVES * 64) lstm_kernel(const Dec
     }
   }
   __syncthreads();
-  // gate gi rows gi*H + u0 .. +16 for stream tile sb: K = [x ; h] against
-  // [W_ih | W_hh]
-  const int gi = wave & 3, sb = wave >> 2;
-  const int64_t row = (int64_t)layer * 4 * H + gi * H + u0 + lr;
-  constexpr int ks = H / (4 * VEC);
-  const f32x4_t d = mma_rows<ST>((const ST*)p.w_ih + row * H, (const ST*)p.w_hh + row * H, ks, 2 * ks,
-                                 &inp[sb * 16 + lr][0], lg, f32x4_t{0.f, 0.f, 0.f, 0.f});
+  const f32x4_t d = mma_rows<ST>(w0, wi, wh, ks, 2 * ks, &inp[sb * 16 + lr][0], lg, f32x4_t{0.f, 0.f, 0.f, 0.f});
   // lane: units u0 + 4*lg + i of gate gi, stream sb*16 + lr
 #pragma unroll
   for (int i = 0; i < 4; ++i) gsm[gi][sb * 16 + lr][4 * lg + i] = d[i];
@@ -415,6 +443,14 @@ __global__ void __launch_bounds__(256) pred_kernel(const DecK p) {
   bool any = false;
   for (int k = 0; k < 16; ++k) any |= tok_s[k] >= 0;
   if (!any) return;
+  // this wave's weight rows (their first chunk issued ahead of the staging
+  // loads); a wave past the joint size keeps its lanes but loads row J - 1
+  constexpr int ks = H / (4 * VEC);
+  const bool wave_live = j0 + wave * 16 < J;  // uniform per wave
+  const ST* wrow = (const ST*)p.w_pred + (int64_t)min(j0 + wave * 16 + lr, J - 1) * H;
+  u32x4 w0[KChunk<ST>::CH];
+  load_chunk<ST>(w0, wrow, wrow, ks, ks, 0, lg);
+  __builtin_amdgcn_sched_barrier(0);
   // the top layer's new h of the 16 streams: loads first (valid addresses for
   // any stream), then masked into LDS
   constexpr int nch = H / VEC, IT = (16 * nch + 255) / 256;
@@ -459,11 +495,8 @@ __global__ void __launch_bounds__(256) pred_kernel(const DecK p) {
     }
   }
   __syncthreads();
-  const int j = j0 + wave * 16 + lr;
-  if (j0 + wave * 16 >= J) return;  // uniform per wave; no barrier below
-  const ST* wrow = (const ST*)p.w_pred + (int64_t)j * H;
-  constexpr int ks = H / (4 * VEC);
-  const f32x4_t d = mma_rows<ST>(wrow, wrow, ks, ks, &hs[lr][0], lg, f32x4_t{0.f, 0.f, 0.f, 0.f});
+  if (!wave_live) return;  // uniform per wave; no barrier below
+  const f32x4_t d = mma_rows<ST>(w0, wrow, wrow, ks, ks, &hs[lr][0], lg, f32x4_t{0.f, 0.f, 0.f, 0.f});
   // lane: outputs j0 + 16 wave + 4 lg + i for stream lr
   if (tok_s[lr] >= 0) {
 #pragma unroll
