@@ -319,7 +319,7 @@ __device__ static inline void record(const DecK& p, int b, bool act, int tok) {
 // ---------------------------------------------------------------------------
 template <typename ST>
 struct LstmCfg {
-  static constexpr int SPW = sizeof(ST) == 4 ? 16 : 32;  // streams per workgroup
+  static constexpr int SPW = 16;  // streams per workgroup
   static constexpr int WAVES = 4 * (SPW / 16);           // 4 gates x stream tiles
   static constexpr int KMAX = 2 * kMaxDim;
 };
