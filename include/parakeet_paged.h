@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define PK_ABI_VERSION 6
+#define PK_ABI_VERSION 7
 
 enum pk_dtype { PK_DTYPE_F32 = 0, PK_DTYPE_F16 = 1, PK_DTYPE_BF16 = 2 };
 
@@ -454,6 +454,12 @@ int pk_subsample(const pk_sub_args* args, void* stream);
  * lengths    : int32 [batch] frames of each stream (<= max_frames).
  * tokens     : int32 [batch][max_frames * max_symbols] out: the emitted tokens;
  *              frame_counts: int32 [batch][max_frames] out: tokens per frame.
+ * compact    : 0 (by batch size: from 1024 streams), 1 or -1.  Compact mode
+ *              keeps, per iteration, a device list of the streams that emitted a
+ *              token: the next symbol's joint and the LSTM and projection
+ *              launches run over that list instead of every 16-stream tile that
+ *              holds one such stream (one more small launch per iteration, which
+ *              decides and builds the list).  Outputs are the same either way.
  * workspace  : device bytes, at least pk_rnnt_workspace_bytes(...), 16-aligned.
  * One dtype for every floating tensor; fp32 accumulation.  hidden must be 640
  * (both reference models, config.py:19-21); joint a multiple of 64, <= 1024.
@@ -488,6 +494,7 @@ typedef struct pk_rnnt_args {
   int64_t enc_stride_t;
   const int32_t* lengths;
   int32_t max_frames;
+  int32_t compact;  /* 0: by batch size, 1: always, -1: never (see below) */
   int32_t* tokens;
   int32_t* frame_counts;
   void* workspace;

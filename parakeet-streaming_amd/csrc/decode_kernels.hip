@@ -62,6 +62,7 @@ struct MmaR<float> {
 };
 
 constexpr int kVT = 128;      // vocabulary rows per joint workgroup
+constexpr int kCompactMinBatch = 1024;  // compact mode by default from this batch
 constexpr int kMaxDim = 1024;  // hidden / joint sizes held in LDS
 // per-stream words of the step workspace: flag, token, emitted count, pad
 constexpr int kWsHead = 4;
@@ -84,6 +85,12 @@ struct DecK {
   int32_t* ws;            // [batch][kWsHead + 2 * vtiles]
   int32_t layer;
   int32_t prime;
+  // compact mode: list[i & 1] holds the streams that emitted a token in
+  // iteration i = t * max_symbols + s, count[i & 1] their number
+  int32_t* alist;   // [2][batch]
+  int32_t* acount;  // [2]
+  int32_t compact;
+  int32_t it;
 };
 
 // stream state words in the workspace
@@ -101,6 +108,16 @@ __device__ static inline bool stream_ok(const DecK& p, int b) {
 // decided blank in frame t (word 0 of its workspace: 1 = blank seen).
 __device__ static inline bool active_at(const DecK& p, int b, const int32_t* w) {
   return stream_ok(p, b) && p.t < p.lengths[b] && (p.s == 0 || w[0] == 0);
+}
+
+// Entry e of a launch's stream set: the batch itself (list < 0), or list
+// `list` of the streams that emitted a token; -1 past the set.
+__device__ static inline int listed_stream(const DecK& p, int list, int e) {
+  if (e >= p.batch) return -1;
+  if (list < 0) return e;
+  if (e >= min(p.acount[list], p.batch)) return -1;
+  const int b = p.alist[(int64_t)list * p.batch + e];
+  return (uint32_t)b < (uint32_t)p.batch ? b : -1;
 }
 
 // Weight chunks loaded ahead of their MFMAs: 20 k-steps of a 16-bit row (10 of
@@ -162,14 +179,21 @@ __global__ void __launch_bounds__(512) joint_kernel(const DecK p) {
   __shared__ __align__(16) ST hid[16][kMaxDim + 8];
   __shared__ float bv[8][16];
   __shared__ int bi[8][16];
-  __shared__ int32_t act_s[16], slot_s[16];
+  __shared__ int32_t act_s[16], slot_s[16], bid_s[16];
   const int vt = blockIdx.x, b0 = blockIdx.y * 16;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
+  // this iteration's list starts empty (its other half, read below, is the
+  // previous iteration's)
+  if (p.compact && vt == 0 && blockIdx.y == 0 && tid == 0) p.acount[p.it & 1] = 0;
+  // the tile's streams: the batch, or after a frame's first symbol (compact
+  // mode) the streams that emitted a token in the previous iteration
+  const int list = p.compact && p.s > 0 ? (p.it - 1) & 1 : -1;
   if (tid < 16) {
-    const int b = b0 + tid;
-    const bool a = active_at(p, b, ws_of(p, min(b, p.batch - 1)));
+    const int b = listed_stream(p, list, b0 + tid);
+    const bool a = b >= 0 && active_at(p, b, ws_of(p, b));
     act_s[tid] = a;
     slot_s[tid] = a ? p.slots[b] : 0;
+    bid_s[tid] = b;
   }
   __syncthreads();
   bool any = false;
@@ -194,7 +218,7 @@ __global__ void __launch_bounds__(512) joint_kernel(const DecK p) {
   for (int it = 0; it < IT; ++it) {
     const int i = min(tid + it * 512, 16 * nch - 1);
     const int k = i / nch, cc = (i - k * nch) * VEC;
-    const int b = min(b0 + k, p.batch - 1);
+    const int b = max(bid_s[k], 0);
     er[it] = ld16((const ST*)p.enc + b * p.enc_sb + (int64_t)p.t * p.enc_st + cc);
     qr[it] = ld16((const ST*)p.pred_proj + (int64_t)slot_s[k] * J + cc);
   }
@@ -248,7 +272,7 @@ __global__ void __launch_bounds__(512) joint_kernel(const DecK p) {
     bi[wave][lr] = bidx;
   }
   __syncthreads();
-  if (tid < 16 && b0 + tid < p.batch) {
+  if (tid < 16 && bid_s[tid] >= 0) {
     float v = bv[0][tid];
     int ix = bi[0][tid];
     for (int w = 1; w < 8; ++w)
@@ -256,7 +280,7 @@ __global__ void __launch_bounds__(512) joint_kernel(const DecK p) {
         v = bv[w][tid];
         ix = bi[w][tid];
       }
-    int32_t* ws = ws_of(p, b0 + tid);
+    int32_t* ws = ws_of(p, bid_s[tid]);
     ws[kWsHead + 2 * vt] = __float_as_int(v);
     ws[kWsHead + 2 * vt + 1] = ix;
   }
@@ -316,6 +340,23 @@ __device__ static inline void record(const DecK& p, int b, bool act, int tok) {
   p.frame_counts[(int64_t)b * p.max_frames + p.t] += 1;
 }
 
+// Compact mode: every stream's decision and record for iteration `it`, and
+// the list of the streams that emitted a token (their order in the list is
+// the order of the atomic appends; every later launch treats each stream on
+// its own, so the order does not change any result).
+__global__ void __launch_bounds__(256) select_kernel(const DecK p) {
+  const int b = blockIdx.x * 256 + threadIdx.x;
+  if (b >= p.batch) return;
+  bool act;
+  const int tk = decide(p, b, &act);
+  record(p, b, act, tk);
+  if (tk >= 0) {
+    const int cur = p.it & 1;
+    const int pos = atomicAdd(&p.acount[cur], 1);
+    p.alist[(int64_t)cur * p.batch + pos] = b;
+  }
+}
+
 // ---------------------------------------------------------------------------
 template <typename ST>
 struct LstmCfg {
@@ -331,7 +372,7 @@ __global__ void __launch_bounds__(LstmCfg<ST>::WAVES * 64) lstm_kernel(const Dec
   constexpr int RS = 2 * 640 + VEC;  // [x ; h] row of one stream (hidden 640 in LDS)
   __shared__ __align__(16) ST inp[SPW][RS];
   __shared__ float gsm[4][SPW][17];
-  __shared__ int32_t tok_s[SPW], slot_s[SPW];
+  __shared__ int32_t tok_s[SPW], slot_s[SPW], bid_s[SPW];
   constexpr int H = 640;  // the hidden size the host accepts
   const int L = p.layers, layer = p.layer;
   const int u0 = blockIdx.x * 16, b0 = blockIdx.y * SPW;
@@ -339,9 +380,12 @@ __global__ void __launch_bounds__(LstmCfg<ST>::WAVES * 64) lstm_kernel(const Dec
   // which streams update: layer 0 decides (prime: every stream, token blank),
   // the layers above read layer 0's record
   if (tid < SPW) {
-    const int b = b0 + tid;
+    int b = b0 + tid;
     int tk = -1;
-    if (b < p.batch) {
+    if (p.compact && !p.prime) {  // the select launch decided and recorded
+      b = listed_stream(p, p.it & 1, b0 + tid);
+      tk = b >= 0 ? ws_of(p, b)[1] : -1;
+    } else if (b < p.batch) {
       if (p.prime) {
         tk = stream_ok(p, b) ? p.blank : -1;
       } else if (layer == 0) {  // a stream with a bad slot is never active: no token, zero counts
@@ -354,6 +398,7 @@ __global__ void __launch_bounds__(LstmCfg<ST>::WAVES * 64) lstm_kernel(const Dec
     }
     tok_s[tid] = tk;
     slot_s[tid] = tk >= 0 ? p.slots[b] : 0;  // a stream that updates has a valid slot
+    bid_s[tid] = tk >= 0 ? b : 0;
   }
   __syncthreads();
   bool any = false;
@@ -380,7 +425,7 @@ __global__ void __launch_bounds__(LstmCfg<ST>::WAVES * 64) lstm_kernel(const Dec
   for (int it = 0; it < IT; ++it) {
     const int i = min(tid + it * NTH, SPW * 2 * nch - 1);
     const int k = i / (2 * nch), cc = (i - k * 2 * nch) * VEC;
-    const int b = min(b0 + k, p.batch - 1);
+    const int b = bid_s[k];
     const ST* src;
     if (cc < H)
       src = layer == 0 ? (const ST*)p.embed + (int64_t)max(tok_s[k], 0) * H + cc
@@ -406,8 +451,8 @@ __global__ void __launch_bounds__(LstmCfg<ST>::WAVES * 64) lstm_kernel(const Dec
   __syncthreads();
   // cell update: thread -> (stream, unit)
   for (int i = tid; i < SPW * 16; i += Cfg::WAVES * 64) {
-    const int k = i / 16, u = i % 16, b = b0 + k;
-    if (b >= p.batch || tok_s[k] < 0) continue;
+    const int k = i / 16, u = i % 16, b = bid_s[k];
+    if (tok_s[k] < 0) continue;
     const int64_t so = ((int64_t)slot_s[k] * L + layer) * H + u0 + u;
     const int64_t bo = (int64_t)layer * 4 * H + u0 + u;
     float g4[4];
@@ -428,16 +473,17 @@ template <typename ST>
 __global__ void __launch_bounds__(256) pred_kernel(const DecK p) {
   constexpr int VEC = 16 / sizeof(ST);
   __shared__ __align__(16) ST hs[16][kMaxDim + 8];
-  __shared__ int32_t tok_s[16], slot_s[16];
+  __shared__ int32_t tok_s[16], slot_s[16], bid_s[16];
   constexpr int H = 640;  // the hidden size the host accepts
   const int J = p.J, L = p.layers;
   const int j0 = blockIdx.x * 64, b0 = blockIdx.y * 16;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
   if (tid < 16) {
-    const int b = b0 + tid;
-    const int tk = stream_ok(p, b) ? (p.prime ? 0 : ws_of(p, b)[1]) : -1;
+    const int b = listed_stream(p, p.compact && !p.prime ? p.it & 1 : -1, b0 + tid);
+    const int tk = b >= 0 && stream_ok(p, b) ? (p.prime ? 0 : ws_of(p, b)[1]) : -1;
     tok_s[tid] = tk;
     slot_s[tid] = tk >= 0 ? p.slots[b] : 0;
+    bid_s[tid] = tk >= 0 ? b : 0;
   }
   __syncthreads();
   bool any = false;
@@ -458,7 +504,7 @@ __global__ void __launch_bounds__(256) pred_kernel(const DecK p) {
 #pragma unroll
   for (int it = 0; it < IT; ++it) {
     const int i = min(tid + it * 256, 16 * nch - 1);
-    const int k = i / nch, cc = (i - k * nch) * VEC, b = min(b0 + k, p.batch - 1);
+    const int k = i / nch, cc = (i - k * nch) * VEC, b = bid_s[k];
     hr[it] = ld16((const ST*)p.hn + ((int64_t)b * L + L - 1) * H + cc);
   }
 #pragma unroll
@@ -477,7 +523,7 @@ __global__ void __launch_bounds__(256) pred_kernel(const DecK p) {
 #pragma unroll
       for (int it = 0; it < IT; ++it) {
         const int i = min(i0 + tid + it * 256, 16 * L * nch - 1);
-        const int k = i / (L * nch), r = i - k * L * nch, b = min(b0 + k, p.batch - 1);
+        const int k = i / (L * nch), r = i - k * L * nch, b = bid_s[k];
         const int l = r / nch, cc = (r - l * nch) * VEC;
         v[it] = ld16((const ST*)p.hn + ((int64_t)b * L + l) * H + cc);
       }
@@ -509,9 +555,11 @@ __global__ void __launch_bounds__(256) pred_kernel(const DecK p) {
 }
 
 // ---------------------------------------------------------------------------
+// int32 words: the per-stream words, then the two stream lists and their two
+// counts (compact mode), rounded up to 256 bytes
 static int64_t ws_int_bytes(int batch, int vocab1) {
-  const int64_t b = (int64_t)batch * (kWsHead + 2 * ((vocab1 + kVT - 1) / kVT)) * 4;
-  return (b + 255) / 256 * 256;
+  const int64_t w = (int64_t)batch * (kWsHead + 2 * ((vocab1 + kVT - 1) / kVT)) + 2 * (int64_t)batch + 4;
+  return (w * 4 + 255) / 256 * 256;
 }
 
 template <typename ST>
@@ -547,6 +595,10 @@ static int run_step(const pk_rnnt_args* a, hipStream_t st) {
   k.frame_counts = a->frame_counts;
   k.ws = (int32_t*)a->workspace;
   k.hn = (char*)a->workspace + ws_int_bytes(a->batch, a->vocab1);
+  const int64_t words = (int64_t)a->batch * (kWsHead + 2 * k.vtiles);
+  k.alist = (int32_t*)a->workspace + words;
+  k.acount = k.alist + 2 * (int64_t)a->batch;
+  k.compact = !a->prime && (a->compact > 0 || (a->compact == 0 && a->batch >= kCompactMinBatch));
   k.h = a->h;
   k.prime = a->prime;
   const dim3 gj(k.vtiles, (a->batch + 15) / 16);
@@ -565,7 +617,9 @@ static int run_step(const pk_rnnt_args* a, hipStream_t st) {
       for (int s = 0; s < a->max_symbols; ++s) {
         k.t = t;
         k.s = s;
+        k.it = t * a->max_symbols + s;
         hipLaunchKernelGGL(joint_kernel<ST>, gj, dim3(512), 0, st, k);
+        if (k.compact) hipLaunchKernelGGL(select_kernel, dim3((a->batch + 255) / 256), dim3(256), 0, st, k);
         lstm();
         pred();
       }

@@ -15,7 +15,7 @@ from pathlib import Path
 LIB_NAME = "libparakeet_paged.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -285,6 +285,7 @@ class RnntArgs(ctypes.Structure):
         ("enc_stride_t", c_int64),
         ("lengths", c_void_p),
         ("max_frames", c_int32),
+        ("compact", c_int32),
         ("tokens", c_void_p),
         ("frame_counts", c_void_p),
         ("workspace", c_void_p),

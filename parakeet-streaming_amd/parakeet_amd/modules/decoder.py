@@ -71,6 +71,9 @@ class GreedyDecoder:
     def __init__(self, predictor: nn.Module, joiner: nn.Module, blank_id: int, num_slots: int, max_symbols: int = 5):
         self.pred, self.joiner = predictor, joiner
         self.blank, self.max_symbols = int(blank_id), int(max_symbols)
+        # 0: the library compacts each iteration's updating streams from 1024
+        # streams on; 1 / -1: always / never (the outputs are the same)
+        self.compact = 0
         self.num_slots = S = int(num_slots)
         lstm = predictor.prediction["dec_rnn"]
         embed = predictor.prediction["embed"]
@@ -126,6 +129,7 @@ class GreedyDecoder:
         a.batch, a.slots, a.num_slots = int(slots.numel()), slots.data_ptr(), self.num_slots
         a.layers, a.hidden, a.joint, a.vocab1 = self.layers, self.hidden, self.joint, self.vocab1
         a.blank, a.max_symbols, a.prime = self.blank, self.max_symbols, int(prime)
+        a.compact = int(self.compact)
         a.embed, a.w_ih, a.w_hh = self.embed.data_ptr(), self.w_ih.data_ptr(), self.w_hh.data_ptr()
         a.b_ih, a.b_hh = self.b_ih.data_ptr(), self.b_hh.data_ptr()
         a.w_pred, a.b_pred = self.w_pred.data_ptr(), self.b_pred.data_ptr()

@@ -41,18 +41,21 @@ def _tol(dt):
 
 
 @pytest.mark.parametrize(
-    "dt,layers,vocab,enc_dim,blank_bias,T",  # the bias gives a mix of tokens and blanks
+    "dt,layers,vocab,enc_dim,blank_bias,T,compact",  # the bias gives a mix of tokens and blanks
     [
-        (torch.float16, 1, 1026, 512, 1.5, 3),
-        (torch.bfloat16, 2, 1024, 1024, 3.5, 3),
-        (torch.float32, 1, 1026, 512, 1.5, 3),
-        (torch.bfloat16, 2, 1024, 1024, 3.5, 14),  # the large model's 14 frames a step (config.py:25-31)
+        (torch.float16, 1, 1026, 512, 1.5, 3, 0),
+        (torch.bfloat16, 2, 1024, 1024, 3.5, 3, 0),
+        (torch.float32, 1, 1026, 512, 1.5, 3, 0),
+        (torch.bfloat16, 2, 1024, 1024, 3.5, 14, 0),  # the large model's 14 frames a step (config.py:25-31)
+        (torch.float16, 1, 1026, 512, 1.5, 3, 1),  # compact mode: lists of the updating streams
+        (torch.float32, 2, 1026, 512, 3.0, 3, 1),
     ],
 )
-def test_greedy_decode_matches_oracle_replay(cuda, dt, layers, vocab, enc_dim, blank_bias, T):
+def test_greedy_decode_matches_oracle_replay(cuda, dt, layers, vocab, enc_dim, blank_bias, T, compact):
     pred, joint, P = _model(vocab, enc_dim, layers, dt, cuda, seed=layers + enc_dim, blank_bias=blank_bias)
     S, B = 20, 12
     dec = GreedyDecoder(pred, joint, blank_id=vocab, num_slots=S)
+    dec.compact = compact
     rng = np.random.default_rng(7)
     slots = rng.permutation(S)[:B]
     dec.reset_slot(slots)
@@ -183,4 +186,35 @@ def test_out_of_range_slot_is_skipped_by_the_kernels(cuda):
     for s in (1, 3):
         assert torch.equal(a.h[s], before[0][s]) and torch.equal(a.c[s], before[1][s])
         assert torch.equal(a.pred_proj[s], before[2][s])
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_compact_mode_gives_the_same_outputs(cuda, dt):
+    """Compact mode (per iteration, a device list of the streams that emitted a
+    token; the next symbol's joint and the LSTM / projection launches run over
+    it) against the tile-by-tile launches: tokens and state bit for bit, over
+    direct launches and graph replays (the lists and their counts are reset
+    inside the recording), 2- and 14-frame steps, ragged lengths."""
+    pred, joint, _ = _model(1026, 512, 2, dt, cuda, seed=12)
+    S, B = 80, 70
+    rng = np.random.default_rng(5)
+    slots = rng.permutation(S)[:B]
+    a = GreedyDecoder(pred, joint, blank_id=1026, num_slots=S)
+    b = GreedyDecoder(pred, joint, blank_id=1026, num_slots=S)
+    a.compact, b.compact = -1, 1
+    a.reset_slot(slots)
+    b.reset_slot(slots)
+    n_tok = 0
+    for step in range(8):
+        T = 14 if step % 4 == 3 else 2
+        enc = torch.randn(B, T, 512, generator=torch.Generator().manual_seed(100 + step)).to(dt).to(cuda)
+        lens = rng.integers(0, T + 1, B)
+        graph = step % 2 == 1
+        ta = a.decode(slots, enc, lens, frame_tokens=True, graph=graph)
+        tb = b.decode(slots, enc, lens, frame_tokens=True, graph=graph)
+        assert ta == tb, f"step {step}"
+        assert torch.equal(a.h, b.h) and torch.equal(a.c, b.c) and torch.equal(a.pred_proj, b.pred_proj)
+        n_tok += sum(len(t) for fr in ta for t in fr)
+    assert n_tok > 50, n_tok  # tokens were emitted, so the lists were exercised
     torch.cuda.synchronize()
