@@ -22,6 +22,10 @@
 //   pred_kernel      pred_proj[slot] = W_pred h'_top + b_pred for the updated
 //                    streams, and h' copied from the scratch into the slot state
 //                    (this launch runs after every read of the old h).
+// In compact mode (large batches) a select_kernel launch after the joint takes
+// every stream's decision, records it and lists the streams that emitted a
+// token; the LSTM and pred launches, and the next symbol's joint, then tile over
+// that list instead of the whole batch.
 
 #include <hip/hip_runtime.h>
 
