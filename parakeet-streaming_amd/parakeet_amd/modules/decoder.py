@@ -160,7 +160,7 @@ class GreedyDecoder:
         """A HIP graph of one decode step for B streams and T frames: the enc GEMM
         and every launch of pk_rnnt_greedy_step, over persistent input and output
         buffers (recorded once, replayed per step)."""
-        key = (B, T, D)
+        key = (B, T, D, int(self.compact))  # a recording keeps the mode it was made with
         g = self._graphs.get(key)
         if g is not None:
             return g
