@@ -170,13 +170,20 @@ class GreedyDecoder:
         out = torch.zeros((B, W), dtype=torch.int32, device=dev)
         g = {
             "meta": meta,
-            "meta_h": torch.zeros(2 * B, dtype=torch.int32, pin_memory=True),
+            # two pinned upload and two pinned result buffers, used in turn: a call
+            # may return before its copies ran, so the next call fills the other
+            # pair (each buffer is reused only after its event)
+            "meta_h": [torch.zeros(2 * B, dtype=torch.int32, pin_memory=True) for _ in range(2)],
+            "meta_ev": [None, None],
+            "out_ev": [None, None],
+            "pending": [None, None],
+            "turn": 0,
             "slots": meta[:B],
             "lens": meta[B:],
             "enc": torch.zeros((B, T, D), dtype=self.dtype, device=dev),
             "e": torch.empty((B, T, self.joint), dtype=self.dtype, device=dev),
             "out": out,
-            "out_h": torch.zeros((B, W), dtype=torch.int32, pin_memory=True),
+            "out_h": [torch.zeros((B, W), dtype=torch.int32, pin_memory=True) for _ in range(2)],
             "tokens": out[:, : T * self.max_symbols],
             "counts": out[:, T * self.max_symbols :],
         }
@@ -210,15 +217,21 @@ class GreedyDecoder:
         self._graphs[key] = g
         return g
 
-    def decode(self, slots, enc_out: Tensor, lengths=None, frame_tokens: bool = False, graph: bool = False):
+    def decode(
+        self, slots, enc_out: Tensor, lengths=None, frame_tokens: bool = False, graph: bool = False, wait: bool = True
+    ):
         """Greedy decoding of one step's encoder frames.
 
         enc_out: [B, T, D] encoder output (frames of stream b in enc_out[b, :lengths[b]]);
         lengths: frames per stream (None: all T).  Returns the emitted tokens of
         each stream (``frame_tokens=True``: a list per frame).  ``graph=True``
         replays a recorded step over persistent buffers: one upload of slots and
-        lengths, one copy of the tokens back (the pinned upload buffer is reused
-        by the next call, after this call's blocking copy)."""
+        lengths, one copy of the tokens back.  With ``graph=True, wait=False`` the
+        call returns a :class:`PendingTokens` as soon as the step and the copy are
+        issued; its ``result()`` waits for the copy and builds the lists, so a
+        caller can split one step's tokens while the GPU runs the next step.  A
+        pending result is built at the latest when its buffer comes round again,
+        two calls of the same shape later."""
         sl = self._check_slots(slots)
         B = len(sl)
         if enc_out.dim() != 3 or enc_out.shape[0] != B:
@@ -234,15 +247,26 @@ class GreedyDecoder:
             return [[] for _ in range(B)]
         if graph:
             g = self._graph_for(B, T, int(enc_out.shape[2]))
-            mh = g["meta_h"].numpy()
+            i = g["turn"]
+            g["turn"] = i ^ 1
+            if g["meta_ev"][i] is not None:
+                g["meta_ev"][i].synchronize()  # the upload that last read this buffer ran
+            mh = g["meta_h"][i].numpy()
             mh[:B] = sl
             mh[B:] = lens
-            g["meta"].copy_(g["meta_h"], non_blocking=True)
+            g["meta"].copy_(g["meta_h"][i], non_blocking=True)
+            g["meta_ev"][i] = torch.cuda.Event()
+            g["meta_ev"][i].record()
             g["enc"].copy_(enc_out)
             g["graph"].replay()
-            g["out_h"].copy_(g["out"])  # the step's one synchronisation
-            o = g["out_h"].numpy()
-            return self._split(o[:, : T * self.max_symbols], o[:, T * self.max_symbols :], lens, frame_tokens)
+            if g["pending"][i] is not None:
+                g["pending"][i].result()  # its buffer is about to be overwritten
+            g["out_h"][i].copy_(g["out"], non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record()
+            res = PendingTokens(g["out_h"][i], ev, T * self.max_symbols, lens, frame_tokens)
+            g["pending"][i] = res
+            return res.result() if wait else res
         st = torch.from_numpy(sl).to(self.device)
         with torch.no_grad():
             e = F.linear(enc_out.to(self.dtype), self.w_enc, self.b_enc).contiguous()  # Joiner.enc (decoder.py:83)
@@ -282,4 +306,23 @@ class GreedyDecoder:
         return [[flat[e[i] : e[i + 1]] for i in range(int(l))] for e, l in zip(edges, lens)]
 
 
-__all__ = ["Predictor", "Joiner", "GreedyDecoder"]
+class PendingTokens:
+    """The tokens of a decode step whose copy back may still be running:
+    ``result()`` waits for it and returns the per-stream token lists (per frame
+    with ``frame_tokens``), as ``GreedyDecoder.decode`` does with ``wait=True``."""
+
+    def __init__(self, buf: Tensor, event, n_tok: int, lens: np.ndarray, frame_tokens: bool):
+        self._buf, self._event, self._n_tok = buf, event, int(n_tok)
+        self._lens, self._frame_tokens = np.array(lens, copy=True), frame_tokens
+        self._out = None
+
+    def result(self):
+        if self._out is None:
+            self._event.synchronize()
+            o = self._buf.numpy()
+            self._out = GreedyDecoder._split(o[:, : self._n_tok], o[:, self._n_tok :], self._lens, self._frame_tokens)
+            self._buf = None
+        return self._out
+
+
+__all__ = ["Predictor", "Joiner", "GreedyDecoder", "PendingTokens"]

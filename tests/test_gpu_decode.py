@@ -218,3 +218,33 @@ def test_compact_mode_gives_the_same_outputs(cuda, dt):
         n_tok += sum(len(t) for fr in ta for t in fr)
     assert n_tok > 50, n_tok  # tokens were emitted, so the lists were exercised
     torch.cuda.synchronize()
+
+
+def test_pending_results_match_blocking_calls(cuda):
+    """decode(graph=True, wait=False) returns before the tokens are copied back;
+    its results, consumed right away, one call later, after their buffer comes
+    round again (built then) or at the end, equal the blocking calls' results,
+    and the state after each step is the same."""
+    dt = torch.float16
+    pred, joint, _ = _model(1026, 512, 1, dt, cuda, seed=13)
+    a = GreedyDecoder(pred, joint, blank_id=1026, num_slots=12)
+    b = GreedyDecoder(pred, joint, blank_id=1026, num_slots=12)
+    slots = np.array([3, 8, 0, 11, 5, 6, 1])
+    a.reset_slot(slots)
+    b.reset_slot(slots)
+    rng = np.random.default_rng(4)
+    want, pending = [], []
+    for step in range(7):
+        enc = torch.randn(7, 2, 512, generator=torch.Generator().manual_seed(50 + step)).to(dt).to(cuda)
+        lens = rng.integers(0, 3, 7).astype(np.int32)  # int32: the decoder may take it as it is
+        want.append(a.decode(slots, enc, lens, frame_tokens=True, graph=True))
+        pending.append(b.decode(slots, enc, lens, frame_tokens=True, graph=True, wait=False))
+        lens[:] = 0  # the caller's array may change; the pending result kept its own
+        if step == 2:
+            assert pending[2].result() == want[2]  # right away
+        if step == 4:
+            assert pending[3].result() == want[3]  # one call later
+        torch.cuda.synchronize()
+        assert torch.equal(a.h, b.h) and torch.equal(a.c, b.c) and torch.equal(a.pred_proj, b.pred_proj)
+    assert [p.result() for p in pending] == want  # the rest at the end (0, 1 built when their buffer came round)
+    assert sum(len(t) for w in want for s_ in w for t in s_) > 5
