@@ -92,3 +92,47 @@ def test_empty_batch_is_noop(cuda):
     k, v = ops.kv_gather(sc.pages, 0, 0, sc.L, sc.T)
     assert k.shape == (0, sc.L, sc.D)
     torch.cuda.synchronize()
+
+
+def _poison_free_pages(sc):
+    """NaN into every page of the free queue: a read of a page after it was
+    freed (a stale window row) shows up as NaN."""
+    free = torch.from_numpy(sc.pool.free_list().astype(np.int64)).to(sc.k_pages.device)
+    if free.numel():
+        sc.k_pages[:, free] = float("nan")
+        sc.v_pages[:, free] = float("nan")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_freed_pages_are_never_read(cuda, dtype):
+    """Use-after-free check: after every step's eviction and allocation, every
+    free page is filled with NaN.  The windows the pages give stay equal to the
+    dense shift buffer (cache.py:36-45) and the fused append + attention reads no
+    NaN, over churn with slot resets on a shuffled pool (pages are reused by
+    other streams soon after they are freed)."""
+    print(f"\n[poisoned free pages] dtype={dtype}", flush=True)
+    sc = PagedScenario(cuda, dtype, B=6, layers=2, d_model=128, left=70, right=1, page_size=16, seed=3, shuffle=True)
+    H, dk = 2, 64
+    g = torch.Generator().manual_seed(1)
+    pos = torch.randn(sc.L + sc.T - 1, sc.D, generator=g).to(dtype).to(cuda)
+    bu = (torch.randn(H, dk, generator=g) * 0.02).to(dtype).to(cuda)
+    bv = (torch.randn(H, dk, generator=g) * 0.02).to(dtype).to(cuda)
+    rng = np.random.default_rng(5)
+    for step in range(80):
+        if step in (15, 40, 41, 60):
+            for s in rng.choice(sc.B, size=2, replace=False):
+                sc.reset(int(s))
+        sc.open_step()
+        _poison_free_pages(sc)
+        for layer in range(sc.Ly):
+            _, (q, k, v) = sc.frames()
+            if layer == 0:
+                ops.kv_append(sc.pages, layer, k, v)
+            else:  # the fused append inside the attention launch
+                out = ops.paged_relpos_attn(q, k, v, pos, bu, bv, None, num_heads=H, left=sc.left, pages=sc.pages,
+                                            layer=layer, append=True)
+                assert torch.isfinite(out.float()).all(), f"step {step}: attention read a freed page"
+            dk_, dv_ = sc.dense_update(layer, k, v)
+            _check_window(sc, layer, dk_, dv_)
+    torch.cuda.synchronize()
