@@ -302,7 +302,8 @@ def test_encoder_step_graph_matches_eager_steps(cuda, dtype):
 
 
 @pytest.mark.gpu
-def test_engine_loop_with_scheduler_matches_per_stream_reference(cuda):
+@pytest.mark.parametrize("sync_each_step", [True, False])
+def test_engine_loop_with_scheduler_matches_per_stream_reference(cuda, sync_each_step):
     """The reference's _encode_step call pattern (parakeet/engine/model_runner.py:
     254-304) on the drop-ins: Scheduler.init_state_pool, acquire_state_slot,
     pack_states -> encoder(batch, state, length) -> unpack_states,
@@ -311,7 +312,10 @@ def test_engine_loop_with_scheduler_matches_per_stream_reference(cuda):
     streams.  Every stream's output of every step equals the float64 reference
     encoder (oracle attention over a dense shift cache, oracle conv step, oracle
     masks) run on that stream alone from its own start: streams are independent,
-    so that is what the reference's batched pack / unpack computes."""
+    so that is what the reference's batched pack / unpack computes.  Without a
+    synchronisation per step, every release and re-acquire happens while earlier
+    steps may still run on the GPU (the reference's "release while a chunk is in
+    flight"); stream order keeps the reused pages and slots correct."""
     print("\n[engine loop] scheduler + paged encoder vs per-stream dense reference", flush=True)
     from parakeet_amd.engine.scheduler import Scheduler
 
@@ -354,6 +358,7 @@ def test_engine_loop_with_scheduler_matches_per_stream_reference(cuda):
     rng = np.random.default_rng(12)
     g = torch.Generator().manual_seed(13)
     live: list[Seq] = []
+    deferred = []  # (GPU output, input, streams, their (proc, cache_len)) checked at the end
     slot_users: dict[int, int] = {}
     compared = worst = 0.0
     with torch.no_grad():
@@ -372,25 +377,41 @@ def test_engine_loop_with_scheduler_matches_per_stream_reference(cuda):
                 state, index = sch.pack_states(ready)
                 out, state = enc(x.to(cuda), state, length=torch.full((B,), T, dtype=torch.int64, device=cuda))
                 sch.unpack_states(state, index)
-                out = out.double().cpu()
-                for b, s in enumerate(ready):
-                    rstate = StreamingState(
-                        s.dense, torch.tensor([s.proc], dtype=torch.int64), torch.tensor([s.cl], dtype=torch.int64)
-                    )
-                    rout, _ = ref(x[b : b + 1].double(), rstate, length=torch.full((1,), T, dtype=torch.int64))
-                    err = float((out[b] - rout[0]).abs().max())
-                    worst = max(worst, err)
-                    assert err <= 2e-4, f"step {step} slot {s.encoder_state}: max abs err {err:.3e}"
-                    s.proc += T
-                    s.cl = min(s.cl + T, left)
-                    s.done += 1
-                    compared += 1
-                pf = sch.pool_state.processed_frames.cpu().tolist()
-                for s in live:
-                    assert pf[s.encoder_state] == s.proc
+                if not sync_each_step:
+                    deferred.append((out.clone(), x, list(ready), [(s.proc, s.cl) for s in ready]))
+                    for s in ready:
+                        s.proc += T
+                        s.cl = min(s.cl + T, left)
+                        s.done += 1
+                else:
+                    out = out.double().cpu()
+                    for b, s in enumerate(ready):
+                        rstate = StreamingState(
+                            s.dense, torch.tensor([s.proc], dtype=torch.int64), torch.tensor([s.cl], dtype=torch.int64)
+                        )
+                        rout, _ = ref(x[b : b + 1].double(), rstate, length=torch.full((1,), T, dtype=torch.int64))
+                        err = float((out[b] - rout[0]).abs().max())
+                        worst = max(worst, err)
+                        assert err <= 2e-4, f"step {step} slot {s.encoder_state}: max abs err {err:.3e}"
+                        s.proc += T
+                        s.cl = min(s.cl + T, left)
+                        s.done += 1
+                        compared += 1
+                    pf = sch.pool_state.processed_frames.cpu().tolist()
+                    for s in live:
+                        assert pf[s.encoder_state] == s.proc
             for s in [s for s in live if s.done >= s.steps]:  # departures
                 sch.release_state_slot(s.encoder_state)
                 live.remove(s)
+        for out, x, streams, pre in deferred:  # the reference, in step order, per stream
+            out = out.double().cpu()
+            for b, (s, (proc, cl)) in enumerate(zip(streams, pre)):
+                rstate = StreamingState(s.dense, torch.tensor([proc], dtype=torch.int64), torch.tensor([cl], dtype=torch.int64))
+                rout, _ = ref(x[b : b + 1].double(), rstate, length=torch.full((1,), T, dtype=torch.int64))
+                err = float((out[b] - rout[0]).abs().max())
+                worst = max(worst, err)
+                assert err <= 2e-4, f"deferred check, slot {s.encoder_state}: max abs err {err:.3e}"
+                compared += 1
     assert compared >= 60, compared
     assert max(slot_users.values()) >= 2, "no slot was reused by a new stream"
     print(f"  {int(compared)} stream-steps, worst max-abs error {worst:.3e}", flush=True)
