@@ -16,8 +16,11 @@ The convolution module's GLU / depthwise conv / LayerNorm / SiLU runs as one HIP
 launch with each stream's conv state updated in place (convolution.py:107-162,
 cache.py:47-53); the feed-forward blocks, layer norms and pointwise projections
 are torch modules with the reference's parameter names (encoder.py:11-81,
-feedforward.py:4-26); the convolution subsampling front end (``pre_encode``) is
-not part of this package.
+feedforward.py:4-26).  ``pre_encode`` is the batched convolution subsampling of
+``modules/frontend.py`` (one HIP launch for the 8x stack), built from the same
+constructor arguments as the reference's (encoder.py:105-112), so a reference
+checkpoint loads strictly and ``ModelRunner`` finds ``encoder.pre_encode``
+(model_runner.py:44,221).
 """
 
 from __future__ import annotations
@@ -29,6 +32,7 @@ from torch.nn import functional as F
 from .. import ops
 from .attention import ConformerAttention, PositionalEncoding
 from .cache import ConvCacheRef, ModelCache, StreamingState
+from .frontend import ConvSubsampling
 
 
 class ConformerFeedForward(nn.Module):
@@ -164,7 +168,14 @@ class ConformerEncoder(nn.Module):
         self.embed_dim = hidden_size
         self.feat_in = feat_in
         self.subsampling_factor = subsampling_factor
-        self.pre_encode = None
+        self.pre_encode = ConvSubsampling(
+            hidden_size=hidden_size,
+            subsampling_conv_channels=subsampling_conv_channels,
+            feat_in=feat_in,
+            subsampling_factor=subsampling_factor,
+            stride=2,
+            kernel_size=3,
+        )
         self.pos_enc = PositionalEncoding(hidden_size=hidden_size, dropout_rate_emb=0.0, max_len=pos_emb_max_len, dropout=0.0)
         self.layers = nn.ModuleList(
             ConformerLayer(i, hidden_size, hidden_size * ff_expansion_factor, num_heads, 0.0, conv_kernel_size, use_bias)
