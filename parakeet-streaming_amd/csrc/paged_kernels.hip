@@ -562,7 +562,12 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
   const int b_raw = sb * SPW + sw;
   const int b = min(b_raw, p.B - 1);  // loads stay inside the batch arrays
   const int hcol = h * DK + hf * 64;       // first column of the wave
-  const int cbyte = (hcol + kg * 16) * ES;  // byte offset of the lane's 16 columns in a row
+  // k-step ks of the wave's 64 columns covers columns ks*32 .. ks*32 + 31; the
+  // lane holds 8 of them, ks*32 + kg*8 ..  So one 16-byte load per lane and
+  // k-step reads one whole 64-byte half of each of 16 rows' 128-byte lines,
+  // and every half line is requested once.
+  const int cbyte = (hcol + kg * 8) * ES;  // byte offset of the lane's k-step 0 columns in a row
+  constexpr int KSB = 32 * ES;             // bytes between a lane's k-steps
   const int M = p.pg.max_pages;
   const bool paged = p.pg.rows != nullptr;
 
@@ -602,18 +607,18 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
   const int32_t nact_v = p.nact ? *p.nact : p.B;
   // A operand source: row m = q16 is (q+u)_hi, (q+u)_lo, (q+v)_hi, (q+v)_lo of
   // query m & 1 for m < 8, zero above; element e of k-step ks is column
-  // kg*16 + ks*8 + e of the wave's 64
+  // ks*32 + kg*8 + e of the wave's 64
   const int a_ii = q16 & 1;
   const int a_kind = q16 >> 1;  // 0 u-hi, 1 u-lo, 2 v-hi, 3 v-lo, >= 4 zero
   u32x4 qraw[KS], braw[KS];
   {
     const int ic = min(i0 + a_ii, p.T - 1);
-    const ST* qrow = p.q + b * p.q_sb + (int64_t)ic * p.q_st + hcol + kg * 16;
-    const ST* brow = (a_kind < 2 ? p.bu : p.bv) + hcol + kg * 16;
+    const ST* qrow = p.q + b * p.q_sb + (int64_t)ic * p.q_st + hcol + kg * 8;
+    const ST* brow = (a_kind < 2 ? p.bu : p.bv) + hcol + kg * 8;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      qraw[ks] = ld16(qrow + ks * 8);
-      braw[ks] = ld16(brow + ks * 8);
+      qraw[ks] = ld16(qrow + ks * 32);
+      braw[ks] = ld16(brow + ks * 32);
     }
   }
   // this step's frames (last pass; they do not depend on the pages)
@@ -622,8 +627,8 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
     const uint32_t fr = q16 < p.T ? (uint32_t)q16 : kNoRow;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      kf[ks] = pk_buffer_load_x4(r_kn, fr, cbyte + ks * 16, 0, 0);
-      vf[ks] = pk_buffer_load_x4(r_vn, fr, cbyte + ks * 16, 0, 0);
+      kf[ks] = pk_buffer_load_x4(r_kn, fr, cbyte + ks * KSB, 0, 0);
+      vf[ks] = pk_buffer_load_x4(r_vn, fr, cbyte + ks * KSB, 0, 0);
     }
   }
   // position rows (rows outside the table read zeros) and mask bytes of a pass
@@ -732,8 +737,8 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
         *reinterpret_cast<u32x4*>(pos_lds + (idx / CHR) * PSTRIDE + (idx % CHR) * 16) = pst[c];
     }
 
-    // ---- history K and V rows, lane = slot 16*kt + q16, columns kg*16 ..
-    //      kg*16 + 15 of the wave's 64: page rows first, then all loads
+    // ---- history K and V rows, lane = slot 16*kt + q16, columns ks*32 + kg*8
+    //      .. ks*32 + kg*8 + 7 of the wave's 64: page rows first, then all loads
     uint32_t prow[NT];
 #pragma unroll
     for (int kt = 0; kt < NT; ++kt) {
@@ -745,7 +750,7 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
 #pragma unroll
     for (int kt = 0; kt < NT; ++kt)
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) kr[kt][ks] = pk_buffer_load_x4(r_kp, prow[kt], cbyte + ks * 16, 0, 0);
+      for (int ks = 0; ks < KS; ++ks) kr[kt][ks] = pk_buffer_load_x4(r_kp, prow[kt], cbyte + ks * KSB, 0, 0);
     // the frames' page rows (append target): looked up with every lane
     // active, then restricted to the lanes holding one of the chunk's frames
     const uint32_t frow_all = page_row(p.left + q16);
@@ -756,10 +761,10 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
 #pragma unroll
     for (int pt = 0; pt < NPT; ++pt) {
       f32x4_t d = {0.f, 0.f, 0.f, 0.f};
-      const uint8_t* src = pos_lds + (pt * 16 + q16) * PSTRIDE + (hf * 64 + kg * 16) * 2;
+      const uint8_t* src = pos_lds + (pt * 16 + q16) * PSTRIDE + (hf * 64 + kg * 8) * 2;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
-        d = Mma<ST>::k32(aop[ks], *reinterpret_cast<const u32x4*>(src + ks * 16), d);
+        d = Mma<ST>::k32(aop[ks], *reinterpret_cast<const u32x4*>(src + ks * KSB), d);
       if (kg == 1) {
         bd_lds[wave][0][pt * 16 + q16] = d[0] + d[2];
         bd_lds[wave][1][pt * 16 + q16] = d[1] + d[3];
@@ -781,8 +786,8 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
     if (do_append && last) {
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        pk_buffer_store_x4(kf[ks], r_kp, frow, cbyte + ks * 16, 0, 0);
-        pk_buffer_store_x4(vf[ks], r_vp, frow, cbyte + ks * 16, 0, 0);
+        pk_buffer_store_x4(kf[ks], r_kp, frow, cbyte + ks * KSB, 0, 0);
+        pk_buffer_store_x4(vf[ks], r_vp, frow, cbyte + ks * KSB, 0, 0);
       }
     }
     // ---- history V rows, issued once the K rows are consumed (half the
@@ -791,7 +796,7 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
 #pragma unroll
     for (int kt = 0; kt < NT; ++kt)
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) vr[kt][ks] = pk_buffer_load_x4(r_vp, prow[kt], cbyte + ks * 16, 0, 0);
+      for (int ks = 0; ks < KS; ++ks) vr[kt][ks] = pk_buffer_load_x4(r_vp, prow[kt], cbyte + ks * KSB, 0, 0);
     __syncthreads();  // partial dot products of the stream's waves in LDS
 
     // ---- scores: lane handles slots lane + 64*r; online softmax
@@ -860,9 +865,9 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
     const uint16_t* p_arow = &p_lds[wave][(q16 >> 1) & 1][q16 & 1][0];
 #pragma unroll
     for (int kt = 0; kt <= NT; ++kt) {
-      uint8_t* vrow = vl + q16 * VSTRIDE + kg * 32;
+      uint8_t* vrow = vl + q16 * VSTRIDE + kg * 16;
       *reinterpret_cast<u32x4*>(vrow) = kt < NT ? vr[kt][0] : vf[0];
-      *reinterpret_cast<u32x4*>(vrow + 16) = kt < NT ? vr[kt][1] : vf[1];
+      *reinterpret_cast<u32x4*>(vrow + KSB) = kt < NT ? vr[kt][1] : vf[1];
       const i16x4_t pop = *reinterpret_cast<const i16x4_t*>(p_arow + 16 * kt + 4 * kg);
       wave_lds_sync();
 #pragma unroll

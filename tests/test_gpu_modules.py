@@ -18,27 +18,22 @@ paged cache -- against the oracle:
 """
 
 import copy
-import math
 
 import numpy as np
 import pytest
 import torch
 
-import torch.nn.functional as F
-
 from oracle import attention as oa
-from oracle import conv as oc
 from oracle import masks as om
 from parakeet_amd.modules.attention import ConformerAttention, PositionalEncoding
 from parakeet_amd.modules.cache import ModelCache, StreamingState
 from parakeet_amd.modules.encoder import ConformerEncoder
 
-
-def _dense_shift(win, slot, layer, left, new):
-    """cache.py:37-44 for one stream: keep the last `left` frames, append."""
-    if left > 0:
-        win[slot, layer, :left] = win[slot, layer, -left:].copy()
-    win[slot, layer, left:] = new
+from _dense_encoder import DenseCache as _DenseCache
+from _dense_encoder import dense_shift as _dense_shift
+from _dense_encoder import init_attention as _init_attention
+from _dense_encoder import oracle_attention as _oracle_attention
+from _dense_encoder import oracle_conv as _oracle_conv
 
 
 @pytest.mark.gpu
@@ -79,15 +74,6 @@ def test_model_cache_windows_match_dense(cuda, dtype):
             assert torch.equal(gk.cpu(), torch.from_numpy(win_k[slots, layer]).to(dtype)), f"step {step} layer {layer}"
             assert torch.equal(gv.cpu(), torch.from_numpy(win_v[slots, layer]).to(dtype)), f"step {step} layer {layer}"
     torch.cuda.synchronize()
-
-
-def _init_attention(att, D, seed):
-    g = torch.Generator().manual_seed(seed)
-    with torch.no_grad():
-        for lin in (att.qkv, att.linear_pos, att.linear_out):
-            lin.weight.copy_(torch.randn(lin.weight.shape, generator=g) / math.sqrt(D))
-        att.pos_bias_u.copy_(torch.randn(att.pos_bias_u.shape, generator=g) * 0.02)
-        att.pos_bias_v.copy_(torch.randn(att.pos_bias_v.shape, generator=g) * 0.02)
 
 
 # fp32: the kernel's 1e-4; fp16: the kernel's 2e-3 plus linear_out's fp16
@@ -147,63 +133,6 @@ def test_conformer_attention_matches_oracle(cuda, dtype):
     ref = oa.relpos_attention(q, k, v, pos, bu, bv, None, H) @ w_out.T
     assert float(np.abs(out.double().cpu().numpy() - ref).max()) <= ATT_TOL[dtype]
     torch.cuda.synchronize()
-
-
-class _DenseCache:
-    """Dense per-stream cache for the CPU reference encoder: K/V shift buffers
-    (cache.py:19-45) and the conv cache (cache.py:30-34,47-53)."""
-
-    def __init__(self, B, Ly, left, right, D, K):
-        self.left = left
-        self.k = np.zeros((B, Ly, left + right + 1, D))
-        self.v = np.zeros_like(self.k)
-        self.conv = torch.zeros(B, Ly, D, K - 1, dtype=torch.float64)
-
-    def get_conv_cache(self, layer):
-        return self.conv[:, layer]
-
-    def update_conv_cache(self, layer, state):
-        self.conv[:, layer] = state
-
-    conv_ref = get_conv_cache  # the CPU reference's conv step takes the state tensor
-
-
-def _oracle_conv(conv):
-    """Replaces ConformerConvolution.forward on the CPU reference: the module's
-    pointwise projections around the oracle's streaming step over the dense
-    [B, D, K-1] conv cache."""
-
-    def forward(x, pad_mask, cache=None):
-        bn, dw = conv.batch_norm, conv.depthwise_conv
-        h = F.linear(x, conv.pointwise_conv1.weight.squeeze(-1)).numpy()
-        y, nxt = oc.conv_module_step(
-            h, cache.transpose(1, 2).numpy(), pad_mask.numpy(), dw.weight.detach().numpy().reshape(conv.d_model, -1),
-            None, bn.weight.detach().numpy(), bn.bias.detach().numpy(), bn.eps,
-        )
-        out = F.linear(torch.from_numpy(y), conv.pointwise_conv2.weight.squeeze(-1))
-        return out, torch.from_numpy(nxt).transpose(1, 2)
-
-    return forward
-
-
-def _oracle_attention(att, left, H):
-    """Replaces ConformerAttention.forward on the CPU reference: the module's
-    projections, the dense cache update and the oracle's rel-pos attention."""
-
-    def forward(x, pos_emb, attn_mask=None, cache=None):
-        q, k, v = (t.numpy() for t in att.qkv(x).chunk(3, dim=-1))
-        pos = att.linear_pos(pos_emb)[0].numpy()
-        layer = att.layer_idx
-        for b in range(x.shape[0]):
-            _dense_shift(cache.k, b, layer, left, k[b])
-            _dense_shift(cache.v, b, layer, left, v[b])
-        core = oa.relpos_attention(
-            q, cache.k[:, layer], cache.v[:, layer], pos,
-            att.pos_bias_u.detach().numpy(), att.pos_bias_v.detach().numpy(), attn_mask.numpy(), H,
-        )
-        return att.linear_out(torch.from_numpy(core))
-
-    return forward
 
 
 @pytest.mark.gpu
