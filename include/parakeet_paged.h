@@ -11,7 +11,14 @@
  * no device pointer past a call.
  *
  * Paged layout shared by the kernels (pk_paged_layout):
- *   k_pool, v_pool : [num_layers][num_pages][page_size][d_model] of `dtype`
+ *   k_pool, v_pool : num_layers x num_pages pages of page_size frames x d_model
+ *                    elements of `dtype`, contiguous; inside a page the frames
+ *                    are stored as column blocks [d_model / CB][page_size][CB],
+ *                    CB = gcd(d_model, 64 / element size) (64-byte blocks for
+ *                    any d_model of a multiple of 64 bytes), so element (layer,
+ *                    page, row r, column c) is at
+ *                    ((layer * num_pages + page) * page_size * d_model)
+ *                      + (c / CB) * page_size * CB + r * CB + c % CB.
  *   rows           : int32 [batch][rows_stride], one row per stream of the batch:
  *                    rows[b][0]     = frames appended to stream b before this step (A)
  *                    rows[b][1 + r] = page id held in ring entry r, -1 if none,
@@ -31,7 +38,7 @@
 extern "C" {
 #endif
 
-#define PK_ABI_VERSION 7
+#define PK_ABI_VERSION 8
 
 enum pk_dtype { PK_DTYPE_F32 = 0, PK_DTYPE_F16 = 1, PK_DTYPE_BF16 = 2 };
 

@@ -26,6 +26,12 @@ namespace pk {
 // ---------------------------------------------------------------------------
 // paged layout, device view
 
+// A page holds its page_size frames as column blocks: element (page, row r,
+// column c) of a layer's slab is at
+//   page * page_size * D + (c / CB) * page_size * CB + r * CB + c % CB,
+// CB = gcd(D, 64 / element size): 64-byte blocks at the model shapes (32
+// fp16/bf16 elements, 16 fp32), so one block of 16 consecutive frames is 1 KB
+// of contiguous memory; rows narrower than 64 bytes are one block.
 struct PagesK {
   const int32_t* rows;
   int32_t rows_stride;
@@ -34,16 +40,24 @@ struct PagesK {
   int32_t num_pages;
   int64_t page_elems;  // page_size * d_model
   int32_t D;
+  int32_t cb_shift;    // log2(CB)
 };
 
 // Element offset of frame `pos` (0 <= pos < 2^31, the int32 range of the
-// rows' frame counter) of stream `ring` in a layer's pool slab, or -1 when the
-// ring holds no valid page for it.  32-bit index arithmetic.
+// rows' frame counter) of stream `ring` in a layer's pool slab, without the
+// column part (page_col), or -1 when the ring holds no valid page for it.
+// 32-bit index arithmetic.
 __device__ static inline int64_t page_offset(const PagesK& pg, const int32_t* ring, int64_t pos) {
   const uint32_t p32 = (uint32_t)pos;
   const int32_t page = ring[(p32 >> pg.page_shift) % (uint32_t)pg.max_pages];
   if (page < 0 || page >= pg.num_pages) return -1;
-  return (int64_t)page * pg.page_elems + (int64_t)(p32 & ((1u << pg.page_shift) - 1u)) * pg.D;
+  return (int64_t)page * pg.page_elems + ((int64_t)(p32 & ((1u << pg.page_shift) - 1u)) << pg.cb_shift);
+}
+
+// Column part of a page element offset: column c (a 16-byte chunk never
+// crosses a block).
+__device__ static inline int64_t page_col(const PagesK& pg, int c) {
+  return ((int64_t)(c >> pg.cb_shift) << (pg.page_shift + pg.cb_shift)) + (c & ((1 << pg.cb_shift) - 1));
 }
 
 // ---------------------------------------------------------------------------
@@ -153,6 +167,7 @@ __global__ void __launch_bounds__(64) relpos_attn_kernel(const AttnK<ST> p) {
   const int i0 = blockIdx.y * TQ;
   const int nq = min(TQ, p.T - i0);
   const int col = h * DK + g * VEC;
+  const int64_t pcol = page_col(p.pg, col);  // the lane's columns in a page row
 
   // page header of the stream: frames appended before this step and the ring,
   // one ring entry per lane
@@ -274,12 +289,12 @@ __global__ void __launch_bounds__(64) relpos_attn_kernel(const AttnK<ST> p) {
       ok[n] = j < p.Lk && (fresh || paged_ok);
       const int t = fresh ? jc - p.left : 0;
       const int64_t poff = (int64_t)(paged_ok ? page : 0) * p.pg.page_elems +
-                           (int64_t)((uint32_t)max(pos, 0) & pmask) * p.pg.D;
+                           ((int64_t)((uint32_t)max(pos, 0) & pmask) << p.pg.cb_shift);
       const bool from_new = fresh || !paged_ok;
-      const ST* ka = from_new ? kn_b + (int64_t)t * p.k_st : p.kp + poff;
-      const ST* va = from_new ? vn_b + (int64_t)t * p.v_st : p.vp + poff;
-      kr[n] = ld16(ka + col);
-      vr[n] = ld16(va + col);
+      const ST* ka = from_new ? kn_b + (int64_t)t * p.k_st + col : p.kp + poff + pcol;
+      const ST* va = from_new ? vn_b + (int64_t)t * p.v_st + col : p.vp + poff + pcol;
+      kr[n] = ld16(ka);
+      vr[n] = ld16(va);
     }
     wave_lds_sync();
 
@@ -348,8 +363,8 @@ __global__ void __launch_bounds__(64) relpos_attn_kernel(const AttnK<ST> p) {
         if (j < p.Lk && j >= p.left) {
           const int64_t off = page_offset(p.pg, ring, A + (j - p.left));
           if (off >= 0) {
-            st16(p.kp + off + col, kr[n]);
-            st16(p.vp + off + col, vr[n]);
+            st16(p.kp + off + pcol, kr[n]);
+            st16(p.vp + off + pcol, vr[n]);
           }
         }
       }
@@ -486,31 +501,33 @@ __device__ static inline __amdgpu_buffer_rsrc_t rows_rsrc(const void* base, int 
 
 // Workgroup of 4 waves: 4 / SPLIT streams of one head h and one query pair,
 // each stream's head split over SPLIT = head_dim / 64 waves of 64 columns.
-// The window's keys are handled in score slots: per pass, NT tiles of 16 slots
-// hold cached history (window column j = jb + slot, read from the pages) and
-// one more tile holds this step's frames (j = left + slot - 16*NT, read from
-// the projection output); the frames' tile is live in the last pass only, and
-// a chunk is at most 16 frames.  So every load reads exactly one source, and
-// absent rows (positions before the stream's first frame, columns past the
-// history, slots past the chunk) read zeros through the buffer range check.
+// Score slots are window columns: per pass, NT tiles of 16 slots hold columns
+// jb .. jb + 16*NT - 1; column j is cached history (j < left, read from the
+// pages), one of this step's frames (left <= j < left + chunk, read from the
+// projection output) or past the window.  Absent rows (positions before the
+// stream's first frame, pages the stream does not hold, columns past the
+// window) read zeros through the buffer range check.
 // Per pass:
 //   * the position rows the pass needs (shared by the workgroup's streams) are
 //     staged once in LDS, rows padded by 16 bytes so the 16 lanes of an MFMA
-//     operand read hit distinct banks;
+//     operand read hit distinct banks; only the tiles that hold a row some
+//     valid slot reads are staged and multiplied;
 //   * (q+u).k and (q+v).pos on 16x16x32 MFMAs: A rows 0..7 hold (q+u) and
 //     (q+v) of both queries split into high and low 16-bit parts, so the
 //     16-bit operands lose nothing against the fp32 query + bias sums; B is a
-//     tile of 16 K rows (lane = key, 16 columns) or 16 staged position rows;
-//     the SPLIT waves' partial sums meet in LDS;
+//     tile of 16 K rows (lane = key, 8 columns per k-step) or 16 staged
+//     position rows; the SPLIT waves' partial sums meet in LDS;
 //   * scores and the online softmax spread over the 64 lanes (slot = lane,
 //     lane + 64);
 //   * P.V on 16x16x16 MFMAs: A = the probabilities (high and low 16-bit
 //     parts), B = 16 V rows x 16 columns transposed on the way out of LDS by
 //     ds_read_b64_tr_b16 (the wave writes its V tile row-major and each 16-lane
 //     group reads 4 rows x 16 columns back transposed);
-//   * the fused append stores the frames' tile into the pages (query group 0).
-// Every load that does not depend on the page table is issued in one round
-// trip; all K and V rows of the pass follow back to back.
+//   * the fused append stores the lanes holding this step's frames into their
+//     pages (query group 0).
+// Pages hold 64-byte column blocks ([page][block][page_size][32 elements]),
+// so one k-step load of a 16-slot tile reads 16 rows x 64 bytes of one block:
+// 1 KB of contiguous memory when the 16 slots share a page.
 template <typename ST, int DK, int NT, int MODE, bool MULTI>
 __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p) {
   constexpr int SPLIT = DK / 64;
@@ -519,19 +536,19 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
   constexpr int NTH = 64 * NW;
   constexpr int TQ = 2;
   constexpr int KS = 2;            // 16x16x32 k-steps over the wave's 64 columns
-  constexpr int KT = 16 * NT;      // history slots per pass
-  constexpr int NS = KT + 16;      // slots per pass: history + this step's frames
-  constexpr int NPT = (NS + TQ - 1 + 15) / 16;  // position-row tiles
+  constexpr int KT = 16 * NT;      // slots (window columns) per pass
+  constexpr int NPT = NT + 1;      // position-row tiles: slot s of query ii reads row s + TQ-1-ii
   constexpr int PROWS = 16 * NPT;
   constexpr int PSTRIDE = DK * 2 + 16;          // bytes per staged position row
   constexpr int CHR = DK / 8;                   // 16-byte chunks per staged row
   constexpr int PCH = (PROWS * CHR + NTH - 1) / NTH;  // staged chunks per thread
   constexpr int VSTRIDE = 64 * 2 + 16;          // bytes per staged V row
-  constexpr int SK = (NS + 63) / 64;            // slots per lane per query
+  constexpr int SK = (KT + 63) / 64;            // slots per lane per query
   constexpr float NEG = -1e30f;
   constexpr float MASKED = -1e5f * 1.4426950408889634f;  // -1e5 in log2 units
   constexpr int mask_mode = MODE;  // 0 none, 1 mask bytes, 2 stream state
   constexpr int ES = 2;            // bytes per element
+  constexpr int BLK = 64;          // bytes per page row in a column block
   typedef typename Mma<ST>::H H;
 
   // The staged position rows are dead once the dot products are in LDS (the
@@ -539,14 +556,14 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
   // and low parts of the probabilities, [hi|lo][query][slot]) reuses their
   // space.
   constexpr int POS_BYTES = PROWS * PSTRIDE;
-  constexpr int PV_BYTES = NW * 16 * VSTRIDE + NW * 2 * TQ * NS * 2;
+  constexpr int PV_BYTES = NW * 16 * VSTRIDE + NW * 2 * TQ * KT * 2;
   __shared__ __attribute__((aligned(16))) uint8_t stage_lds[POS_BYTES > PV_BYTES ? POS_BYTES : PV_BYTES];
   __shared__ float bd_lds[NW][TQ][PROWS];
-  __shared__ float ac_lds[NW][TQ][NS];
+  __shared__ float ac_lds[NW][TQ][KT];
   uint8_t* const pos_lds = stage_lds;
   uint8_t (*const v_lds)[16 * VSTRIDE] = reinterpret_cast<uint8_t (*)[16 * VSTRIDE]>(stage_lds);
-  uint16_t (*const p_lds)[2][TQ][NS] =
-      reinterpret_cast<uint16_t (*)[2][TQ][NS]>(stage_lds + NW * 16 * VSTRIDE);
+  uint16_t (*const p_lds)[2][TQ][KT] =
+      reinterpret_cast<uint16_t (*)[2][TQ][KT]>(stage_lds + NW * 16 * VSTRIDE);
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -562,36 +579,33 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
   const int b_raw = sb * SPW + sw;
   const int b = min(b_raw, p.B - 1);  // loads stay inside the batch arrays
   const int hcol = h * DK + hf * 64;       // first column of the wave
-  // k-step ks of the wave's 64 columns covers columns ks*32 .. ks*32 + 31; the
-  // lane holds 8 of them, ks*32 + kg*8 ..  So one 16-byte load per lane and
-  // k-step reads one whole 64-byte half of each of 16 rows' 128-byte lines,
-  // and every half line is requested once.
+  // k-step ks of the wave's 64 columns covers columns ks*32 .. ks*32 + 31 (one
+  // 64-byte page block); the lane holds 8 of them, ks*32 + kg*8 ..
   const int cbyte = (hcol + kg * 8) * ES;  // byte offset of the lane's k-step 0 columns in a row
   constexpr int KSB = 32 * ES;             // bytes between a lane's k-steps
   const int M = p.pg.max_pages;
   const bool paged = p.pg.rows != nullptr;
+  const int nblk = p.pg.D >> 5;            // column blocks per page row
+  // byte offset of the wave's k-step ks block in a page, added as soffset
+  const int blk_soff = (hcol >> 5) << (p.pg.page_shift + 6);
+  const int blk_step = 1 << (p.pg.page_shift + 6);
 
   // Every resource has a valid base and a non-zero row stride (the range check
   // that turns absent rows into zeros is index-based); a zero stride can only
-  // come with a single row, where any stride addresses it.  Without pages the
-  // pool resources are never read or written.
+  // come with a single row, where any stride addresses it.  The pool resources
+  // address 64-byte block rows: index page*page_size*nblk + row, so a page row
+  // index never reaches past the layer slab.  Without pages the pool resources
+  // are never read or written.
   const int dmodel = p.H * DK;
   const int st_k = (int)(p.k_st > 0 ? p.k_st : dmodel) * ES;
   const int st_v = (int)(p.v_st > 0 ? p.v_st : dmodel) * ES;
   const int st_p = (int)(p.pos_sr > 0 ? p.pos_sr : dmodel) * ES;
-  const __amdgpu_buffer_rsrc_t r_kp =
-      paged ? rows_rsrc(p.kp, p.pg.D * ES, (uint32_t)p.pg.num_pages << p.pg.page_shift)
-            : rows_rsrc(p.kn, st_k, 0u);
-  const __amdgpu_buffer_rsrc_t r_vp =
-      paged ? rows_rsrc(p.vp, p.pg.D * ES, (uint32_t)p.pg.num_pages << p.pg.page_shift)
-            : rows_rsrc(p.vn, st_v, 0u);
+  const uint32_t pool_rows = paged ? ((uint32_t)p.pg.num_pages << p.pg.page_shift) * (uint32_t)nblk : 0u;
+  const __amdgpu_buffer_rsrc_t r_kp = rows_rsrc(paged ? (const void*)p.kp : (const void*)p.kn, BLK, pool_rows);
+  const __amdgpu_buffer_rsrc_t r_vp = rows_rsrc(paged ? (const void*)p.vp : (const void*)p.vn, BLK, pool_rows);
   const __amdgpu_buffer_rsrc_t r_kn = rows_rsrc(p.kn + b * p.k_sb, st_k, (uint32_t)p.T);
   const __amdgpu_buffer_rsrc_t r_vn = rows_rsrc(p.vn + b * p.v_sb, st_v, (uint32_t)p.T);
   const __amdgpu_buffer_rsrc_t r_pos = rows_rsrc(p.pos, st_p, (uint32_t)p.pos_rows);
-
-  // window column of score slot s in pass jb; the frames' slots follow the
-  // history slots
-  auto slot_col = [&](int jb, int s) { return s < KT ? jb + s : p.left + (s - KT); };
 
   // ---------------- prologue: every load independent of the page table,
   //                  issued branch-free (absent inputs read a valid stand-in
@@ -621,25 +635,23 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
       braw[ks] = ld16(brow + ks * 32);
     }
   }
-  // this step's frames (last pass; they do not depend on the pages)
-  u32x4 kf[KS], vf[KS];
-  {
-    const uint32_t fr = q16 < p.T ? (uint32_t)q16 : kNoRow;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      kf[ks] = pk_buffer_load_x4(r_kn, fr, cbyte + ks * KSB, 0, 0);
-      vf[ks] = pk_buffer_load_x4(r_vn, fr, cbyte + ks * KSB, 0, 0);
-    }
-  }
+  // the last slot any query of the pass at jb reads, and the position-row
+  // tiles it needs (slot s of query ii reads staged row s + TQ - 1 - ii)
+  auto pass_tiles = [&](int jb) {
+    const int s_max = min(KT, p.Lk - jb) - 1;
+    return min(NPT, (s_max + TQ - 1) / 16 + 1);
+  };
   // position rows (rows outside the table read zeros) and mask bytes of a pass
   u32x4 pst[PCH];
   uint8_t mk[SK][TQ];
   auto load_pass_shared = [&](int jb) {
     const int rb = jb + p.T - i0 - TQ;
+    const int nchunk = pass_tiles(jb) * 16 * CHR;
 #pragma unroll
     for (int c = 0; c < PCH; ++c) {
       const int idx = min((int)threadIdx.x + c * NTH, PROWS * CHR - 1);
-      pst[c] = pk_buffer_load_x4(r_pos, rb + idx / CHR, (h * DK + (idx % CHR) * 8) * ES, 0, 0);
+      pst[c] = u32x4{0u, 0u, 0u, 0u};
+      if (idx < nchunk) pst[c] = pk_buffer_load_x4(r_pos, rb + idx / CHR, (h * DK + (idx % CHR) * 8) * ES, 0, 0);
     }
     if (mask_mode == 1) {
 #pragma unroll
@@ -647,7 +659,7 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
 #pragma unroll
         for (int ii = 0; ii < TQ; ++ii) {
           const int ic = min(i0 + ii, p.T - 1);
-          const int jc = min(max(slot_col(jb, min(lane + 64 * r, NS - 1)), 0), p.Lk - 1);
+          const int jc = min(jb + min(lane + 64 * r, KT - 1), p.Lk - 1);
           mk[r][ii] = p.mask[b * p.m_sb + h * p.m_sh + (int64_t)ic * p.m_st + jc];
         }
     }
@@ -671,16 +683,16 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
   const uint32_t lp0 = (uint32_t)max(win0, 0) >> p.pg.page_shift;
   const int r0 = paged ? (int)(lp0 % (uint32_t)M) : 0;
   const uint32_t pmask = (1u << p.pg.page_shift) - 1u;
-  // page row of window column j (a frame position of the stream), kNoRow if
-  // the stream holds none; every lane must be active (ds_bpermute)
+  const uint32_t page_blk_rows = (uint32_t)nblk << p.pg.page_shift;  // block rows per page
+  // block-row index of window column j (a frame position of the stream), kNoRow
+  // if the stream holds none; every lane must be active (ds_bpermute)
   auto page_row = [&](int j) {
     const int pos = win0 + j;
     int ridx = r0 + (int)(((uint32_t)max(pos, 0) >> p.pg.page_shift) - lp0);
     ridx = ridx >= M ? ridx - M : ridx;
     const int page = __shfl(ring_lane, ridx);
-    return (paged && pos >= 0 && page >= 0)
-               ? ((uint32_t)page << p.pg.page_shift) | ((uint32_t)pos & pmask)
-               : kNoRow;
+    return (paged && pos >= 0 && page >= 0) ? (uint32_t)page * page_blk_rows + ((uint32_t)pos & pmask)
+                                            : kNoRow;
   };
   StreamMask sm{};
   int qchunk[TQ];
@@ -721,12 +733,12 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
   uint8_t* vl = v_lds[wave];
   const bool do_append = p.append && blockIdx.z == 0 && active && paged;
 
-  // MULTI: history longer than one pass (the single-pass form is straight-line
+  // MULTI: windows longer than one pass (the single-pass form is straight-line
   // code, with nothing carried around a loop)
   const int npass = MULTI ? p.tiles : 1;
   for (int pass = 0; pass < npass; ++pass) {
     const int jb = pass * KT;
-    const bool last = pass == npass - 1;  // the frames' slots are live
+    const int npt = pass_tiles(jb);
     if (MULTI && pass > 0) load_pass_shared(jb);
 
     // ---- stage the position rows of the pass
@@ -737,29 +749,37 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
         *reinterpret_cast<u32x4*>(pos_lds + (idx / CHR) * PSTRIDE + (idx % CHR) * 16) = pst[c];
     }
 
-    // ---- history K and V rows, lane = slot 16*kt + q16, columns ks*32 + kg*8
-    //      .. ks*32 + kg*8 + 7 of the wave's 64: page rows first, then all loads
-    uint32_t prow[NT];
+    // ---- K and V rows, lane = slot 16*kt + q16 (window column jb + slot),
+    //      columns ks*32 + kg*8 .. + 7 of the wave's 64: block rows and frame
+    //      rows first, then the K loads.  A tile that holds one of this step's
+    //      frames also reads the projection output; every lane takes exactly
+    //      one source (the other reads zeros), so the two are OR-ed.
+    uint32_t prow[NT], frow[NT], arow[NT];
 #pragma unroll
     for (int kt = 0; kt < NT; ++kt) {
       const int j = jb + 16 * kt + q16;
       const uint32_t r = page_row(j);
+      const bool frame = j >= p.left && j < p.Lk;
       prow[kt] = j < p.left ? r : kNoRow;
+      frow[kt] = frame ? (uint32_t)(j - p.left) : kNoRow;
+      arow[kt] = frame ? r : kNoRow;  // append target of a frame
     }
+    // tile kt holds a frame of this step (workgroup-uniform)
+    auto has_frames = [&](int kt) { return jb + 16 * kt + 15 >= p.left && jb + 16 * kt < p.Lk; };
     u32x4 kr[NT][KS], vr[NT][KS];
 #pragma unroll
     for (int kt = 0; kt < NT; ++kt)
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) kr[kt][ks] = pk_buffer_load_x4(r_kp, prow[kt], cbyte + ks * KSB, 0, 0);
-    // the frames' page rows (append target): looked up with every lane
-    // active, then restricted to the lanes holding one of the chunk's frames
-    const uint32_t frow_all = page_row(p.left + q16);
-    const uint32_t frow = (last && q16 < p.T) ? frow_all : kNoRow;
+      for (int ks = 0; ks < KS; ++ks) {
+        kr[kt][ks] = pk_buffer_load_x4(r_kp, prow[kt], kg * 16, blk_soff + ks * blk_step, 0);
+        if (has_frames(kt)) kr[kt][ks] |= pk_buffer_load_x4(r_kn, frow[kt], cbyte + ks * KSB, 0, 0);
+      }
     __syncthreads();  // position rows staged
 
     // ---- (q+v).pos over the wave's columns: D rows 4..7 (lanes 16..31)
 #pragma unroll
     for (int pt = 0; pt < NPT; ++pt) {
+      if (pt >= npt) break;
       f32x4_t d = {0.f, 0.f, 0.f, 0.f};
       const uint8_t* src = pos_lds + (pt * 16 + q16) * PSTRIDE + (hf * 64 + kg * 8) * 2;
 #pragma unroll
@@ -772,31 +792,35 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
     }
     // ---- (q+u).k over the wave's columns: D rows 0..3 (lanes 0..15)
 #pragma unroll
-    for (int kt = 0; kt <= NT; ++kt) {
+    for (int kt = 0; kt < NT; ++kt) {
       f32x4_t d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) d = Mma<ST>::k32(aop[ks], kt < NT ? kr[kt][ks] : kf[ks], d);
+      for (int ks = 0; ks < KS; ++ks) d = Mma<ST>::k32(aop[ks], kr[kt][ks], d);
       if (kg == 0) {
         ac_lds[wave][0][16 * kt + q16] = d[0] + d[2];
         ac_lds[wave][1][16 * kt + q16] = d[1] + d[3];
       }
     }
-    // ---- fused append of this step's K and V rows (query group 0): the row
-    //      index is valid only for lanes holding one of the chunk's frames
-    if (do_append && last) {
+    // ---- fused append of this step's K rows (query group 0): the row index
+    //      is valid only for lanes holding one of the chunk's frames
+    if (do_append) {
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        pk_buffer_store_x4(kf[ks], r_kp, frow, cbyte + ks * KSB, 0, 0);
-        pk_buffer_store_x4(vf[ks], r_vp, frow, cbyte + ks * KSB, 0, 0);
-      }
+      for (int kt = 0; kt < NT; ++kt)
+        if (has_frames(kt))
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks)
+            pk_buffer_store_x4(kr[kt][ks], r_kp, arow[kt], kg * 16, blk_soff + ks * blk_step, 0);
     }
-    // ---- history V rows, issued once the K rows are consumed (half the
-    //      registers in flight); their latency overlaps the scores and softmax
+    // ---- V rows, issued once the K rows are consumed (half the registers in
+    //      flight); their latency overlaps the scores and softmax
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int kt = 0; kt < NT; ++kt)
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) vr[kt][ks] = pk_buffer_load_x4(r_vp, prow[kt], cbyte + ks * KSB, 0, 0);
+      for (int ks = 0; ks < KS; ++ks) {
+        vr[kt][ks] = pk_buffer_load_x4(r_vp, prow[kt], kg * 16, blk_soff + ks * blk_step, 0);
+        if (has_frames(kt)) vr[kt][ks] |= pk_buffer_load_x4(r_vn, frow[kt], cbyte + ks * KSB, 0, 0);
+      }
     __syncthreads();  // partial dot products of the stream's waves in LDS
 
     // ---- scores: lane handles slots lane + 64*r; online softmax
@@ -804,14 +828,14 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
 #pragma unroll
     for (int r = 0; r < SK; ++r) {
       const int sl = lane + 64 * r;
-      const int slc = min(sl, NS - 1);
-      const int j = slot_col(jb, slc);
-      const bool valid = sl < NS && (slc < KT ? j < p.left : (last && slc - KT < p.T));
+      const int slc = min(sl, KT - 1);
+      const int j = jb + slc;
+      const bool valid = sl < KT && j < p.Lk;
 #pragma unroll
       for (int ii = 0; ii < TQ; ++ii) {
         float ac = 0.f, bd = 0.f;
         // (q+v).pos row of column j for query i0 + ii, relative to the staged rows
-        const int prw = min(max(j - jb + TQ - 1 - ii, 0), PROWS - 1);
+        const int prw = min(slc + TQ - 1 - ii, PROWS - 1);
 #pragma unroll
         for (int x = 0; x < SPLIT; ++x) {
           ac += ac_lds[w0 + x][ii][slc];
@@ -839,7 +863,7 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
         const int sl = lane + 64 * r;
         const float e = s[r][ii] > 0.5f * NEG ? __builtin_amdgcn_exp2f(s[r][ii] - mnew) : 0.f;
         lsum += e;
-        if (sl < NS) {  // e = hi + lo in the operand type, exact to ~2^-17
+        if (sl < KT) {  // e = hi + lo in the operand type, exact to ~2^-17
           const H hi = (H)e;
           const H lo = (H)(e - (float)hi);
           p_lds[wave][0][ii][sl] = __builtin_bit_cast(uint16_t, hi);
@@ -857,6 +881,16 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
     }
     wave_lds_sync();
 
+    // ---- fused append of this step's V rows
+    if (do_append) {
+#pragma unroll
+      for (int kt = 0; kt < NT; ++kt)
+        if (has_frames(kt))
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks)
+            pk_buffer_store_x4(vr[kt][ks], r_vp, arow[kt], kg * 16, blk_soff + ks * blk_step, 0);
+    }
+
     // ---- P.V, 16 slots at a time: stage the V rows, read them back
     //      transposed; A row m = q16 & 3 holds the high (m < 2) or low part of
     //      query m & 1's probabilities, so D[q] + D[2 + q] is the product with
@@ -864,10 +898,10 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
     //      are never read
     const uint16_t* p_arow = &p_lds[wave][(q16 >> 1) & 1][q16 & 1][0];
 #pragma unroll
-    for (int kt = 0; kt <= NT; ++kt) {
+    for (int kt = 0; kt < NT; ++kt) {
       uint8_t* vrow = vl + q16 * VSTRIDE + kg * 16;
-      *reinterpret_cast<u32x4*>(vrow) = kt < NT ? vr[kt][0] : vf[0];
-      *reinterpret_cast<u32x4*>(vrow + KSB) = kt < NT ? vr[kt][1] : vf[1];
+      *reinterpret_cast<u32x4*>(vrow) = vr[kt][0];
+      *reinterpret_cast<u32x4*>(vrow + KSB) = vr[kt][1];
       const i16x4_t pop = *reinterpret_cast<const i16x4_t*>(p_arow + 16 * kt + 4 * kg);
       wave_lds_sync();
 #pragma unroll
@@ -882,17 +916,24 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
     if (MULTI) __syncthreads();  // the next pass restages pos_lds and rewrites bd / ac
   }
 
-  // ---- write: lanes 0..15 hold column nt*16 + q16 of both queries
-  if (active && kg == 0) {
+  // ---- write: lanes 0..15 hold column nt*16 + q16 of both queries; the wave's
+  //      two 128-byte output rows go through its V staging rows so that 16
+  //      lanes store them 16 bytes each
+  if (active) {
+    if (kg == 0) {
 #pragma unroll
-    for (int ii = 0; ii < TQ; ++ii) {
-      if (ii >= nq) continue;
-      const float inv = l_run[ii] > 0.f ? __builtin_amdgcn_rcpf(l_run[ii]) : 0.f;
-      ST* orow = p.out + b * p.o_sb + (int64_t)(i0 + ii) * p.o_st + hcol + q16;
+      for (int ii = 0; ii < TQ; ++ii) {
+        const float inv = l_run[ii] > 0.f ? __builtin_amdgcn_rcpf(l_run[ii]) : 0.f;
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt)
-        *reinterpret_cast<H*>(orow + nt * 16) = (H)((oacc[nt][ii] + oacc[nt][2 + ii]) * inv);
+        for (int nt = 0; nt < 4; ++nt)
+          *reinterpret_cast<H*>(vl + ii * VSTRIDE + (nt * 16 + q16) * 2) = (H)((oacc[nt][ii] + oacc[nt][2 + ii]) * inv);
+      }
     }
+    wave_lds_sync();
+    const int oi = lane >> 3;  // query of the lane's 16 bytes
+    if (lane < 16 && oi < nq)
+      *reinterpret_cast<u32x4*>(p.out + b * p.o_sb + (int64_t)(i0 + oi) * p.o_st + hcol + (lane & 7) * 8) =
+          *reinterpret_cast<const u32x4*>(vl + oi * VSTRIDE + (lane & 7) * 16);
   }
 }
 
@@ -926,7 +967,7 @@ __global__ void __launch_bounds__(256) kv_append_kernel(const CopyK<ST> p) {
     const int32_t* row = p.pg.rows + (int64_t)b * p.pg.rows_stride;
     const int64_t off = page_offset(p.pg, row + 1, (int64_t)row[0] + t);
     if (off < 0) continue;
-    const int64_t e = off + (int64_t)c * VEC;
+    const int64_t e = off + page_col(p.pg, c * VEC);
     st16(p.kp + e, ld16(p.k + b * p.k_sb + (int64_t)t * p.k_st + c * VEC));
     st16(p.vp + e, ld16(p.v + b * p.v_sb + (int64_t)t * p.v_st + c * VEC));
   }
@@ -948,8 +989,8 @@ __global__ void __launch_bounds__(256) kv_gather_kernel(const CopyK<ST> p) {
     if (pos >= 0) {
       const int64_t off = page_offset(p.pg, row + 1, pos);
       if (off >= 0) {
-        kv = ld16(p.kp + off + (int64_t)c * VEC);
-        vv = ld16(p.vp + off + (int64_t)c * VEC);
+        kv = ld16(p.kp + off + page_col(p.pg, c * VEC));
+        vv = ld16(p.vp + off + page_col(p.pg, c * VEC));
       }
     }
     st16(p.ko + b * p.k_sb + (int64_t)r * p.k_st + c * VEC, kv);
@@ -1021,7 +1062,8 @@ int log2_exact(int x) {
 }
 
 // Validates the paged layout for `batch` rows; fills the device view.
-int pages_view(const pk_paged_layout& L, int layer, int vec, const char* what, PagesK* out) {
+int pages_view(const pk_paged_layout& L, int layer, int vec, int elem_bytes, const char* what,
+               PagesK* out) {
   if (!L.k_pool || !L.v_pool || !L.rows)
     return fail(PK_ERR_INVALID, "%s: k_pool, v_pool and rows must be set", what);
   if (!aligned16(L.k_pool) || !aligned16(L.v_pool))
@@ -1037,6 +1079,11 @@ int pages_view(const pk_paged_layout& L, int layer, int vec, const char* what, P
   if (L.d_model <= 0 || L.d_model % vec != 0)
     return fail(PK_ERR_INVALID, "%s: d_model %d must be a positive multiple of %d", what,
                 L.d_model, vec);
+  int cb = 64 / elem_bytes;  // column block: gcd(d_model, 64 bytes of elements)
+  while (L.d_model % cb != 0) cb >>= 1;
+  if ((int64_t)L.num_pages * L.page_size * (L.d_model / cb) >= (1LL << 32))
+    return fail(PK_ERR_INVALID, "%s: a layer slab of %d pages exceeds 2^32 block rows", what,
+                L.num_pages);
   out->rows = L.rows;
   out->rows_stride = L.rows_stride;
   out->max_pages = L.max_pages;
@@ -1044,6 +1091,7 @@ int pages_view(const pk_paged_layout& L, int layer, int vec, const char* what, P
   out->num_pages = L.num_pages;
   out->page_elems = (int64_t)L.page_size * L.d_model;
   out->D = L.d_model;
+  out->cb_shift = log2_exact(cb);
   return PK_OK;
 }
 
@@ -1148,8 +1196,8 @@ int launch_attn_mfma_mode(const pk_attn_args* a, const AttnK<ST>& k, hipStream_t
 
 template <typename ST, int DK>
 int launch_attn_mfma(const pk_attn_args* a, AttnK<ST>& k, hipStream_t s) {
-  constexpr int KT = 16 * kMfmaTiles;  // history slots per pass
-  k.tiles = k.left > 0 ? (k.left + KT - 1) / KT : 1;
+  constexpr int KT = 16 * kMfmaTiles;  // window columns per pass
+  k.tiles = (k.Lk + KT - 1) / KT;
   if (k.mask) return launch_attn_mfma_mode<ST, DK, 1>(a, k, s);
   if (k.st_proc) return launch_attn_mfma_mode<ST, DK, 2>(a, k, s);
   return launch_attn_mfma_mode<ST, DK, 0>(a, k, s);
@@ -1199,7 +1247,7 @@ int attn_typed(const pk_attn_args* a, hipStream_t s) {
   k.v_st = a->value_stride_t;
   const bool need_pages = a->left > 0 || a->append;
   if (need_pages) {
-    const int rc = pages_view(a->pages, a->layer, VEC, what, &k.pg);
+    const int rc = pages_view(a->pages, a->layer, VEC, (int)sizeof(ST), what, &k.pg);
     if (rc != PK_OK) return rc;
     if (a->pages.d_model != D)
       return fail(PK_ERR_INVALID, "%s: pages.d_model %d != heads*head_dim %d", what,
@@ -1262,7 +1310,7 @@ int attn_typed(const pk_attn_args* a, hipStream_t s) {
                       row_bytes(a->key_stride_t) <= kMaxBufferStride &&
                       row_bytes(a->value_stride_t) <= kMaxBufferStride &&
                       row_bytes(a->pos_stride) <= kMaxBufferStride &&
-                      (!need_pages || ((int64_t)a->pages.num_pages * a->pages.page_size < (1LL << 32)));
+                      (!need_pages || k.pg.cb_shift == 5);  // 64-byte page column blocks
     if (a->rows_per_lane == 0 && fits && a->chunk <= 16) {
       if (DK == 64) return launch_attn_mfma<ST, 64>(a, k, s);
       return launch_attn_mfma<ST, 128>(a, k, s);
@@ -1288,7 +1336,7 @@ int copy_typed(bool gather, const pk_paged_layout& L, int layer, int B, int rows
   constexpr int VEC = Tr<ST>::VEC;
   CopyK<ST> p{};
   if (B == 0) return PK_OK;
-  int rc = pages_view(L, layer, VEC, what, &p.pg);
+  int rc = pages_view(L, layer, VEC, (int)sizeof(ST), what, &p.pg);
   if (rc != PK_OK) return rc;
   if (!k || !v || !aligned16(k) || !aligned16(v))
     return fail(PK_ERR_INVALID, "%s: K/V tensors must be non-NULL and 16-byte aligned", what);

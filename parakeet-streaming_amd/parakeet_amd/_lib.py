@@ -15,7 +15,7 @@ from pathlib import Path
 LIB_NAME = "libparakeet_paged.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1

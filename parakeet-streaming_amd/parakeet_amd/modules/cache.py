@@ -5,7 +5,8 @@
 ``reset_slot``, ``view``) but stores attention K/V in pages instead of a dense
 ``[N, Ly, left+right+1, D]`` shift buffer:
 
-* ``k_pages`` / ``v_pages``: ``[Ly, num_pages, page_size, D]`` device pools;
+* ``k_pages`` / ``v_pages``: ``[Ly, num_pages, page_size, D]`` device pools
+  (each page stored as 64-byte column blocks, ``ops.page_blocks``);
 * a host :class:`~parakeet_amd.pool.PagePool` owns the page rings of every slot;
 * each step (one pass over all layers) advances every stream of the batch by
   ``right + 1`` frames: pages that slid out of the window go back to the free

@@ -8,6 +8,7 @@ here computes on the CPU: without the library or a HIP device the call raises.
 from __future__ import annotations
 
 import ctypes
+import math
 from dataclasses import dataclass
 
 import torch
@@ -63,10 +64,29 @@ def _rows3(t: torch.Tensor, name: str, B: int, T: int, D: int, dtype: torch.dtyp
         raise ValueError(f"{name}: last dimension must be contiguous")
 
 
+def page_column_block(d_model: int, element_size: int) -> int:
+    """Columns per page column block: gcd(d_model, 64 bytes of elements)."""
+    return math.gcd(d_model, 64 // element_size)
+
+
+def page_blocks(pool: torch.Tensor) -> torch.Tensor:
+    """The element order of a page pool: a [Ly, num_pages, P, D] pool tensor
+    holds each page as column blocks of CB = page_column_block(D, element size)
+    columns (64 bytes at the model shapes), so page row r, column c of
+    (layer, page) is ``page_blocks(pool)[layer, page, c // CB, r, c % CB]``.
+    Returns that [Ly, num_pages, D // CB, P, CB] view of the same memory (for
+    filling or reading pages directly)."""
+    Ly, N, P, D = pool.shape
+    cb = page_column_block(D, pool.element_size())
+    return pool.view(Ly, N, D // cb, P, cb)
+
+
 @dataclass
 class PagedKV:
-    """Device view of a batch's pages: pools [Ly, num_pages, P, D] and the
-    per-stream rows {A, ring[max_pages]} (int32 [B, 1 + max_pages])."""
+    """Device view of a batch's pages: pools of Ly x num_pages pages of P frames
+    x D columns (tensors [Ly, num_pages, P, D] whose pages are stored as 64-byte
+    column blocks, see page_blocks) and the per-stream rows {A, ring[max_pages]}
+    (int32 [B, 1 + max_pages])."""
 
     k_pool: torch.Tensor
     v_pool: torch.Tensor

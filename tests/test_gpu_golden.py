@@ -55,10 +55,12 @@ def test_attention_kernel_matches_golden(cuda, name, dtype):
         rows[b, 0] = left
         for lp in range((L + P - 1) // P):
             rows[b, 1 + lp % M] = b * M + lp
+        kb, vb = ops.page_blocks(kp), ops.page_blocks(vp)
+        nb = kb.shape[2]
         for pos in range(left):
             page = rows[b, 1 + (pos // P) % M]
-            kp[0, page, pos % P] = torch.from_numpy(d["k"][b, pos]).to(dtype)
-            vp[0, page, pos % P] = torch.from_numpy(d["v"][b, pos]).to(dtype)
+            kb[0, page, :, pos % P] = torch.from_numpy(d["k"][b, pos]).to(dtype).view(nb, -1)
+            vb[0, page, :, pos % P] = torch.from_numpy(d["v"][b, pos]).to(dtype).view(nb, -1)
     pages = ops.PagedKV(kp.to(cuda), vp.to(cuda), torch.from_numpy(rows).to(cuda), M)
     dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dtype).to(cuda)  # noqa: E731
     q, kn, vn = dev(d["q"]), dev(d["k"][:, left:]), dev(d["v"][:, left:])
