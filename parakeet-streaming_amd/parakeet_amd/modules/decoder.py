@@ -94,25 +94,45 @@ class GreedyDecoder:
         self._ws: dict[int, torch.Tensor] = {}
         self._graphs: dict[tuple[int, int, int], dict] = {}
 
+    _WEIGHTS = ("w_ih", "w_hh", "b_ih", "b_hh", "embed", "w_pred", "b_pred", "w_enc", "b_enc", "w_out", "b_out")
+
     def refresh_weights(self) -> None:
-        """Contiguous copies of the parameters in the layouts the kernels read
-        (LSTM weights stacked over layers); call after loading new weights."""
+        """Copies of the parameters in the layouts the kernels read (LSTM weights
+        stacked over layers), owned by the decoder; call after loading new
+        weights.  When the shapes are unchanged the new values are copied into
+        the same buffers, so decode steps recorded earlier (graph=True) replay
+        with the new weights; otherwise the recordings are dropped and made
+        again on the next call."""
         lstm = self.pred.prediction["dec_rnn"]
         L = self.layers
+        j = self.joiner
+        out = j.joint_net[-1]
         with torch.no_grad():
-            g = lambda n: torch.stack([getattr(lstm, f"{n}_l{k}") for k in range(L)]).contiguous()
-            self.w_ih, self.w_hh, self.b_ih, self.b_hh = g("weight_ih"), g("weight_hh"), g("bias_ih"), g("bias_hh")
-            self.embed = self.pred.prediction["embed"].weight.detach().contiguous()
-            j = self.joiner
-            self.w_pred, self.b_pred = j.pred.weight.detach().contiguous(), j.pred.bias.detach().contiguous()
-            self.w_enc, self.b_enc = j.enc.weight.detach(), j.enc.bias.detach()
-            out = j.joint_net[-1]
-            self.w_out, self.b_out = out.weight.detach().contiguous(), out.bias.detach().contiguous()
-        if self.w_ih.shape[2] != self.hidden:
+            own = lambda t: t.detach().clone(memory_format=torch.contiguous_format)  # noqa: E731
+            stack = lambda n: torch.stack([getattr(lstm, f"{n}_l{k}") for k in range(L)]).contiguous()  # noqa: E731
+            new = {
+                "w_ih": stack("weight_ih"), "w_hh": stack("weight_hh"), "b_ih": stack("bias_ih"), "b_hh": stack("bias_hh"),
+                "embed": own(self.pred.prediction["embed"].weight),
+                "w_pred": own(j.pred.weight), "b_pred": own(j.pred.bias),
+                "w_enc": own(j.enc.weight), "b_enc": own(j.enc.bias),
+                "w_out": own(out.weight), "b_out": own(out.bias),
+            }
+        if new["w_ih"].shape[2] != self.hidden:
             raise NotImplementedError("the predictor's embedding size must equal its hidden size (config.py:19)")
-        for t in (self.w_ih, self.w_hh, self.b_ih, self.b_hh, self.embed, self.w_pred, self.b_pred, self.w_out, self.b_out):
+        for t in new.values():
             if t.dtype != self.dtype or t.device != self.device:
                 raise ValueError("predictor and joiner parameters must share one dtype and device")
+        cur = getattr(self, "w_ih", None)
+        same = cur is not None and all(getattr(self, k).shape == v.shape for k, v in new.items())
+        if same:
+            with torch.no_grad():
+                for k, v in new.items():
+                    getattr(self, k).copy_(v)  # recorded steps keep reading these buffers
+        else:
+            for k, v in new.items():
+                setattr(self, k, v)
+            if getattr(self, "_graphs", None):
+                self._graphs.clear()  # they hold the old buffers' addresses
 
     def _workspace(self, batch: int) -> torch.Tensor:
         n = int(lib().pk_rnnt_workspace_bytes(ops.dtype_code(self.dtype), batch, self.vocab1, self.layers, self.hidden))

@@ -162,6 +162,35 @@ def test_graph_replay_matches_direct_launches(cuda):
         torch.cuda.synchronize()
 
 
+def test_graph_replay_after_refresh_weights(cuda):
+    """A decode step recorded before new weights are loaded replays with the new
+    weights once refresh_weights() ran (same shapes: the decoder's buffers are
+    updated in place), matching direct launches of a decoder built on them."""
+    dt = torch.float16
+    pred, joint, _ = _model(1026, 512, 1, dt, cuda, seed=9)
+    pred2, joint2, _ = _model(1026, 512, 1, dt, cuda, seed=10)
+    a = GreedyDecoder(pred, joint, blank_id=1026, num_slots=8)
+    slots = np.array([3, 0, 6, 1])
+    a.reset_slot(slots)
+    g = torch.Generator().manual_seed(5)
+    enc = torch.randn(4, 2, 512, generator=g).to(dt).to(cuda)
+    a.decode(slots, enc, graph=True)  # records the step with the first weights
+    with torch.no_grad():
+        pred.load_state_dict(pred2.state_dict())
+        joint.load_state_dict(joint2.state_dict())
+    a.refresh_weights()
+    b = GreedyDecoder(pred2, joint2, blank_id=1026, num_slots=8)
+    a.reset_slot(slots)
+    b.reset_slot(slots)
+    for step in range(3):
+        enc = torch.randn(4, 2, 512, generator=g).to(dt).to(cuda)
+        ta = a.decode(slots, enc, graph=True)
+        tb = b.decode(slots, enc)
+        assert ta == tb, f"step {step}"
+        assert torch.equal(a.h, b.h) and torch.equal(a.c, b.c) and torch.equal(a.pred_proj, b.pred_proj)
+    torch.cuda.synchronize()
+
+
 def test_out_of_range_slot_is_skipped_by_the_kernels(cuda):
     """A slot id outside the state arrays (a caller error the host wrapper
     rejects) reaching the kernels through the C ABI: the kernels treat that
