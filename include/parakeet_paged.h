@@ -509,6 +509,22 @@ typedef struct pk_rnnt_args {
 int64_t pk_rnnt_workspace_bytes(int32_t dtype, int32_t batch, int32_t vocab1, int32_t layers, int32_t hidden);
 int pk_rnnt_greedy_step(const pk_rnnt_args* args, void* stream);
 
+/* pk_rnnt_greedy_step_static -- pk_rnnt_greedy_step without a workspace
+ * argument and without allocating: the step's workspace is a static device
+ * array of PK_RNNT_STATIC_SCRATCH_BYTES (8 MiB) that each GPU the library runs
+ * on holds until the process ends.  No counterpart in the reference; it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops that forbid hipMalloc).  args->workspace must be NULL; every
+ * other argument is pk_rnnt_greedy_step's.  A step whose
+ * pk_rnnt_workspace_bytes(...) exceeds the array is rejected with
+ * PK_ERR_UNSUPPORTED (at fp16 with one 640-unit LSTM layer, about 6,000
+ * streams).  The kernels initialise every scratch word they read, so nothing
+ * needs clearing between calls.  Every call on one GPU shares that GPU's
+ * array: calls that overlap on one GPU (different streams, different threads)
+ * race and must be serialised by the caller. */
+#define PK_RNNT_STATIC_SCRATCH_BYTES (8 << 20)
+int pk_rnnt_greedy_step_static(const pk_rnnt_args* args, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Host page pool: FIFO free-page queue and per-slot page rings.  Thread safe
  * (one internal mutex, the counterpart of Scheduler._state_lock,

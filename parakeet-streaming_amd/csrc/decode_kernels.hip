@@ -30,6 +30,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <mutex>
 
 #include "pk_common.h"
 #include "pk_device.h"
@@ -679,4 +680,60 @@ extern "C" int pk_rnnt_greedy_step(const pk_rnnt_args* a, void* stream) {
     default:
       return run_step<float>(a, (hipStream_t)stream);
   }
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free decode step: the step's workspace is a static device array,
+// one per GPU, held until the process ends.  Its device address is looked up
+// once per device (with that device current) and passed to the kernels like a
+// caller's workspace; the array's name is never used as an address on the host.
+
+static __device__ __align__(256) uint8_t scratch[PK_RNNT_STATIC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// This device's scratch address; the device must be current.
+int scratch_address(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(PK_ERR_HIP, "pk_rnnt_greedy_step_static: no usable current device (%d)", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(PK_ERR_HIP, "pk_rnnt_greedy_step_static: hipGetSymbolAddress on device %d: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return PK_OK;
+}
+
+}  // namespace
+
+extern "C" int pk_rnnt_greedy_step_static(const pk_rnnt_args* a, void* stream) {
+  clear_error();
+  if (!a) return fail(PK_ERR_INVALID, "pk_rnnt_greedy_step_static: args is NULL");
+  if (a->workspace)
+    return fail(PK_ERR_INVALID, "pk_rnnt_greedy_step_static: workspace must be NULL (the static scratch is used)");
+  const int64_t need = pk_rnnt_workspace_bytes(a->dtype, a->batch, a->vocab1, a->layers, a->hidden);
+  if (need < 0) return fail(PK_ERR_INVALID, "pk_rnnt_greedy_step_static: bad batch/vocab1/layers/hidden");
+  if (need > (int64_t)PK_RNNT_STATIC_SCRATCH_BYTES)
+    return fail(PK_ERR_UNSUPPORTED,
+                "pk_rnnt_greedy_step_static: batch %d needs %lld bytes of workspace, the static scratch holds %lld "
+                "(use pk_rnnt_greedy_step with a workspace)",
+                a->batch, (long long)need, (long long)PK_RNNT_STATIC_SCRATCH_BYTES);
+  DeviceGuard dg(a->device);
+  if (!dg.ok) return fail(PK_ERR_HIP, "pk_rnnt_greedy_step_static: cannot select device %d", a->device);
+  void* ptr = nullptr;
+  const int rc = scratch_address(&ptr);
+  if (rc != PK_OK) return rc;
+  pk_rnnt_args b = *a;
+  b.workspace = ptr;
+  return pk_rnnt_greedy_step(&b, stream);
 }

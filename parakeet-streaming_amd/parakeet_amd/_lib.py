@@ -303,6 +303,7 @@ SIGNATURES = {
     "pk_subsample": (c_int, [POINTER(SubArgs), c_void_p]),
     "pk_rnnt_workspace_bytes": (c_int64, [c_int32, c_int32, c_int32, c_int32, c_int32]),
     "pk_rnnt_greedy_step": (c_int, [POINTER(RnntArgs), c_void_p]),
+    "pk_rnnt_greedy_step_static": (c_int, [POINTER(RnntArgs), c_void_p]),
     "pk_pool_create": (
         c_int,
         [c_int32, c_int32, c_int32, c_int32, c_int32, POINTER(c_int32), POINTER(c_void_p)],
