@@ -437,6 +437,38 @@ def encoder_bench(args, device) -> int:
                               layer=layer, eps=conv.batch_norm.eps)
 
         conv_us = _graph_time_us(conv_all_layers, device, inner=1) / Ly
+
+        # the attention kernel alone on the step's own pages, every layer, with
+        # the mask tensor the encoder passes it (full windows after the timed
+        # steps), each launch between HIP events on its stream
+        cache = state.cache
+        pages = cache.paged()
+        ga = torch.Generator().manual_seed(9)
+        qkv_t = torch.randn(B, T, 3 * D, generator=ga).to(dt).to(device)
+        q_t, k_t, v_t = qkv_t.chunk(3, dim=-1)
+        pe = enc.pos_enc.pe[0]
+        ctr = pe.shape[0] // 2 + 1
+        pos_t = torch.nn.functional.linear(pe[ctr - (T + left) : ctr + T + left - 1].to(dt),
+                                           enc.layers[0].self_attn.linear_pos.weight)
+        bu_t = enc.layers[0].self_attn.pos_bias_u.to(dt).contiguous()
+        bv_t = enc.layers[0].self_attn.pos_bias_v.to(dt).contiguous()
+        _, mask_t = ops.streaming_mask(state.processed_frames - T, state.cache_lengths, T, chunk=T, left=left, chunk_size=T)
+        att_out = torch.empty((B, T, D), dtype=dt, device=device)
+        att_reps = 20
+        att_ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(att_reps * Ly)]
+        for a_ev2, b_ev2 in att_ev:
+            a_ev2.record()
+            b_ev2.record()
+        torch.cuda.synchronize()
+        for r in range(att_reps):
+            for layer in range(Ly):
+                a_ev2, b_ev2 = att_ev[r * Ly + layer]
+                ops.paged_relpos_attn(q_t, k_t, v_t, pos_t, bu_t, bv_t, mask_t, num_heads=H, left=left, pages=pages,
+                                      layer=layer, append=True, out=att_out,
+                                      start_event=ops._event_handle(a_ev2), stop_event=ops._event_handle(b_ev2))
+        torch.cuda.synchronize()
+        att_us = 1000.0 * sum(a_ev2.elapsed_time(b_ev2) for a_ev2, b_ev2 in att_ev) / len(att_ev)
+        log("timed the attention kernel on the step's pages")
     s = 2
     conv_bytes = B * s * (T * 2 * D + 2 * (K - 1) * D + T * D) + s * D * (K + 2)
     # front-end algorithmic work per step (steady state: 16 new frames, window of 25)
@@ -446,8 +478,19 @@ def encoder_bench(args, device) -> int:
     # first depthwise + pointwise rows 2..6, second depthwise + pointwise rows 2..3
     sub_macs = B * (11 * F1 * C * 9 + 5 * F2 * C * 9 + 5 * F2 * C * C + 2 * F3 * C * 9 + 2 * F3 * C * C)
     sub_tflops = 2 * sub_macs / (sub_us * 1e-6) / 1e12
-    cpu = dec_cpu = None
+    # attention: algorithmic bytes per launch (K/V window read, K/V append write,
+    # query read and output write, block-table row, mask bytes) plus the shared
+    # position rows and biases
+    max_pages = cache.max_pages
+    att_bytes = B * (s * D * (2 * (left + T) + 4 * T) + 4 * (1 + max_pages) + T * (left + T)) + s * D * (left + 2 * T - 1) + 2 * s * D
+    att_gbs = att_bytes / (att_us * 1e-6) / 1e9
+    cpu = dec_cpu = att_cpu = None
     if not args.no_cpu_baseline:
+        from parakeet_amd import synth
+
+        att_cpu = cpu_baseline(synth.SMALL_FP16, B, args.cpu_baseline_seconds, seed=5)
+        att_cpu["sample"] = ("the reference's dense encoder-attention path only (not the whole pcm16 -> tokens step): "
+                             + att_cpu["sample"])
         dec_cpu = decode_cpu_baseline(pred, joint, vocab, min(args.cpu_baseline_seconds, 10.0), B)
         sd = {k: v.detach().double().cpu().numpy() for k, v in sub.state_dict().items()}
         cb = front_end_cpu_baseline(sd, min(args.cpu_baseline_seconds, 10.0), seed=8)
@@ -508,6 +551,19 @@ def encoder_bench(args, device) -> int:
             },
             "cpu_baseline": cpu,
         },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(att_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(att_gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "relpos_attn_mfma_kernel (fused append + paged rel-pos attention, mask tensor)",
+            "avg_kernel_us": round(att_us, 3),
+            "bytes_per_launch": att_bytes,
+            "launches_timed": len(att_ev),
+        },
+        "cpu_baseline": att_cpu,
         "realtime": {
             "audio_ms_per_step": 1000.0 * chunk / 16000.0,
             "streams": B,

@@ -145,7 +145,11 @@ class Scheduler:
             raise RuntimeError("State pool not initialized.")
         seqs = list(seqs)
         slot_ids = [seq.encoder_state for seq in seqs]
-        slot_index = torch.tensor(slot_ids, device=self._state_device, dtype=torch.long)
+        # from pinned memory, without waiting for the GPU (torch keeps the pinned
+        # buffer until the copy has run)
+        slot_index = torch.tensor(slot_ids, dtype=torch.long)
+        dev = torch.device(self._state_device)
+        slot_index = slot_index.pin_memory().to(dev, non_blocking=True) if dev.type == "cuda" else slot_index.to(dev)
         pool = self._pool_state
         state = StreamingState(
             cache=pool.cache.batch(slot_ids),

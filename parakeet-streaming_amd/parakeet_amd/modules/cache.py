@@ -123,8 +123,14 @@ class ModelCache:
         n = int(self._slots.shape[0])
         self._prefix = bool(n == 0 or np.array_equal(self._slots, np.arange(n, dtype=np.int32)))
         dev = self._base.k_pages.device
-        self._slot_index = None if self._prefix else torch.as_tensor(self._slots, dtype=torch.long).to(dev)
-        self._slots_i32 = torch.as_tensor(self._slots, dtype=torch.int32).to(dev)
+        # uploads from pinned memory that do not wait for the GPU (torch keeps the
+        # pinned buffers until the copies have run)
+        def up(a):
+            t = torch.from_numpy(a)
+            return t.pin_memory().to(dev, non_blocking=True) if dev.type == "cuda" else t.to(dev)
+
+        self._slot_index = None if self._prefix else up(self._slots.astype(np.int64))
+        self._slots_i32 = up(self._slots.copy())
         self._rows = torch.zeros((n, 1 + self.max_pages), dtype=torch.int32, device=dev)
         self._seen: set[int] = set()
         self._step_open = False
