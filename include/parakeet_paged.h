@@ -128,8 +128,11 @@ int pk_kv_gather(const pk_kv_gather_args* args, void* stream);
  * (cache=None in the reference).
  * query/key/value: [batch][chunk][num_heads*head_dim], strides (b, t), last dim
  * contiguous.  pos: [pos_rows][num_heads*head_dim], row stride pos_stride; needs
- * pos_rows >= window + chunk - 1.  bias_u/bias_v: [num_heads][head_dim]
- * contiguous.  out: [batch][chunk][d_model].
+ * pos_rows >= window + chunk - 1; pos_stride_b != 0 gives every stream its own
+ * table, stream b's at pos + b * pos_stride_b (a linear_pos(pos_emb) of batch
+ * `batch`, which the reference broadcasts like a batch-1 table,
+ * attention.py:102-106).  bias_u/bias_v: [num_heads][head_dim] contiguous.
+ * out: [batch][chunk][d_model].
  * The mask comes from one of three sources:
  *   mask != NULL   uint8/bool [batch][heads][chunk][window] with element strides
  *                  (b, h, t) and unit stride along window (mask_stride_h 0
@@ -193,6 +196,7 @@ typedef struct pk_attn_args {
   void* start_event;
   void* stop_event;
   const int32_t* live_streams;
+  int64_t pos_stride_b; /* elements between streams' position tables; 0: one table for all */
 } pk_attn_args;
 int pk_paged_relpos_attn(const pk_attn_args* args, void* stream);
 

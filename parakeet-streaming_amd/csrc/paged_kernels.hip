@@ -74,6 +74,7 @@ struct AttnK {
   PagesK pg;
   const ST* pos;
   int64_t pos_sr;
+  int64_t pos_sb;  // per-stream tables (vector-ALU kernel only); 0: one shared table
   int32_t pos_rows;
   const ST* bu;
   const ST* bv;
@@ -222,7 +223,7 @@ __global__ void __launch_bounds__(64) relpos_attn_kernel(const AttnK<ST> p) {
 #pragma unroll
     for (int k = 0; k < NP; ++k) {
       const int r = min(max(rb + rl + k * RLW, 0), p.pos_rows - 1);
-      pr[k] = ld16(p.pos + r * p.pos_sr + col);
+      pr[k] = ld16(p.pos + b * p.pos_sb + r * p.pos_sr + col);
     }
     if (mask_mode == 1) {
       for (int x = lane; x < TQ * BLK; x += 64) {
@@ -1225,9 +1226,10 @@ int attn_typed(const pk_attn_args* a, hipStream_t s) {
   const void* ptrs[7] = {a->query, a->key, a->value, a->pos, a->bias_u, a->bias_v, a->out};
   for (const void* q : ptrs)
     if (!aligned16(q)) return fail(PK_ERR_INVALID, "%s: tensors must be 16-byte aligned", what);
-  const int64_t strides[9] = {a->query_stride_b, a->query_stride_t, a->key_stride_b,
-                              a->key_stride_t,   a->value_stride_b, a->value_stride_t,
-                              a->pos_stride,     a->out_stride_b,   a->out_stride_t};
+  const int64_t strides[10] = {a->query_stride_b, a->query_stride_t, a->key_stride_b,
+                               a->key_stride_t,   a->value_stride_b, a->value_stride_t,
+                               a->pos_stride,     a->out_stride_b,   a->out_stride_t,
+                               a->pos_stride_b};
   for (int64_t st : strides)
     if (st < 0 || st % VEC != 0)
       return fail(PK_ERR_INVALID, "%s: strides must be non-negative multiples of %d elements",
@@ -1261,6 +1263,7 @@ int attn_typed(const pk_attn_args* a, hipStream_t s) {
   }
   k.pos = static_cast<const ST*>(a->pos);
   k.pos_sr = a->pos_stride;
+  k.pos_sb = a->pos_stride_b;
   k.pos_rows = a->pos_rows;
   k.bu = static_cast<const ST*>(a->bias_u);
   k.bv = static_cast<const ST*>(a->bias_v);
@@ -1311,7 +1314,9 @@ int attn_typed(const pk_attn_args* a, hipStream_t s) {
                       row_bytes(a->value_stride_t) <= kMaxBufferStride &&
                       row_bytes(a->pos_stride) <= kMaxBufferStride &&
                       (!need_pages || k.pg.cb_shift == 5);  // 64-byte page column blocks
-    if (a->rows_per_lane == 0 && fits && a->chunk <= 16) {
+    // per-stream position tables take the vector-ALU kernel: the matrix-core
+    // kernel stages one table per workgroup for all of its streams
+    if (a->rows_per_lane == 0 && fits && a->chunk <= 16 && a->pos_stride_b == 0) {
       if (DK == 64) return launch_attn_mfma<ST, 64>(a, k, s);
       return launch_attn_mfma<ST, 128>(a, k, s);
     }

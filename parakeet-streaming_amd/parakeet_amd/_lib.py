@@ -123,6 +123,7 @@ class AttnArgs(ctypes.Structure):
         ("start_event", c_void_p),
         ("stop_event", c_void_p),
         ("live_streams", c_void_p),
+        ("pos_stride_b", c_int64),
     ]
 
 

@@ -76,10 +76,10 @@ class ConformerAttention(nn.Module):
         B, T = x.shape[:2]
         qkv = self.qkv(x)
         query, key, value = qkv.chunk(3, dim=-1)
+        # [1, P, D] is one table for every stream; [B, P, D] gives each stream
+        # its own (the reference broadcasts both, attention.py:102-106)
         pos = self.linear_pos(pos_emb)
-        if pos.dim() == 3:
-            if pos.shape[0] != 1:
-                raise NotImplementedError("a per-stream position table (pos_emb batch > 1) is not supported")
+        if pos.dim() == 3 and pos.shape[0] == 1:
             pos = pos[0]
         mask = attn_mask.bool() if attn_mask is not None else None
         bias_u = self.pos_bias_u.to(x.dtype).contiguous()

@@ -238,7 +238,9 @@ def paged_relpos_attn(
     parakeet/modules/attention.py:97-121; returns [B, T, D] before linear_out.
 
     query/key/value: [B, T, D] (views of the qkv projection are fine);
-    pos: [>= L + T - 1, D] (linear_pos of the sinusoid slice, batch dim dropped);
+    pos: [>= L + T - 1, D] (linear_pos of the sinusoid slice, batch dim dropped),
+    or [B, >= L + T - 1, D]: one table per stream (attention.py:102-106
+    broadcasts a pos_emb of batch B the same way);
     bias_u/bias_v: [H, dk]; mask: [B, T, L] / [B, 1|H, T, L] bool, True = masked.
     With ``mask`` None and ``mask_state`` given, the kernel evaluates the
     streaming mask from the stream state instead.
@@ -253,8 +255,18 @@ def paged_relpos_attn(
         raise ValueError(f"d_model {D} not divisible by {H} heads")
     dk = D // H
     Lk = int(left) + T
+    pos_sb = 0
+    if pos.dim() == 3:
+        if pos.shape[0] == 1:
+            pos = pos[0]
+        elif pos.shape[0] == B:
+            pos_sb = pos.stride(0)  # 0 for an expanded table: one table shared by all
+            pos = pos[0]
+        else:
+            raise ValueError(f"pos batch {pos.shape[0]} must be 1 or the query batch {B}")
     if pos.dim() != 2 or pos.shape[1] != D or pos.stride(1) != 1 or pos.dtype != dt:
-        raise ValueError(f"pos must be [rows, {D}] of {dt} with unit inner stride, got {tuple(pos.shape)} {pos.dtype}")
+        raise ValueError(f"pos must be [rows, {D}] or [B, rows, {D}] of {dt} with unit inner stride, "
+                         f"got {tuple(pos.shape)} {pos.dtype}")
     for name, bias in (("bias_u", bias_u), ("bias_v", bias_v)):
         if tuple(bias.shape) != (H, dk) or bias.dtype != dt or not bias.is_contiguous():
             raise ValueError(f"{name} must be contiguous [{H}, {dk}] of {dt}")
@@ -282,7 +294,7 @@ def paged_relpos_attn(
     a.query, a.query_stride_b, a.query_stride_t = query.data_ptr(), query.stride(0), query.stride(1)
     a.key, a.key_stride_b, a.key_stride_t = key.data_ptr(), key.stride(0), key.stride(1)
     a.value, a.value_stride_b, a.value_stride_t = value.data_ptr(), value.stride(0), value.stride(1)
-    a.pos, a.pos_stride, a.pos_rows = pos.data_ptr(), pos.stride(0), pos.shape[0]
+    a.pos, a.pos_stride, a.pos_rows, a.pos_stride_b = pos.data_ptr(), pos.stride(0), pos.shape[0], pos_sb
     a.bias_u, a.bias_v = bias_u.data_ptr(), bias_v.data_ptr()
     if mask is not None:
         mask, sb, sh, st = _mask_strides(mask, B, H, T, Lk)

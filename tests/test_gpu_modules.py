@@ -136,6 +136,52 @@ def test_conformer_attention_matches_oracle(cuda, dtype):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_conformer_attention_per_stream_position_tables(cuda, dtype):
+    """pos_emb of batch B: every stream attends with its own position table, as
+    the reference's broadcast of linear_pos(pos_emb) [B, P, H, dk] against the
+    queries does (attention.py:102-113); each stream is checked against the
+    oracle with its own table, through eviction."""
+    print(f"\n[conformer-attention per-stream pos] {dtype}", flush=True)
+    H, dk, left, right, B = 8, 64, 20, 1, 3
+    D, T = H * dk, right + 1
+    L = left + T
+    att = ConformerAttention(0, H, D)
+    _init_attention(att, D, seed=3)
+    att = att.to(device=cuda, dtype=dtype)
+    mc = ModelCache(1, (left, right), D, 9, batch_size=B, device=cuda, dtype=dtype, page_size=16)
+    win_k = np.zeros((B, 1, L, D))
+    win_v = np.zeros((B, 1, L, D))
+    proc = np.zeros(B, dtype=np.int64)
+    g = torch.Generator().manual_seed(4)
+    w_out = att.linear_out.weight.detach().double().cpu().numpy()
+    bu = att.pos_bias_u.detach().double().cpu().numpy()
+    bv = att.pos_bias_v.detach().double().cpu().numpy()
+    worst = 0.0
+    for step in range(14):
+        x = torch.randn(B, T, D, generator=g).to(dtype).to(cuda)
+        pos_emb = torch.randn(B, 2 * L - 1, D, generator=g).to(dtype).to(cuda)  # a different table per stream
+        cl = np.minimum(proc, left)
+        _, mask = om.create_streaming_masks(T, cl, proc, T, (left, right))
+        with torch.no_grad():
+            out = att(x, pos_emb, torch.from_numpy(mask).to(cuda), cache=mc)
+            q, k, v = (t.double().cpu().numpy() for t in att.qkv(x).chunk(3, dim=-1))
+            pos = att.linear_pos(pos_emb).double().cpu().numpy()
+        for b in range(B):
+            _dense_shift(win_k, b, 0, left, k[b])
+            _dense_shift(win_v, b, 0, left, v[b])
+        for b in range(B):
+            core = oa.relpos_attention(q[b : b + 1], win_k[b : b + 1, 0], win_v[b : b + 1, 0], pos[b], bu, bv,
+                                       mask[b : b + 1], H)
+            err = float(np.abs(out[b].double().cpu().numpy() - (core @ w_out.T)[0]).max())
+            worst = max(worst, err)
+            assert err <= ATT_TOL[dtype], f"step {step} stream {b}: max abs err {err:.3e}"
+        proc += T
+    print(f"  worst max-abs error {worst:.3e}", flush=True)
+    torch.cuda.synchronize()
+
+
+@pytest.mark.gpu
 def test_encoder_streaming_matches_dense_reference(cuda):
     print("\n[encoder] 2 layers fp32 vs float64 dense reference", flush=True)
     left, right, D, H, Ly, B, K = 6, 1, 128, 2, 2, 3, 9
