@@ -710,13 +710,428 @@ __global__ void __launch_bounds__(kSubThreads) subsample_kernel(const SubK<ST> p
   }
 }
 
+// ---------------------------------------------------------------------------
+// Convolution stack for the 16-bit types: NF output frames x QT output columns
+// of one stream per workgroup of 16 waves, so the frames of a stream share the
+// rows their receptive fields overlap in and each pointwise weight matrix is
+// read once per tile.  The channels run in groups of 32:
+//   conv.0 (1 -> 32 channels) on 16x16x16 MFMAs (taps 0..8 of each position
+//     with the bias on tap 9; a position outside the map has all-zero
+//     operands, so it comes out 0) -> ReLU -> a1g;
+//   the first depthwise conv of the group on dot2 instructions -> a2g;
+//   conv.3's product accumulated over the groups: one 16x16x32 k-step per
+//     group on the group's 32 input channels, the fp32 sums (started at the
+//     bias) held in the waves' accumulators (wave w: output channels
+//     16 (w mod C/16) ..);
+// then conv.3's mask, ReLU -> a2out (which zeroes every position outside the
+// map, so the first depthwise conv needs no mask of its own); the second
+// depthwise conv -> a3; conv.6 + bias, ReLU -> the output tile
+// [frame][channel][column].  Every layer's output is rounded to the storage
+// type (to nearest even), as in the stack above.
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef short s16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+template <typename ST>
+struct Mma16;
+template <>
+struct Mma16<_Float16> {
+  typedef _Float16 H4 __attribute__((ext_vector_type(4)));
+  __device__ static inline f32x4_t k16(s16x4_t a, s16x4_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(H4, a), __builtin_bit_cast(H4, b), c, 0, 0, 0);
+  }
+};
+template <>
+struct Mma16<bf16_t> {
+  __device__ static inline f32x4_t k16(s16x4_t a, s16x4_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+  }
+};
+
+typedef _Float16 h2x __attribute__((ext_vector_type(2)));
+typedef __bf16 b2x __attribute__((ext_vector_type(2)));
+// acc + a.lo * w.lo + a.hi * w.hi, two 16-bit pairs, fp32 accumulation
+template <typename ST>
+__device__ static inline float dot2(uint32_t a, uint32_t w, float acc);
+template <>
+__device__ inline float dot2<_Float16>(uint32_t a, uint32_t w, float acc) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2x, a), __builtin_bit_cast(h2x, w), acc, false);
+}
+template <>
+__device__ inline float dot2<bf16_t>(uint32_t a, uint32_t w, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2x, a), __builtin_bit_cast(b2x, w), acc, false);
+}
+// two fp32 values as two storage elements in one dword (lo = a), rounded to
+// nearest even by the packed conversion instructions
+template <typename ST>
+__device__ static inline uint32_t cvt2(float a, float b);
+template <>
+__device__ inline uint32_t cvt2<_Float16>(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, h2x));
+}
+template <>
+__device__ inline uint32_t cvt2<bf16_t>(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, b2x));
+}
+// ReLU of two packed fp16 or bf16 values: an element with its sign bit set is
+// a negative int16, so an int16 max with 0 clears it (-0 included)
+__device__ static inline uint32_t relu2(uint32_t v) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(s16x2_t, v), (s16x2_t){0, 0}));
+}
+// x.lo | y.lo << 16, and x.hi | y.hi << 16 (v_perm_b32 byte selects)
+__device__ static inline uint32_t lo2(uint32_t x, uint32_t y) { return __builtin_amdgcn_perm(y, x, 0x05040100u); }
+__device__ static inline uint32_t hi2(uint32_t x, uint32_t y) { return __builtin_amdgcn_perm(y, x, 0x07060302u); }
+
+constexpr int kSub2Waves = 16;
+constexpr int kSub2Threads = 64 * kSub2Waves;
+constexpr int kSub2CG = 32;  // channels per group: one k-step of conv.3
+
+// second depthwise conv weights in LDS: tap pair pp = (2 pp, 2 pp + 1) of
+// channel c as one dword (tap 9 is 0); channels c .. c + 3 of an 8-channel
+// chunk sit in one 16-byte run and c + 4 .. c + 7 in another, half a row on
+template <int C>
+__device__ static inline int w5_index(int pp, int c) {
+  return pp * C + ((c >> 2) & 1) * (C / 2) + (c >> 3) * 4 + (c & 3);
+}
+
+template <typename ST, int NF, int QT, int C>
+struct Sub2Geom {
+  static constexpr int VEC = 8;                                     // 16-bit elements per 16 bytes
+  static constexpr int XR = 8 * NF + 7, XC = 8 * QT + 7;             // input rows / cols of the tile
+  static constexpr int XN = (XR * XC + 7) / 8 * 8;
+  static constexpr int R2 = 2 * NF + 1, C2 = 2 * QT + 1, M2 = R2 * C2, T2 = (M2 + 15) / 16;  // after dw 1
+  static constexpr int JG = (C2 + 3) / 4;   // first depthwise conv: groups of 4 output columns
+  // after conv.0: rows of C1 columns stored C1P apart, so a row's 4-output group
+  // reads 9 columns from one 16-byte aligned chunk and the next dword
+  static constexpr int R1 = 4 * NF + 3, C1 = 4 * QT + 3, C1P = 8 * JG + 8;
+  static constexpr int M1 = R1 * C1P, T1 = (M1 + 15) / 16;
+  static constexpr int M1S = ((T1 * 2) | 1) * 8;  // a1g channel stride: 8 x odd elements (distinct banks)
+  static constexpr int M3 = NF * QT, T3 = (M3 + 15) / 16;                                   // after dw 2
+  static constexpr int GS = kSub2CG + VEC;  // a2g position stride (padded by 16 bytes)
+  static constexpr int RS = C + VEC;        // a2out / a3 position stride
+  static constexpr int NTL = C / 16;        // channel tiles of a pointwise conv
+  static constexpr int PG = kSub2Waves / NTL;  // waves per channel tile (position groups)
+  static constexpr int T1W = (T1 + kSub2Waves - 1) / kSub2Waves;
+  static constexpr int T2W = (T2 + PG - 1) / PG;
+  static constexpr int T3W = (T3 + PG - 1) / PG;
+  static constexpr int KS = C / 32;         // k-steps of a pointwise conv
+  static constexpr int P1 = XN + kSub2CG * M1S + T2 * 16 * GS;  // xin | a1g | a2g
+  static constexpr int P2 = T2 * 16 * RS + T3 * 16 * RS;       // a2out (output tile) | a3
+  static constexpr int REG = cmax<P1, P2>::v;
+  static_assert(NF * C * QT <= T2 * 16 * RS, "output tile fits over a2out");
+};
+
+template <typename ST, int NF, int QT, int C>
+__global__ void __launch_bounds__(kSub2Threads) subsample2_kernel(const SubK<ST> p) {
+  typedef Sub2Geom<ST, NF, QT, C> G;
+  constexpr int VEC = G::VEC;
+  static_assert(C % 64 == 0 && C / 16 <= kSub2Waves, "channels");
+  __shared__ __align__(16) ST reg[G::REG];
+  __shared__ __align__(16) ST w0p[C * 16];  // conv.0 [C][16]: taps 0..8, bias at 9, zeros
+  __shared__ __align__(16) uint32_t w2p[C][8];  // first depthwise conv per channel: rows kt (w0 w1 | w2 0)
+  __shared__ __align__(16) uint32_t w5p[5 * C];  // second depthwise conv by tap pairs (w5_index)
+  __shared__ __align__(16) float bsm[4][C];  // biases of conv.2/3/5/6, 0 where absent
+  ST* const xin = reg;
+  ST* const a1g = reg + G::XN;
+  ST* const a2g = a1g + kSub2CG * G::M1S;
+  ST* const a2o = reg;  // after the group loop
+  ST* const a3 = reg + G::T2 * 16 * G::RS;
+  ST* const ot = reg;   // after the second depthwise conv: [frame][C][qv]
+
+  const int b = blockIdx.z;
+  const pk_sub_stream s = p.streams[b];
+  const int j0 = blockIdx.x * NF;  // first output frame of the tile (of the kept frames)
+  const int n_keep = min(s.n_out, p.max_out);
+  if (j0 >= n_keep || s.slot < 0 || s.slot >= p.in_slots || s.rows < 0 || s.length < 0 || s.length > s.rows ||
+      s.drop < 0 || s.out_row < 0 || s.out_row + s.n_out > p.out_rows)
+    return;
+  if (!p.in_ring && (s.row0 < 0 || (int64_t)s.row0 + s.rows > p.in_rows)) return;
+  const int t0 = s.drop + j0;  // its frame of the stack
+  const int L3 = half_up(half_up(half_up(s.rows)));
+  const int nf = min(NF, min(n_keep - j0, L3 - t0));  // frames the tile writes
+  if (nf <= 0) return;
+  const int F = p.F;
+  const int F1 = half_up(F), F2 = half_up(F1), F3 = half_up(F2);
+  const int p0 = blockIdx.y * QT;
+  if (p0 >= F3) return;
+  const int qv = min(QT, F3 - p0);
+  const int len1 = half_up(s.length), len2 = half_up(len1), len3 = half_up(len2);
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int nt = wave % G::NTL, pg = wave / G::NTL;  // the wave's pointwise channel tile and position group
+  const int c3 = nt * 16 + 4 * lg;                    // the lane's 4 output channels of conv.3 and conv.6
+
+  // ---- weights, biases and the input tile, every global load issued before
+  //      the first LDS store (one round trip): the 3x3 weights as 16-byte
+  //      chunks of their [C][9] arrays, the input rows >= length and the
+  //      padding as zeros
+  constexpr int kWCh = 9 * C / VEC;                                   // 16-byte chunks of a [C][9] array
+  constexpr int kWPer = (kWCh + kSub2Threads - 1) / kSub2Threads;
+  constexpr int kXPer = (G::XN + kSub2Threads - 1) / kSub2Threads;
+  u32x4 w0c[kWPer], w2c[kWPer], w5c[kWPer];
+#pragma unroll
+  for (int u = 0; u < kWPer; ++u) {
+    const int ch = min(tid + u * kSub2Threads, kWCh - 1);
+    w0c[u] = ld16(p.w0 + ch * VEC);
+    w2c[u] = ld16(p.w2 + ch * VEC);
+    w5c[u] = ld16(p.w5 + ch * VEC);
+  }
+  float bias[5] = {0.f, 0.f, 0.f, 0.f, 0.f};  // conv.0/2/3/5/6 of channel tid
+  if (tid < C) {
+    const ST* bp[5] = {p.b0, p.b2, p.b3, p.b5, p.b6};
+#pragma unroll
+    for (int k = 0; k < 5; ++k)
+      if (bp[k]) bias[k] = from_st(bp[k][tid]);
+  }
+  float xr[kXPer];
+  {
+    const int r0 = 8 * t0 - 14, c0 = 8 * p0 - 14;
+    const float* inb = p.in + (int64_t)s.slot * p.in_rows * F;
+    const int rmask = p.in_rows - 1;
+#pragma unroll
+    for (int u = 0; u < kXPer; ++u) {
+      const int i = tid + u * kSub2Threads;
+      const int rr = i / G::XC, cc = i - rr * G::XC;
+      const int gr = r0 + rr, gc = c0 + cc;
+      const bool ok = i < G::XR * G::XC && gr >= 0 && gr < s.length && gc >= 0 && gc < F;
+      const int row = p.in_ring ? ((s.row0 + gr) & rmask) : s.row0 + gr;
+      const float v = inb[ok ? (int64_t)row * F + gc : 0];
+      xr[u] = ok ? v : 0.f;
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kWPer; ++u) {
+    const int ch = tid + u * kSub2Threads;
+    if (ch < kWCh) {
+      const Chunk<ST> a = __builtin_bit_cast(Chunk<ST>, w0c[u]);
+      const Chunk<ST> b2 = __builtin_bit_cast(Chunk<ST>, w2c[u]);
+      const Chunk<ST> b5 = __builtin_bit_cast(Chunk<ST>, w5c[u]);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const int i = ch * VEC + e, c = i / 9, k = i - c * 9;
+        const int kt = k / 3, kf = k - kt * 3;
+        w0p[c * 16 + k] = a.v[e];
+        // tap kf of row kt: half kf & 1 of dword 2 kt + kf / 2 (taps 0, 1 | 2, 0)
+        reinterpret_cast<ST*>(&w2p[c][2 * kt + kf / 2])[kf & 1] = b2.v[e];
+        reinterpret_cast<ST*>(&w5p[w5_index<C>(k >> 1, c)])[k & 1] = b5.v[e];
+      }
+    }
+  }
+  if (tid < C) {
+#pragma unroll
+    for (int kt = 0; kt < 3; ++kt) reinterpret_cast<ST*>(&w2p[tid][2 * kt + 1])[1] = to_st<ST>(0.f);
+    reinterpret_cast<ST*>(&w5p[w5_index<C>(4, tid)])[1] = to_st<ST>(0.f);
+    w0p[tid * 16 + 9] = to_st<ST>(bias[0]);  // the bias rides on a tap that reads 1
+#pragma unroll
+    for (int k = 10; k < 16; ++k) w0p[tid * 16 + k] = to_st<ST>(0.f);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) bsm[k][tid] = bias[k + 1];
+  }
+#pragma unroll
+  for (int u = 0; u < kXPer; ++u) {
+    const int i = tid + u * kSub2Threads;
+    if (i < G::XN) xin[i] = to_st<ST>(xr[u]);
+  }
+  // conv.3's weight k-step for the first group: lane holds W3[n][g + 8 lg ..]
+  // for the wave's channel tile (each group's step loads during the previous one)
+  const ST* const w3row = p.w3 + (int64_t)(nt * 16 + lr) * C + VEC * lg;
+  u32x4 wk = ld16(w3row);
+  __syncthreads();
+
+  // ---- conv.0 A operands, per wave its position tiles wave + 16 u: lane
+  //      (lr, lg) holds taps 4 lg .. 4 lg + 3 of position 16 mt + lr (tap 9
+  //      reads 1, taps 10.. read 0), all zero for a position outside the map
+  int toff[4];
+  short tval[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int tap = 4 * lg + e;
+    toff[e] = tap < 9 ? (tap / 3) * G::XC + tap % 3 : 0;
+    tval[e] = tap < 9 ? -1 : __builtin_bit_cast(short, to_st<ST>(tap == 9 ? 1.f : 0.f));
+  }
+  s16x4_t xop[G::T1W];
+#pragma unroll
+  for (int u = 0; u < G::T1W; ++u) {
+    const int m = (wave + kSub2Waves * u) * 16 + lr;
+    const int mm = min(m, G::M1 - 1);
+    const int i1 = mm / G::C1P, qr = mm - i1 * G::C1P, q1 = min(qr, G::C1 - 1);
+    const int r1 = 4 * t0 - 6 + i1, c1 = 4 * p0 - 6 + qr;
+    const bool ok = m < G::M1 && qr < G::C1 && r1 >= 0 && r1 < len1 && c1 >= 0 && c1 < F1;
+    const ST* const x = &xin[2 * i1 * G::XC + 2 * q1];
+    short v[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const short t = __builtin_bit_cast(short, x[toff[e]]);
+      v[e] = ok ? (4 * lg + e < 9 ? t : tval[e]) : short(0);
+    }
+    xop[u] = s16x4_t{v[0], v[1], v[2], v[3]};
+  }
+
+  f32x4_t acc[G::T2W];
+  {
+    const float4 b3 = *reinterpret_cast<const float4*>(&bsm[1][c3]);
+#pragma unroll
+    for (int u = 0; u < G::T2W; ++u) acc[u] = f32x4_t{b3.x, b3.y, b3.z, b3.w};
+  }
+
+#pragma unroll 1
+  for (int g = 0; g < C; g += kSub2CG) {
+    // conv.0 for channels g .. g + 31 -> a1g [channel][position]: D rows are
+    // positions, so a lane holds 4 consecutive positions of one channel
+    s16x4_t wop[2];
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) wop[ct] = *reinterpret_cast<const s16x4_t*>(&w0p[(g + ct * 16 + lr) * 16 + 4 * lg]);
+#pragma unroll
+    for (int u = 0; u < G::T1W; ++u) {
+      const int mt = wave + kSub2Waves * u;
+      if (mt < G::T1) {
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+          const f32x4_t d = Mma16<ST>::k16(xop[u], wop[ct], f32x4_t{0.f, 0.f, 0.f, 0.f});
+          *reinterpret_cast<uint2*>(&a1g[(ct * 16 + lr) * G::M1S + mt * 16 + 4 * lg]) =
+              make_uint2(relu2(cvt2<ST>(d[0], d[1])), relu2(cvt2<ST>(d[2], d[3])));
+        }
+      }
+    }
+    __syncthreads();
+    // first depthwise conv of the group -> a2g [position][32]: a thread takes
+    // one channel and 4 adjacent output columns of one output row; per input
+    // row, 9 columns come from one 16-byte chunk and the next dword, and each
+    // tap pair is one fp32-accumulating dot2 (w0 w1 | w2 0)
+    for (int it = tid; it < kSub2CG * G::R2 * G::JG; it += kSub2Threads) {
+      const int c = it % kSub2CG, rest = it / kSub2CG;
+      const int i2 = rest % G::R2, jg = rest / G::R2;
+      const u32x4 wa = *reinterpret_cast<const u32x4*>(&w2p[g + c][0]);
+      const u32x4 wb = *reinterpret_cast<const u32x4*>(&w2p[g + c][4]);
+      const uint32_t wr[6] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y};
+      const float bv = bsm[0][g + c];
+      float o[4] = {bv, bv, bv, bv};
+#pragma unroll
+      for (int kt = 0; kt < 3; ++kt) {
+        const ST* row = &a1g[c * G::M1S + (2 * i2 + kt) * G::C1P + 8 * jg];
+        const u32x4 q = *reinterpret_cast<const u32x4*>(row);
+        const uint32_t d[5] = {q.x, q.y, q.z, q.w, *reinterpret_cast<const uint32_t*>(row + 8)};
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) o[jj] = dot2<ST>(d[jj + 1], wr[2 * kt + 1], dot2<ST>(d[jj], wr[2 * kt], o[jj]));
+      }
+      const uint32_t p01 = cvt2<ST>(o[0], o[1]), p23 = cvt2<ST>(o[2], o[3]);
+      const uint16_t h[4] = {(uint16_t)p01, (uint16_t)(p01 >> 16), (uint16_t)p23, (uint16_t)(p23 >> 16)};
+      uint16_t* const dst = reinterpret_cast<uint16_t*>(&a2g[(i2 * G::C2 + 4 * jg) * G::GS + c]);
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+        if (4 * jg + jj < G::C2) dst[jj * G::GS] = h[jj];
+    }
+    __syncthreads();
+    // conv.3: one k-step over the group's 32 input channels
+#pragma unroll
+    for (int u = 0; u < G::T2W; ++u) {
+      const int mt = pg + G::PG * u;
+      if (mt < G::T2) {
+        const u32x4 x = *reinterpret_cast<const u32x4*>(&a2g[(mt * 16 + lr) * G::GS + VEC * lg]);
+        acc[u] = MmaK<ST>::step(wk, x, acc[u]);
+      }
+    }
+    if (g + kSub2CG < C) wk = ld16(w3row + g + kSub2CG);
+    __syncthreads();  // the next group rewrites a1g / a2g
+  }
+
+  // ---- conv.3 mask, ReLU -> a2out [position][C] (over the group buffers)
+#pragma unroll
+  for (int u = 0; u < G::T2W; ++u) {
+    const int mt = pg + G::PG * u;
+    if (mt < G::T2) {
+      const int m = mt * 16 + lr;
+      const int i2 = m / G::C2, q2 = m - i2 * G::C2;
+      const int r2 = 2 * t0 - 2 + i2, c2 = 2 * p0 - 2 + q2;
+      const bool ok = m < G::M2 && r2 >= 0 && r2 < len2 && c2 >= 0 && c2 < F2;
+      const uint2 v = make_uint2(relu2(cvt2<ST>(acc[u][0], acc[u][1])), relu2(cvt2<ST>(acc[u][2], acc[u][3])));
+      *reinterpret_cast<uint2*>(&a2o[m * G::RS + c3]) = ok ? v : make_uint2(0u, 0u);
+    }
+  }
+  // conv.6's weights for the wave's channel tile load while the second
+  // depthwise conv runs
+  u32x4 w6q[G::KS];
+#pragma unroll
+  for (int kk = 0; kk < G::KS; ++kk) w6q[kk] = ld16(p.w6 + (int64_t)(nt * 16 + lr) * C + VEC * lg + kk * 32);
+  __syncthreads();
+
+  // ---- second depthwise conv -> a3 [frame * QT + column][C], masked: a thread
+  //      takes 8 channels of one position; per tap pair, the two taps' values
+  //      of a channel are gathered into one dword (v_perm) for a dot2
+  for (int it = tid; it < G::T3 * 16 * (C / VEC); it += kSub2Threads) {
+    const int m3 = it / (C / VEC), cc = (it - m3 * (C / VEC)) * VEC;
+    const int f = min(m3 / QT, NF - 1), q = m3 - (m3 / QT) * QT;
+    float sum[VEC];
+    {
+      const float4 x = *reinterpret_cast<const float4*>(&bsm[2][cc]);
+      const float4 y = *reinterpret_cast<const float4*>(&bsm[2][cc + 4]);
+      sum[0] = x.x, sum[1] = x.y, sum[2] = x.z, sum[3] = x.w;
+      sum[4] = y.x, sum[5] = y.y, sum[6] = y.z, sum[7] = y.w;
+    }
+    const ST* const src = &a2o[(2 * f * G::C2 + 2 * q) * G::RS + cc];
+#pragma unroll
+    for (int pp = 0; pp < 5; ++pp) {
+      const int ta = 2 * pp, tb = 2 * pp + 1;
+      const u32x4 A = ld16(src + ((ta / 3) * G::C2 + ta % 3) * G::RS);
+      const u32x4 B = tb < 9 ? ld16(src + ((tb / 3) * G::C2 + tb % 3) * G::RS) : u32x4{0u, 0u, 0u, 0u};
+      const u32x4 W0 = *reinterpret_cast<const u32x4*>(&w5p[w5_index<C>(pp, cc)]);
+      const u32x4 W1 = *reinterpret_cast<const u32x4*>(&w5p[w5_index<C>(pp, cc + 4)]);
+      const uint32_t a[4] = {A.x, A.y, A.z, A.w}, bb[4] = {B.x, B.y, B.z, B.w};
+      const uint32_t w[8] = {W0.x, W0.y, W0.z, W0.w, W1.x, W1.y, W1.z, W1.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        sum[2 * e] = dot2<ST>(lo2(a[e], bb[e]), w[2 * e], sum[2 * e]);
+        sum[2 * e + 1] = dot2<ST>(hi2(a[e], bb[e]), w[2 * e + 1], sum[2 * e + 1]);
+      }
+    }
+    const bool ok = m3 < G::M3 && t0 + f < len3;
+    const u32x4 o = {cvt2<ST>(sum[0], sum[1]), cvt2<ST>(sum[2], sum[3]), cvt2<ST>(sum[4], sum[5]),
+                     cvt2<ST>(sum[6], sum[7])};
+    *reinterpret_cast<u32x4*>(&a3[m3 * G::RS + cc]) = ok ? o : u32x4{0u, 0u, 0u, 0u};
+  }
+  __syncthreads();
+
+  // ---- conv.6 + bias, ReLU, mask -> output tile [frame][channel][qv columns] (over a2out)
+#pragma unroll
+  for (int u = 0; u < G::T3W; ++u) {
+    const int mt = pg + G::PG * u;
+    if (mt < G::T3) {
+      f32x4_t d = *reinterpret_cast<const f32x4_t*>(&bsm[3][c3]);
+#pragma unroll
+      for (int kk = 0; kk < G::KS; ++kk) {
+        const u32x4 x = *reinterpret_cast<const u32x4*>(&a3[(mt * 16 + lr) * G::RS + kk * 32 + VEC * lg]);
+        d = MmaK<ST>::step(w6q[kk], x, d);
+      }
+      const int m3 = mt * 16 + lr;
+      const int f = m3 / QT, q = m3 - f * QT;
+      if (m3 < G::M3 && q < qv) {
+        const bool ok = t0 + f < len3;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ot[(f * C + c3 + e) * qv + q] = to_st<ST>(ok ? fmaxf(d[e], 0.f) : 0.f);
+      }
+    }
+  }
+  __syncthreads();
+  ST* const out = p.out + (int64_t)(s.out_row + j0) * C * F3;
+  if (qv == F3 && (reinterpret_cast<uintptr_t>(p.out) & 15) == 0) {
+    // the tile spans every column: its nf frames of [C][F3] are one run
+    for (int i = tid * VEC; i < nf * C * F3; i += kSub2Threads * VEC) st16(out + i, ld16(ot + i));
+  } else {
+    for (int f = 0; f < nf; ++f)
+      for (int i = tid; i < C * qv; i += kSub2Threads) {
+        const int c = i / qv, q = i - c * qv;
+        out[(int64_t)f * C * F3 + c * F3 + p0 + q] = ot[f * C * qv + i];
+      }
+  }
+}
+
 // ===========================================================================
 // host side
 
 static bool pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
 
-template <typename ST, int QT, int C>
-static int launch_sub(const pk_sub_args* a, hipStream_t st) {
+template <typename ST>
+static SubK<ST> sub_args(const pk_sub_args* a, int C) {
   SubK<ST> k;
   k.streams = a->streams;
   k.in = a->feats;
@@ -738,6 +1153,13 @@ static int launch_sub(const pk_sub_args* a, hipStream_t st) {
   k.C = C;
   k.out_rows = a->out_rows;
   k.max_out = a->max_out;
+  return k;
+}
+
+// fp32: one output frame x QT columns per workgroup
+template <typename ST, int QT, int C>
+static int launch_sub(const pk_sub_args* a, hipStream_t st) {
+  const SubK<ST> k = sub_args<ST>(a, C);
   const int F3 = half_up(half_up(half_up(a->n_mels)));
   const dim3 grid(a->max_out, (F3 + QT - 1) / QT, a->batch);
   hipLaunchKernelGGL((subsample_kernel<ST, QT, C>), grid, dim3(kSubThreads), 0, st, k);
@@ -753,6 +1175,30 @@ static int launch_sub_c(const pk_sub_args* a, hipStream_t st) {
       return launch_sub<ST, QT, 128>(a, st);
     default:
       return launch_sub<ST, QT, 256>(a, st);
+  }
+}
+
+// fp16 / bf16: two output frames x QT columns per workgroup of 16 waves
+constexpr int kSub2Frames = 2;
+
+template <typename ST, int QT, int C>
+static int launch_sub2(const pk_sub_args* a, hipStream_t st) {
+  const SubK<ST> k = sub_args<ST>(a, C);
+  const int F3 = half_up(half_up(half_up(a->n_mels)));
+  const dim3 grid((a->max_out + kSub2Frames - 1) / kSub2Frames, (F3 + QT - 1) / QT, a->batch);
+  hipLaunchKernelGGL((subsample2_kernel<ST, kSub2Frames, QT, C>), grid, dim3(kSub2Threads), 0, st, k);
+  return check_launch("pk_subsample");
+}
+
+template <typename ST, int QT>
+static int launch_sub2_c(const pk_sub_args* a, hipStream_t st) {
+  switch (a->channels) {
+    case 64:
+      return launch_sub2<ST, QT, 64>(a, st);
+    case 128:
+      return launch_sub2<ST, QT, 128>(a, st);
+    default:
+      return launch_sub2<ST, QT, 256>(a, st);
   }
 }
 
@@ -848,9 +1294,9 @@ extern "C" int pk_subsample(const pk_sub_args* a, void* stream) {
   const int F3 = half_up(half_up(half_up(a->n_mels)));
   switch (a->dtype) {
     case PK_DTYPE_F16:
-      return F3 <= 11 ? launch_sub_c<_Float16, 11>(a, st) : launch_sub_c<_Float16, 9>(a, st);
+      return F3 <= 11 ? launch_sub2_c<_Float16, 11>(a, st) : launch_sub2_c<_Float16, 17>(a, st);
     case PK_DTYPE_BF16:
-      return F3 <= 11 ? launch_sub_c<bf16_t, 11>(a, st) : launch_sub_c<bf16_t, 9>(a, st);
+      return F3 <= 11 ? launch_sub2_c<bf16_t, 11>(a, st) : launch_sub2_c<bf16_t, 17>(a, st);
     default:
       return launch_sub_c<float, 6>(a, st);
   }
