@@ -786,6 +786,13 @@ constexpr int kSub2Waves = 16;
 constexpr int kSub2Threads = 64 * kSub2Waves;
 constexpr int kSub2CG = 32;  // channels per group: one k-step of conv.3
 
+// conv.0 weights in LDS as the MFMA B operand: tap k of channel c at lane
+// (c mod 16, k / 4) of channel tile c / 16, 4 taps a lane, so the 16 lanes of
+// one LDS pass read consecutive 8-byte runs
+__device__ static inline int w0_index(int c, int k) {
+  return (((c >> 4) * 4 + (k >> 2)) * 16 + (c & 15)) * 4 + (k & 3);
+}
+
 // second depthwise conv weights in LDS: tap pair pp = (2 pp, 2 pp + 1) of
 // channel c as one dword (tap 9 is 0); channels c .. c + 3 of an 8-channel
 // chunk sit in one 16-byte run and c + 4 .. c + 7 in another, half a row on
@@ -812,12 +819,18 @@ struct Sub2Geom {
   static constexpr int NTL = C / 16;        // channel tiles of a pointwise conv
   static constexpr int PG = kSub2Waves / NTL;  // waves per channel tile (position groups)
   static constexpr int T1W = (T1 + kSub2Waves - 1) / kSub2Waves;
-  static constexpr int T2W = (T2 + PG - 1) / PG;
+  // conv.3: a wave takes channel tiles 2 (w mod NP), 2 (w mod NP) + 1 and
+  // position tiles w / NP + P3 u, so each wave reads half the positions' rows
+  static constexpr int NP = C / 32, P3 = kSub2Waves / NP, T2W = (T2 + P3 - 1) / P3;
   static constexpr int T3W = (T3 + PG - 1) / PG;
   static constexpr int KS = C / 32;         // k-steps of a pointwise conv
-  static constexpr int P1 = XN + kSub2CG * M1S + T2 * 16 * GS;  // xin | a1g | a2g
+  static constexpr int A1N = kSub2CG * M1S, A2N = T2 * 16 * GS;  // the a1g / a2g buffers
+  static constexpr int P1 = XN + A1N + A2N;                        // xin | a1g | a2g
   static constexpr int P2 = T2 * 16 * RS + T3 * 16 * RS;       // a2out (output tile) | a3
   static constexpr int REG = cmax<P1, P2>::v;
+  // LDS of the kernel: reg, w0p, w2p, w5p, bsm
+  static constexpr int LDS_BYTES = REG * 2 + C * 16 * 2 + C * 32 + 5 * C * 4 + 4 * C * 4;
+  static constexpr bool FITS = LDS_BYTES <= 160 * 1024;
   static_assert(NF * C * QT <= T2 * 16 * RS, "output tile fits over a2out");
 };
 
@@ -827,13 +840,15 @@ __global__ void __launch_bounds__(kSub2Threads) subsample2_kernel(const SubK<ST>
   constexpr int VEC = G::VEC;
   static_assert(C % 64 == 0 && C / 16 <= kSub2Waves, "channels");
   __shared__ __align__(16) ST reg[G::REG];
-  __shared__ __align__(16) ST w0p[C * 16];  // conv.0 [C][16]: taps 0..8, bias at 9, zeros
-  __shared__ __align__(16) uint32_t w2p[C][8];  // first depthwise conv per channel: rows kt (w0 w1 | w2 0)
+  __shared__ __align__(16) ST w0p[C * 16];  // conv.0 (w0_index): taps 0..8, bias at 9, zeros
+  // first depthwise conv: dword d of channel c at [d / 4][c][d % 4], rows kt as
+  // dwords 2 kt (w0 w1) and 2 kt + 1 (w2 0)
+  __shared__ __align__(16) uint32_t w2p[2][C][4];
   __shared__ __align__(16) uint32_t w5p[5 * C];  // second depthwise conv by tap pairs (w5_index)
   __shared__ __align__(16) float bsm[4][C];  // biases of conv.2/3/5/6, 0 where absent
   ST* const xin = reg;
   ST* const a1g = reg + G::XN;
-  ST* const a2g = a1g + kSub2CG * G::M1S;
+  ST* const a2g = a1g + G::A1N;
   ST* const a2o = reg;  // after the group loop
   ST* const a3 = reg + G::T2 * 16 * G::RS;
   ST* const ot = reg;   // after the second depthwise conv: [frame][C][qv]
@@ -858,8 +873,9 @@ __global__ void __launch_bounds__(kSub2Threads) subsample2_kernel(const SubK<ST>
   const int len1 = half_up(s.length), len2 = half_up(len1), len3 = half_up(len2);
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int lr = lane & 15, lg = lane >> 4;
-  const int nt = wave % G::NTL, pg = wave / G::NTL;  // the wave's pointwise channel tile and position group
-  const int c3 = nt * 16 + 4 * lg;                    // the lane's 4 output channels of conv.3 and conv.6
+  const int nt = wave % G::NTL, pg = wave / G::NTL;  // the wave's conv.6 channel tile and position group
+  const int c3 = nt * 16 + 4 * lg;                    // the lane's 4 output channels of conv.6
+  const int np = wave % G::NP, pg3 = wave / G::NP;    // the wave's conv.3 channel tile pair and position group
 
   // ---- weights, biases and the input tile, every global load issued before
   //      the first LDS store (one round trip): the 3x3 weights as 16-byte
@@ -910,20 +926,21 @@ __global__ void __launch_bounds__(kSub2Threads) subsample2_kernel(const SubK<ST>
       for (int e = 0; e < VEC; ++e) {
         const int i = ch * VEC + e, c = i / 9, k = i - c * 9;
         const int kt = k / 3, kf = k - kt * 3;
-        w0p[c * 16 + k] = a.v[e];
+        w0p[w0_index(c, k)] = a.v[e];
         // tap kf of row kt: half kf & 1 of dword 2 kt + kf / 2 (taps 0, 1 | 2, 0)
-        reinterpret_cast<ST*>(&w2p[c][2 * kt + kf / 2])[kf & 1] = b2.v[e];
+        const int d = 2 * kt + kf / 2;
+        reinterpret_cast<ST*>(&w2p[d >> 2][c][d & 3])[kf & 1] = b2.v[e];
         reinterpret_cast<ST*>(&w5p[w5_index<C>(k >> 1, c)])[k & 1] = b5.v[e];
       }
     }
   }
   if (tid < C) {
 #pragma unroll
-    for (int kt = 0; kt < 3; ++kt) reinterpret_cast<ST*>(&w2p[tid][2 * kt + 1])[1] = to_st<ST>(0.f);
+    for (int kt = 0; kt < 3; ++kt) reinterpret_cast<ST*>(&w2p[(2 * kt + 1) >> 2][tid][(2 * kt + 1) & 3])[1] = to_st<ST>(0.f);
     reinterpret_cast<ST*>(&w5p[w5_index<C>(4, tid)])[1] = to_st<ST>(0.f);
-    w0p[tid * 16 + 9] = to_st<ST>(bias[0]);  // the bias rides on a tap that reads 1
+    w0p[w0_index(tid, 9)] = to_st<ST>(bias[0]);  // the bias rides on a tap that reads 1
 #pragma unroll
-    for (int k = 10; k < 16; ++k) w0p[tid * 16 + k] = to_st<ST>(0.f);
+    for (int k = 10; k < 16; ++k) w0p[w0_index(tid, k)] = to_st<ST>(0.f);
 #pragma unroll
     for (int k = 0; k < 4; ++k) bsm[k][tid] = bias[k + 1];
   }
@@ -934,8 +951,13 @@ __global__ void __launch_bounds__(kSub2Threads) subsample2_kernel(const SubK<ST>
   }
   // conv.3's weight k-step for the first group: lane holds W3[n][g + 8 lg ..]
   // for the wave's channel tile (each group's step loads during the previous one)
-  const ST* const w3row = p.w3 + (int64_t)(nt * 16 + lr) * C + VEC * lg;
-  u32x4 wk = ld16(w3row);
+  const ST* w3row[2];
+  u32x4 wk[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    w3row[h] = p.w3 + (int64_t)((2 * np + h) * 16 + lr) * C + VEC * lg;
+    wk[h] = ld16(w3row[h]);
+  }
   __syncthreads();
 
   // ---- conv.0 A operands, per wave its position tiles wave + 16 u: lane
@@ -967,20 +989,20 @@ __global__ void __launch_bounds__(kSub2Threads) subsample2_kernel(const SubK<ST>
     xop[u] = s16x4_t{v[0], v[1], v[2], v[3]};
   }
 
-  f32x4_t acc[G::T2W];
-  {
-    const float4 b3 = *reinterpret_cast<const float4*>(&bsm[1][c3]);
+  f32x4_t acc[G::T2W][2];  // conv.3 sums, started at the bias
 #pragma unroll
-    for (int u = 0; u < G::T2W; ++u) acc[u] = f32x4_t{b3.x, b3.y, b3.z, b3.w};
+  for (int h = 0; h < 2; ++h) {
+    const float4 b3 = *reinterpret_cast<const float4*>(&bsm[1][(2 * np + h) * 16 + 4 * lg]);
+#pragma unroll
+    for (int u = 0; u < G::T2W; ++u) acc[u][h] = f32x4_t{b3.x, b3.y, b3.z, b3.w};
   }
 
-#pragma unroll 1
-  for (int g = 0; g < C; g += kSub2CG) {
-    // conv.0 for channels g .. g + 31 -> a1g [channel][position]: D rows are
-    // positions, so a lane holds 4 consecutive positions of one channel
+  // conv.0 for channels g .. g + 31 -> a1 [channel][position]: D rows are
+  // positions, so a lane holds 4 consecutive positions of one channel
+  auto conv0 = [&](int g, ST* a1) {
     s16x4_t wop[2];
 #pragma unroll
-    for (int ct = 0; ct < 2; ++ct) wop[ct] = *reinterpret_cast<const s16x4_t*>(&w0p[(g + ct * 16 + lr) * 16 + 4 * lg]);
+    for (int ct = 0; ct < 2; ++ct) wop[ct] = *reinterpret_cast<const s16x4_t*>(&w0p[w0_index(g + ct * 16 + lr, 4 * lg)]);
 #pragma unroll
     for (int u = 0; u < G::T1W; ++u) {
       const int mt = wave + kSub2Waves * u;
@@ -988,64 +1010,93 @@ __global__ void __launch_bounds__(kSub2Threads) subsample2_kernel(const SubK<ST>
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) {
           const f32x4_t d = Mma16<ST>::k16(xop[u], wop[ct], f32x4_t{0.f, 0.f, 0.f, 0.f});
-          *reinterpret_cast<uint2*>(&a1g[(ct * 16 + lr) * G::M1S + mt * 16 + 4 * lg]) =
+          *reinterpret_cast<uint2*>(&a1[(ct * 16 + lr) * G::M1S + mt * 16 + 4 * lg]) =
               make_uint2(relu2(cvt2<ST>(d[0], d[1])), relu2(cvt2<ST>(d[2], d[3])));
         }
       }
     }
-    __syncthreads();
-    // first depthwise conv of the group -> a2g [position][32]: a thread takes
-    // one channel and 4 adjacent output columns of one output row; per input
-    // row, 9 columns come from one 16-byte chunk and the next dword, and each
-    // tap pair is one fp32-accumulating dot2 (w0 w1 | w2 0)
+  };
+  // first depthwise conv of channels g .. g + 31 -> a2 [position][32]: a
+  // thread takes one channel and 4 adjacent output columns of one output row;
+  // per input row, 9 columns come from a 16-byte chunk and the next one's
+  // first dword (that chunk read whole where registers allow: a 16-byte LDS
+  // read of 16 channels' rows is conflict free, a 4-byte one at this stride
+  // is not), and each tap pair is one fp32-accumulating dot2 (w0 w1 | w2 0)
+  auto dwconv1 = [&](int g, const ST* a1, ST* a2) {
     for (int it = tid; it < kSub2CG * G::R2 * G::JG; it += kSub2Threads) {
       const int c = it % kSub2CG, rest = it / kSub2CG;
       const int i2 = rest % G::R2, jg = rest / G::R2;
-      const u32x4 wa = *reinterpret_cast<const u32x4*>(&w2p[g + c][0]);
-      const u32x4 wb = *reinterpret_cast<const u32x4*>(&w2p[g + c][4]);
+      const u32x4 wa = *reinterpret_cast<const u32x4*>(&w2p[0][g + c][0]);
+      const u32x4 wb = *reinterpret_cast<const u32x4*>(&w2p[1][g + c][0]);
       const uint32_t wr[6] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y};
       const float bv = bsm[0][g + c];
       float o[4] = {bv, bv, bv, bv};
 #pragma unroll
       for (int kt = 0; kt < 3; ++kt) {
-        const ST* row = &a1g[c * G::M1S + (2 * i2 + kt) * G::C1P + 8 * jg];
+        const ST* row = &a1[c * G::M1S + (2 * i2 + kt) * G::C1P + 8 * jg];
         const u32x4 q = *reinterpret_cast<const u32x4*>(row);
-        const uint32_t d[5] = {q.x, q.y, q.z, q.w, *reinterpret_cast<const uint32_t*>(row + 8)};
+        uint32_t d4;
+        if constexpr (G::T2W * 2 <= 8) {
+          const u32x4 q2 = *reinterpret_cast<const u32x4*>(row + 8);
+          asm volatile("" ::"v"(q2.y), "v"(q2.z), "v"(q2.w));  // keep the read 16 bytes wide
+          d4 = q2.x;
+        } else {  // no registers to spare beside the conv.3 accumulators
+          d4 = *reinterpret_cast<const uint32_t*>(row + 8);
+        }
+        const uint32_t d[5] = {q.x, q.y, q.z, q.w, d4};
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) o[jj] = dot2<ST>(d[jj + 1], wr[2 * kt + 1], dot2<ST>(d[jj], wr[2 * kt], o[jj]));
       }
       const uint32_t p01 = cvt2<ST>(o[0], o[1]), p23 = cvt2<ST>(o[2], o[3]);
       const uint16_t h[4] = {(uint16_t)p01, (uint16_t)(p01 >> 16), (uint16_t)p23, (uint16_t)(p23 >> 16)};
-      uint16_t* const dst = reinterpret_cast<uint16_t*>(&a2g[(i2 * G::C2 + 4 * jg) * G::GS + c]);
+      uint16_t* const dst = reinterpret_cast<uint16_t*>(&a2[(i2 * G::C2 + 4 * jg) * G::GS + c]);
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj)
         if (4 * jg + jj < G::C2) dst[jj * G::GS] = h[jj];
     }
-    __syncthreads();
-    // conv.3: one k-step over the group's 32 input channels
+  };
+  // conv.3: one k-step over a group's 32 input channels (weights in wk) for
+  // the wave's two channel tiles and its position tiles
+  auto pw3 = [&](const ST* a2) {
 #pragma unroll
     for (int u = 0; u < G::T2W; ++u) {
-      const int mt = pg + G::PG * u;
+      const int mt = pg3 + G::P3 * u;
       if (mt < G::T2) {
-        const u32x4 x = *reinterpret_cast<const u32x4*>(&a2g[(mt * 16 + lr) * G::GS + VEC * lg]);
-        acc[u] = MmaK<ST>::step(wk, x, acc[u]);
+        const u32x4 x = *reinterpret_cast<const u32x4*>(&a2[(mt * 16 + lr) * G::GS + VEC * lg]);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) acc[u][h] = MmaK<ST>::step(wk[h], x, acc[u][h]);
       }
     }
-    if (g + kSub2CG < C) wk = ld16(w3row + g + kSub2CG);
+  };
+#pragma unroll 1
+  for (int g = 0; g < C; g += kSub2CG) {
+    conv0(g, a1g);
+    __syncthreads();
+    dwconv1(g, a1g, a2g);
+    __syncthreads();
+    pw3(a2g);
+    if (g + kSub2CG < C) {  // the next group's k-step loads during its conv.0 and depthwise conv
+#pragma unroll
+      for (int h = 0; h < 2; ++h) wk[h] = ld16(w3row[h] + g + kSub2CG);
+    }
     __syncthreads();  // the next group rewrites a1g / a2g
   }
 
   // ---- conv.3 mask, ReLU -> a2out [position][C] (over the group buffers)
 #pragma unroll
   for (int u = 0; u < G::T2W; ++u) {
-    const int mt = pg + G::PG * u;
+    const int mt = pg3 + G::P3 * u;
     if (mt < G::T2) {
       const int m = mt * 16 + lr;
       const int i2 = m / G::C2, q2 = m - i2 * G::C2;
       const int r2 = 2 * t0 - 2 + i2, c2 = 2 * p0 - 2 + q2;
       const bool ok = m < G::M2 && r2 >= 0 && r2 < len2 && c2 >= 0 && c2 < F2;
-      const uint2 v = make_uint2(relu2(cvt2<ST>(acc[u][0], acc[u][1])), relu2(cvt2<ST>(acc[u][2], acc[u][3])));
-      *reinterpret_cast<uint2*>(&a2o[m * G::RS + c3]) = ok ? v : make_uint2(0u, 0u);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const f32x4_t& a = acc[u][h];
+        const uint2 v = make_uint2(relu2(cvt2<ST>(a[0], a[1])), relu2(cvt2<ST>(a[2], a[3])));
+        *reinterpret_cast<uint2*>(&a2o[m * G::RS + (2 * np + h) * 16 + 4 * lg]) = ok ? v : make_uint2(0u, 0u);
+      }
     }
   }
   // conv.6's weights for the wave's channel tile load while the second
@@ -1178,27 +1229,52 @@ static int launch_sub_c(const pk_sub_args* a, hipStream_t st) {
   }
 }
 
-// fp16 / bf16: two output frames x QT columns per workgroup of 16 waves
-constexpr int kSub2Frames = 2;
+// CUs of the current device, read once per device
+static int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] <= 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
 
-template <typename ST, int QT, int C>
+// fp16 / bf16: NF output frames x QT columns per workgroup of 16 waves
+template <typename ST, int NF, int QT, int C>
 static int launch_sub2(const pk_sub_args* a, hipStream_t st) {
   const SubK<ST> k = sub_args<ST>(a, C);
   const int F3 = half_up(half_up(half_up(a->n_mels)));
-  const dim3 grid((a->max_out + kSub2Frames - 1) / kSub2Frames, (F3 + QT - 1) / QT, a->batch);
-  hipLaunchKernelGGL((subsample2_kernel<ST, kSub2Frames, QT, C>), grid, dim3(kSub2Threads), 0, st, k);
+  const dim3 grid((a->max_out + NF - 1) / NF, (F3 + QT - 1) / QT, a->batch);
+  hipLaunchKernelGGL((subsample2_kernel<ST, NF, QT, C>), grid, dim3(kSub2Threads), 0, st, k);
   return check_launch("pk_subsample");
+}
+
+// Two frames a tile share the conv.0 / first depthwise rows their receptive
+// fields overlap in (about 0.6 of the one-frame tile's work per frame), but
+// when one-frame tiles fit on the CUs in one round they finish sooner, and
+// wide tiles (QT 17) of two frames do not fit in LDS with C of 128 or more.
+template <typename ST, int QT, int C>
+static int launch_sub2_nf(const pk_sub_args* a, hipStream_t st) {
+  const int F3 = half_up(half_up(half_up(a->n_mels)));
+  const int64_t tiles1 = (int64_t)a->max_out * ((F3 + QT - 1) / QT) * a->batch;
+  if constexpr (Sub2Geom<ST, 2, QT, C>::FITS) {
+    if (tiles1 > cu_count()) return launch_sub2<ST, 2, QT, C>(a, st);
+  }
+  return launch_sub2<ST, 1, QT, C>(a, st);
 }
 
 template <typename ST, int QT>
 static int launch_sub2_c(const pk_sub_args* a, hipStream_t st) {
   switch (a->channels) {
     case 64:
-      return launch_sub2<ST, QT, 64>(a, st);
+      return launch_sub2_nf<ST, QT, 64>(a, st);
     case 128:
-      return launch_sub2<ST, QT, 128>(a, st);
+      return launch_sub2_nf<ST, QT, 128>(a, st);
     default:
-      return launch_sub2<ST, QT, 256>(a, st);
+      return launch_sub2_nf<ST, QT, 256>(a, st);
   }
 }
 

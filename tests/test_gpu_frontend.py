@@ -177,6 +177,51 @@ def test_subsampling_matches_oracle(cuda, dt, Fm, C):
     _close_sub(y.double().cpu().numpy().reshape(-1, D), ref_y, dt, "out")
 
 
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("Fm", [80, 128])
+def test_subsampling_tile_shapes_agree(cuda, dt, Fm):
+    """The 16-bit stack kernel takes two output frames a workgroup when
+    one-frame workgroups would not all fit on the CUs at once, one frame
+    otherwise.  The same 64 streams (partial lengths, frames dropped at the
+    front of some) as one batch (two-frame tiles) and in batches of 4
+    (one-frame tiles) give the same bits: every output is the same sums in the
+    same order.  Three of them also match the oracle."""
+    C, D = 256, 64
+    m = _module(C, Fm, D, dt, cuda, seed=7 * Fm)
+    B, T = 64, 41
+    T3 = stack_len(T)
+    cus = torch.cuda.get_device_properties(cuda).multi_processor_count
+    assert B * T3 > cus >= 4 * T3, (B * T3, cus)  # one batch: two-frame tiles; 4 streams: one-frame
+    g = torch.Generator().manual_seed(Fm + 1)
+    x = (torch.randn(B, T, Fm, generator=g) * 3 - 8).to(cuda).contiguous()
+    rng = np.random.default_rng(Fm)
+    lengths = rng.integers(1, T + 1, size=B)
+    drops = rng.integers(0, 3, size=B)
+    names = ("slot", "row0", "rows", "length", "drop", "n_out", "out_row", "reserved")
+    def records(slots, first_row):
+        rec = np.zeros(len(slots), dtype=[(n, "<i4") for n in names])
+        for i, b in enumerate(slots):
+            n_out = T3 - int(drops[b])
+            rec[i] = (b, 0, T, int(lengths[b]), int(drops[b]), n_out, first_row + i * T3, 0)
+        return rec
+    whole = m.stack(x, records(range(B), 0), False, B * T3, T3)
+    parts = torch.zeros_like(whole)
+    for b0 in range(0, B, 4):
+        rec = records(range(b0, b0 + 4), 0)
+        parts[b0 * T3 : (b0 + 4) * T3] = m.stack(x, rec, False, 4 * T3, T3)
+    torch.cuda.synchronize()
+    for b in range(B):
+        n_out = T3 - int(drops[b])
+        got, ref = whole[b * T3 : b * T3 + n_out], parts[b * T3 : b * T3 + n_out]
+        assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), f"stream {b}: tile shapes differ"
+    sd = _sd(m)
+    for b in (0, 17, 63):
+        ref_flat, _ = fe.conv_subsample(x[b].double().cpu().numpy(), int(lengths[b]), sd, dt, linear=False)
+        n_out = T3 - int(drops[b])
+        got = whole[b * T3 : b * T3 + n_out].double().cpu().numpy()
+        _close_sub(got, ref_flat[int(drops[b]) :], dt, f"stream {b} stack")
+
+
 # (n_mels, d_model, first chunk, next chunk, frames per step, sample ring,
 # mel ring, steps): the small model's chunking (right context 1: 9 then 16 mel
 # frames) and the large model's (right context 13: 105 then 112 mel frames,
