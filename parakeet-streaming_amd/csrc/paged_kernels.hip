@@ -791,7 +791,13 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
         bd_lds[wave][1][pt * 16 + q16] = d[1] + d[3];
       }
     }
-    // ---- (q+u).k over the wave's columns: D rows 0..3 (lanes 0..15)
+    // ---- (q+u).k over the wave's columns, D rows 0..3 (lanes 0..15), tile by
+    //      tile.  Once a tile's K rows are consumed (and, for a tile holding
+    //      this step's frames, appended to their pages by query group 0: the
+    //      row index is valid only for the frames' lanes), the tile's V rows
+    //      are issued into the registers it frees: no more registers in flight
+    //      than the K rows alone, and the V round trip overlaps the rest of the
+    //      K phase, the scores and the softmax
 #pragma unroll
     for (int kt = 0; kt < NT; ++kt) {
       f32x4_t d = {0.f, 0.f, 0.f, 0.f};
@@ -801,27 +807,19 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
         ac_lds[wave][0][16 * kt + q16] = d[0] + d[2];
         ac_lds[wave][1][16 * kt + q16] = d[1] + d[3];
       }
-    }
-    // ---- fused append of this step's K rows (query group 0): the row index
-    //      is valid only for lanes holding one of the chunk's frames
-    if (do_append) {
+      if (do_append && has_frames(kt)) {
 #pragma unroll
-      for (int kt = 0; kt < NT; ++kt)
-        if (has_frames(kt))
-#pragma unroll
-          for (int ks = 0; ks < KS; ++ks)
-            pk_buffer_store_x4(kr[kt][ks], r_kp, arow[kt], kg * 16, blk_soff + ks * blk_step, 0);
-    }
-    // ---- V rows, issued once the K rows are consumed (half the registers in
-    //      flight); their latency overlaps the scores and softmax
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int kt = 0; kt < NT; ++kt)
+        for (int ks = 0; ks < KS; ++ks)
+          pk_buffer_store_x4(kr[kt][ks], r_kp, arow[kt], kg * 16, blk_soff + ks * blk_step, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         vr[kt][ks] = pk_buffer_load_x4(r_vp, prow[kt], kg * 16, blk_soff + ks * blk_step, 0);
         if (has_frames(kt)) vr[kt][ks] |= pk_buffer_load_x4(r_vn, frow[kt], cbyte + ks * KSB, 0, 0);
       }
+      __builtin_amdgcn_sched_barrier(0);
+    }
     __syncthreads();  // partial dot products of the stream's waves in LDS
 
     // ---- scores: lane handles slots lane + 64*r; online softmax
