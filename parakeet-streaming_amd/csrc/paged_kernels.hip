@@ -752,9 +752,10 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
 
     // ---- K and V rows, lane = slot 16*kt + q16 (window column jb + slot),
     //      columns ks*32 + kg*8 .. + 7 of the wave's 64: block rows and frame
-    //      rows first, then the K loads.  A tile that holds one of this step's
-    //      frames also reads the projection output; every lane takes exactly
-    //      one source (the other reads zeros), so the two are OR-ed.
+    //      rows first, then the K loads.  In a tile that holds one of this
+    //      step's frames, the frame lanes load from the projection output and
+    //      the others from the pages (an exec-masked pair of loads into one
+    //      register), so nothing waits for the loads until their first use.
     uint32_t prow[NT], frow[NT], arow[NT];
 #pragma unroll
     for (int kt = 0; kt < NT; ++kt) {
@@ -772,8 +773,10 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
     for (int kt = 0; kt < NT; ++kt)
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        kr[kt][ks] = pk_buffer_load_x4(r_kp, prow[kt], kg * 16, blk_soff + ks * blk_step, 0);
-        if (has_frames(kt)) kr[kt][ks] |= pk_buffer_load_x4(r_kn, frow[kt], cbyte + ks * KSB, 0, 0);
+        if (has_frames(kt) && frow[kt] != kNoRow)
+          kr[kt][ks] = pk_buffer_load_x4(r_kn, frow[kt], cbyte + ks * KSB, 0, 0);
+        else
+          kr[kt][ks] = pk_buffer_load_x4(r_kp, prow[kt], kg * 16, blk_soff + ks * blk_step, 0);
       }
     __syncthreads();  // position rows staged
 
@@ -815,8 +818,10 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        vr[kt][ks] = pk_buffer_load_x4(r_vp, prow[kt], kg * 16, blk_soff + ks * blk_step, 0);
-        if (has_frames(kt)) vr[kt][ks] |= pk_buffer_load_x4(r_vn, frow[kt], cbyte + ks * KSB, 0, 0);
+        if (has_frames(kt) && frow[kt] != kNoRow)
+          vr[kt][ks] = pk_buffer_load_x4(r_vn, frow[kt], cbyte + ks * KSB, 0, 0);
+        else
+          vr[kt][ks] = pk_buffer_load_x4(r_vp, prow[kt], kg * 16, blk_soff + ks * blk_step, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
