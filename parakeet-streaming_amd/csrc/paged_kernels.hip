@@ -540,8 +540,9 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
   constexpr int KT = 16 * NT;      // slots (window columns) per pass
   constexpr int NPT = NT + 1;      // position-row tiles: slot s of query ii reads row s + TQ-1-ii
   constexpr int PROWS = 16 * NPT;
-  constexpr int PSTRIDE = DK * 2 + 16;          // bytes per staged position row
-  constexpr int CHR = DK / 8;                   // 16-byte chunks per staged row
+  constexpr int CHR = DK / 8;                   // 16-byte chunks per staged position row
+  constexpr int PSTRIDE = CHR * 16;             // bytes per staged position row (unpadded)
+  constexpr int RPB = 16 / CHR;                 // staged rows per 256 bytes (all 64 banks)
   constexpr int PCH = (PROWS * CHR + NTH - 1) / NTH;  // staged chunks per thread
   constexpr int VSTRIDE = 64 * 2 + 16;          // bytes per staged V row
   constexpr int SK = (KT + 63) / 64;            // slots per lane per query
@@ -643,16 +644,27 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
     return min(NPT, (s_max + TQ - 1) / 16 + 1);
   };
   // position rows (rows outside the table read zeros) and mask bytes of a pass
-  u32x4 pst[PCH];
+  // staged position rows: chunk c of row r sits at chunk c ^ pkey(r) of the
+  // unpadded row, so the 16 rows an MFMA operand read takes (one chunk each)
+  // fall on distinct banks
+  auto pkey = [&](int row) { return (row / RPB) & (CHR - 1); };
   uint8_t mk[SK][TQ];
   auto load_pass_shared = [&](int jb) {
+    // the position rows of the pass go straight to LDS (buffer loads to LDS:
+    // no registers, so the K rows can be issued before they are in); each
+    // wave's instruction c fills 64 consecutive chunks, lane = chunk, reading
+    // the chunk that belongs at its swizzled place.  All PROWS rows, with
+    // every lane active (no branch: the compiler then counts these loads
+    // exactly when it places its waits); rows past the table read zeros.
+    static_assert(PROWS * CHR % NTH == 0, "whole instructions");
     const int rb = jb + p.T - i0 - TQ;
-    const int nchunk = pass_tiles(jb) * 16 * CHR;
 #pragma unroll
     for (int c = 0; c < PCH; ++c) {
-      const int idx = min((int)threadIdx.x + c * NTH, PROWS * CHR - 1);
-      pst[c] = u32x4{0u, 0u, 0u, 0u};
-      if (idx < nchunk) pst[c] = pk_buffer_load_x4(r_pos, rb + idx / CHR, (h * DK + (idx % CHR) * 8) * ES, 0, 0);
+      const int base = c * NTH + wave * 64;  // wave-uniform
+      const int idx = base + lane;
+      const int row = idx / CHR, cc = (idx % CHR) ^ pkey(row);
+      __builtin_amdgcn_struct_ptr_buffer_load_lds(r_pos, (__attribute__((address_space(3))) void*)(pos_lds + base * 16), 16,
+                                                  rb + row, (h * DK + cc * 8) * ES, 0, 0, 0);
     }
     if (mask_mode == 1) {
 #pragma unroll
@@ -720,6 +732,10 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
     for (int e = 0; e < 8; ++e) x[e] = (a_ii < nq ? qf[e] : 0.f) + bf[e];
     aop[ks] = split16<ST, 8, u32x4>(x, a_kind & 1);
     if (a_kind >= 4) aop[ks] = u32x4{0u, 0u, 0u, 0u};
+    // built here, before the K rows are issued: q and the biases are in by
+    // now (they were loaded ahead of the header's wait), whereas after the K
+    // loads the build would wait for all of them
+    asm volatile("" ::"v"(aop[ks]));
   }
 
   f32x4_t oacc[4];  // P.V: D rows (hi q0, hi q1, lo q0, lo q1), 4 column tiles of 16
@@ -741,14 +757,6 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
     const int jb = pass * KT;
     const int npt = pass_tiles(jb);
     if (MULTI && pass > 0) load_pass_shared(jb);
-
-    // ---- stage the position rows of the pass
-#pragma unroll
-    for (int c = 0; c < PCH; ++c) {
-      const int idx = threadIdx.x + c * NTH;
-      if (c + 1 < PCH || idx < PROWS * CHR)
-        *reinterpret_cast<u32x4*>(pos_lds + (idx / CHR) * PSTRIDE + (idx % CHR) * 16) = pst[c];
-    }
 
     // ---- K and V rows, lane = slot 16*kt + q16 (window column jb + slot),
     //      columns ks*32 + kg*8 .. + 7 of the wave's 64: block rows and frame
@@ -778,17 +786,25 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
         else
           kr[kt][ks] = pk_buffer_load_x4(r_kp, prow[kt], kg * 16, blk_soff + ks * blk_step, 0);
       }
-    __syncthreads();  // position rows staged
+    // the wave's position-row loads (issued before any K row, and at least
+    // NT*KS vector loads ago) are in LDS: wait for them, not for the K rows,
+    // before the barrier that makes every wave's part visible
+    static_assert(NT * KS <= 15, "vmcnt");
+    __builtin_amdgcn_s_waitcnt(0x0f70 | (NT * KS));
+    __syncthreads();  // position rows in LDS
 
     // ---- (q+v).pos over the wave's columns: D rows 4..7 (lanes 16..31)
 #pragma unroll
     for (int pt = 0; pt < NPT; ++pt) {
       if (pt >= npt) break;
       f32x4_t d = {0.f, 0.f, 0.f, 0.f};
-      const uint8_t* src = pos_lds + (pt * 16 + q16) * PSTRIDE + (hf * 64 + kg * 8) * 2;
+      const int prow_l = pt * 16 + q16;
+      const uint8_t* src = pos_lds + prow_l * PSTRIDE;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        d = Mma<ST>::k32(aop[ks], *reinterpret_cast<const u32x4*>(src + ks * KSB), d);
+      for (int ks = 0; ks < KS; ++ks) {
+        const int chunk = hf * 8 + ks * (KSB / 16) + kg;  // columns hf*64 + ks*32 + kg*8 ..
+        d = Mma<ST>::k32(aop[ks], *reinterpret_cast<const u32x4*>(src + ((chunk ^ pkey(prow_l)) * 16)), d);
+      }
       if (kg == 1) {
         bd_lds[wave][0][pt * 16 + q16] = d[0] + d[2];
         bd_lds[wave][1][pt * 16 + q16] = d[1] + d[3];
