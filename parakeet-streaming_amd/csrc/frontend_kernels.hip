@@ -62,8 +62,10 @@ __device__ static inline void philox4x32_10(uint32_t& c0, uint32_t& c1, uint32_t
       k0 += 0x9E3779B9u;
       k1 += 0xBB67AE85u;
     }
-    const uint32_t hi0 = __umulhi(0xD2511F53u, c0), lo0 = 0xD2511F53u * c0;
-    const uint32_t hi1 = __umulhi(0xCD9E8D57u, c2), lo1 = 0xCD9E8D57u * c2;
+    // each 32x32 -> 64-bit product as one multiply (both halves at once)
+    const uint64_t p0 = (uint64_t)0xD2511F53u * c0, p1 = (uint64_t)0xCD9E8D57u * c2;
+    const uint32_t hi0 = (uint32_t)(p0 >> 32), lo0 = (uint32_t)p0;
+    const uint32_t hi1 = (uint32_t)(p1 >> 32), lo1 = (uint32_t)p1;
     const uint32_t n0 = hi1 ^ c1 ^ k0, n2 = hi0 ^ c3 ^ k1;
     c0 = n0;
     c1 = lo1;
@@ -111,7 +113,8 @@ __global__ void __launch_bounds__(64 * kFeWaves) fe_kernel(const FeK p) {
   __shared__ float pw[kFeWaves][kBins + 3];
   __shared__ float xs[kSpanMax + 3];  // dithered samples of the workgroup's frames
   __shared__ float win_s[kMaxWin];
-  __shared__ float fbw[kMaxMels][kBand];  // band m's weights from its first bin on
+  __shared__ float fbw[kMaxMels][kBand + 1];  // band m's weights from its first bin on (rows padded:
+                                              // lane m reads row m, so the rows fall on distinct banks)
 
   const int b = blockIdx.y;
   const pk_fe_stream s = p.streams[b];
@@ -186,9 +189,11 @@ __global__ void __launch_bounds__(64 * kFeWaves) fe_kernel(const FeK p) {
   for (int u = 0; u < kXsPer; ++u) {
     const int i = tid + u * 64 * kFeWaves;
     const int64_t g = span0 + i;
-    float x = xr[u];
-    if (p.dither != 0.f && g >= 0 && g < total) x += p.dither * dither_normal(g, s.noise_id, p.seed_lo, p.seed_hi);
-    if (i < span) xs[i] = x;
+    if (i < span) {  // the span is the frames' reach, usually well under the staging's size
+      float x = xr[u];
+      if (p.dither != 0.f && g >= 0 && g < total) x += p.dither * dither_normal(g, s.noise_id, p.seed_lo, p.seed_hi);
+      xs[i] = x;
+    }
   }
   __syncthreads();
   // band m's weights from its first bin (the bins past kBand are read from fb)
