@@ -787,8 +787,6 @@ __device__ static inline uint32_t relu2(uint32_t v) {
 __device__ static inline uint32_t lo2(uint32_t x, uint32_t y) { return __builtin_amdgcn_perm(y, x, 0x05040100u); }
 __device__ static inline uint32_t hi2(uint32_t x, uint32_t y) { return __builtin_amdgcn_perm(y, x, 0x07060302u); }
 
-constexpr int kSub2Waves = 16;
-constexpr int kSub2Threads = 64 * kSub2Waves;
 constexpr int kSub2CG = 32;  // channels per group: one k-step of conv.3
 
 // conv.0 weights in LDS as the MFMA B operand: tap k of channel c at lane
@@ -806,8 +804,12 @@ __device__ static inline int w5_index(int pp, int c) {
   return pp * C + ((c >> 2) & 1) * (C / 2) + (c >> 3) * 4 + (c & 3);
 }
 
-template <typename ST, int NF, int QT, int C>
+// W waves a workgroup: 16 (one workgroup a CU), or 8 with the second stage
+// run over channel halves (NH = 2) so that two workgroups share a CU and one's
+// depthwise (VALU) work overlaps the other's pointwise (MFMA) work
+template <typename ST, int NF, int QT, int C, int W>
 struct Sub2Geom {
+  static constexpr int NTH = 64 * W;                                // threads
   static constexpr int VEC = 8;                                     // 16-bit elements per 16 bytes
   static constexpr int XR = 8 * NF + 7, XC = 8 * QT + 7;             // input rows / cols of the tile
   static constexpr int XN = (XR * XC + 7) / 8 * 8;
@@ -820,30 +822,39 @@ struct Sub2Geom {
   static constexpr int M1S = ((T1 * 2) | 1) * 8;  // a1g channel stride: 8 x odd elements (distinct banks)
   static constexpr int M3 = NF * QT, T3 = (M3 + 15) / 16;                                   // after dw 2
   static constexpr int GS = kSub2CG + VEC;  // a2g position stride (padded by 16 bytes)
-  static constexpr int RS = C + VEC;        // a2out / a3 position stride
+  static constexpr int NH = W < 16 ? 2 : 1;  // channel parts of the second depthwise conv and conv.6
+  static constexpr int CH = C / NH;          // channels of a part
+  static constexpr int RS = CH + VEC;        // a2out / a3 position stride
   static constexpr int NTL = C / 16;        // channel tiles of a pointwise conv
-  static constexpr int PG = kSub2Waves / NTL;  // waves per channel tile (position groups)
-  static constexpr int T1W = (T1 + kSub2Waves - 1) / kSub2Waves;
+  // conv.6: a wave takes CPW channel tiles (consecutive) and position tiles pg + PG u
+  static constexpr int CPW = NTL > W ? NTL / W : 1, NTW = NTL / CPW, PG = W / NTW;
+  static constexpr int T1W = (T1 + W - 1) / W;
   // conv.3: a wave takes channel tiles 2 (w mod NP), 2 (w mod NP) + 1 and
-  // position tiles w / NP + P3 u, so each wave reads half the positions' rows
-  static constexpr int NP = C / 32, P3 = kSub2Waves / NP, T2W = (T2 + P3 - 1) / P3;
+  // position tiles w / NP + P3 u, so each wave reads 1 / P3 of the positions' rows
+  static constexpr int NP = C / 32, P3 = W / NP, T2W = (T2 + P3 - 1) / P3;
   static constexpr int T3W = (T3 + PG - 1) / PG;
   static constexpr int KS = C / 32;         // k-steps of a pointwise conv
+  static constexpr int KSH = KS / NH;       // conv.6 k-steps of a channel part
   static constexpr int A1N = kSub2CG * M1S, A2N = T2 * 16 * GS;  // the a1g / a2g buffers
   static constexpr int P1 = XN + A1N + A2N;                        // xin | a1g | a2g
   static constexpr int P2 = T2 * 16 * RS + T3 * 16 * RS;       // a2out (output tile) | a3
   static constexpr int REG = cmax<P1, P2>::v;
   // LDS of the kernel: reg, w0p, w2p, w5p, bsm
   static constexpr int LDS_BYTES = REG * 2 + C * 16 * 2 + C * 32 + 5 * C * 4 + 4 * C * 4;
-  static constexpr bool FITS = LDS_BYTES <= 160 * 1024;
+  static constexpr bool FITS = LDS_BYTES <= (W < 16 ? 80 : 160) * 1024;  // W < 16: two a CU
+  static_assert(W == 8 || W == 16, "waves");
+  static_assert(W % NP == 0 && (NTL % W == 0 || W % NTL == 0), "channel tiles over waves");
+  static_assert(CH % kSub2CG == 0 && KS % NH == 0, "channel parts");
   static_assert(NF * C * QT <= T2 * 16 * RS, "output tile fits over a2out");
 };
 
-template <typename ST, int NF, int QT, int C>
-__global__ void __launch_bounds__(kSub2Threads) subsample2_kernel(const SubK<ST> p) {
-  typedef Sub2Geom<ST, NF, QT, C> G;
-  constexpr int VEC = G::VEC;
-  static_assert(C % 64 == 0 && C / 16 <= kSub2Waves, "channels");
+// four waves a SIMD (at most 128 registers a lane): one workgroup of 16 waves,
+// or two of 8, a CU
+template <typename ST, int NF, int QT, int C, int W>
+__global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))) subsample2_kernel(const SubK<ST> p) {
+  typedef Sub2Geom<ST, NF, QT, C, W> G;
+  constexpr int VEC = G::VEC, NTH = G::NTH;
+  static_assert(C % 64 == 0, "channels");
   __shared__ __align__(16) ST reg[G::REG];
   __shared__ __align__(16) ST w0p[C * 16];  // conv.0 (w0_index): taps 0..8, bias at 9, zeros
   // first depthwise conv: dword d of channel c at [d / 4][c][d % 4], rows kt as
@@ -858,6 +869,14 @@ __global__ void __launch_bounds__(kSub2Threads) subsample2_kernel(const SubK<ST>
   ST* const a3 = reg + G::T2 * 16 * G::RS;
   ST* const ot = reg;   // after the second depthwise conv: [frame][C][qv]
 
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int nt = (wave % G::NTW) * G::CPW, pg = wave / G::NTW;  // the wave's first conv.6 channel tile, position group
+  const int np = wave % G::NP, pg3 = wave / G::NP;    // the wave's conv.3 channel tile pair and position group
+  const int F = p.F;
+  const int F1 = half_up(F), F2 = half_up(F1), F3 = half_up(F2);
+
+  // ---- the workgroup's tile: output frames blockIdx.x, columns blockIdx.y, stream blockIdx.z
   const int b = blockIdx.z;
   const pk_sub_stream s = p.streams[b];
   const int j0 = blockIdx.x * NF;  // first output frame of the tile (of the kept frames)
@@ -870,29 +889,22 @@ __global__ void __launch_bounds__(kSub2Threads) subsample2_kernel(const SubK<ST>
   const int L3 = half_up(half_up(half_up(s.rows)));
   const int nf = min(NF, min(n_keep - j0, L3 - t0));  // frames the tile writes
   if (nf <= 0) return;
-  const int F = p.F;
-  const int F1 = half_up(F), F2 = half_up(F1), F3 = half_up(F2);
   const int p0 = blockIdx.y * QT;
   if (p0 >= F3) return;
   const int qv = min(QT, F3 - p0);
   const int len1 = half_up(s.length), len2 = half_up(len1), len3 = half_up(len2);
-  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const int lr = lane & 15, lg = lane >> 4;
-  const int nt = wave % G::NTL, pg = wave / G::NTL;  // the wave's conv.6 channel tile and position group
-  const int c3 = nt * 16 + 4 * lg;                    // the lane's 4 output channels of conv.6
-  const int np = wave % G::NP, pg3 = wave / G::NP;    // the wave's conv.3 channel tile pair and position group
 
   // ---- weights, biases and the input tile, every global load issued before
   //      the first LDS store (one round trip): the 3x3 weights as 16-byte
   //      chunks of their [C][9] arrays, the input rows >= length and the
   //      padding as zeros
   constexpr int kWCh = 9 * C / VEC;                                   // 16-byte chunks of a [C][9] array
-  constexpr int kWPer = (kWCh + kSub2Threads - 1) / kSub2Threads;
-  constexpr int kXPer = (G::XN + kSub2Threads - 1) / kSub2Threads;
+  constexpr int kWPer = (kWCh + NTH - 1) / NTH;
+  constexpr int kXPer = (G::XN + NTH - 1) / NTH;
   u32x4 w0c[kWPer], w2c[kWPer], w5c[kWPer];
 #pragma unroll
   for (int u = 0; u < kWPer; ++u) {
-    const int ch = min(tid + u * kSub2Threads, kWCh - 1);
+    const int ch = min(tid + u * NTH, kWCh - 1);
     w0c[u] = ld16(p.w0 + ch * VEC);
     w2c[u] = ld16(p.w2 + ch * VEC);
     w5c[u] = ld16(p.w5 + ch * VEC);
@@ -904,6 +916,7 @@ __global__ void __launch_bounds__(kSub2Threads) subsample2_kernel(const SubK<ST>
     for (int k = 0; k < 5; ++k)
       if (bp[k]) bias[k] = from_st(bp[k][tid]);
   }
+  // the input tile: rows >= length and the padding as zeros
   float xr[kXPer];
   {
     const int r0 = 8 * t0 - 14, c0 = 8 * p0 - 14;
@@ -911,7 +924,7 @@ __global__ void __launch_bounds__(kSub2Threads) subsample2_kernel(const SubK<ST>
     const int rmask = p.in_rows - 1;
 #pragma unroll
     for (int u = 0; u < kXPer; ++u) {
-      const int i = tid + u * kSub2Threads;
+      const int i = tid + u * NTH;
       const int rr = i / G::XC, cc = i - rr * G::XC;
       const int gr = r0 + rr, gc = c0 + cc;
       const bool ok = i < G::XR * G::XC && gr >= 0 && gr < s.length && gc >= 0 && gc < F;
@@ -922,7 +935,7 @@ __global__ void __launch_bounds__(kSub2Threads) subsample2_kernel(const SubK<ST>
   }
 #pragma unroll
   for (int u = 0; u < kWPer; ++u) {
-    const int ch = tid + u * kSub2Threads;
+    const int ch = tid + u * NTH;
     if (ch < kWCh) {
       const Chunk<ST> a = __builtin_bit_cast(Chunk<ST>, w0c[u]);
       const Chunk<ST> b2 = __builtin_bit_cast(Chunk<ST>, w2c[u]);
@@ -949,19 +962,19 @@ __global__ void __launch_bounds__(kSub2Threads) subsample2_kernel(const SubK<ST>
 #pragma unroll
     for (int k = 0; k < 4; ++k) bsm[k][tid] = bias[k + 1];
   }
-#pragma unroll
-  for (int u = 0; u < kXPer; ++u) {
-    const int i = tid + u * kSub2Threads;
-    if (i < G::XN) xin[i] = to_st<ST>(xr[u]);
-  }
-  // conv.3's weight k-step for the first group: lane holds W3[n][g + 8 lg ..]
-  // for the wave's channel tile (each group's step loads during the previous one)
+  // conv.3's weight rows of the wave's channel tiles: lane holds W3[n][g + 8 lg ..];
+  // the first group's k-step loads now, each next one during the group before
   const ST* w3row[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) w3row[h] = p.w3 + (int64_t)((2 * np + h) * 16 + lr) * C + VEC * lg;
+
   u32x4 wk[2];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    w3row[h] = p.w3 + (int64_t)((2 * np + h) * 16 + lr) * C + VEC * lg;
-    wk[h] = ld16(w3row[h]);
+  for (int h = 0; h < 2; ++h) wk[h] = ld16(w3row[h]);
+#pragma unroll
+  for (int u = 0; u < kXPer; ++u) {
+    const int i = tid + u * NTH;
+    if (i < G::XN) xin[i] = to_st<ST>(xr[u]);
   }
   __syncthreads();
 
@@ -979,7 +992,7 @@ __global__ void __launch_bounds__(kSub2Threads) subsample2_kernel(const SubK<ST>
   s16x4_t xop[G::T1W];
 #pragma unroll
   for (int u = 0; u < G::T1W; ++u) {
-    const int m = (wave + kSub2Waves * u) * 16 + lr;
+    const int m = (wave + W * u) * 16 + lr;
     const int mm = min(m, G::M1 - 1);
     const int i1 = mm / G::C1P, qr = mm - i1 * G::C1P, q1 = min(qr, G::C1 - 1);
     const int r1 = 4 * t0 - 6 + i1, c1 = 4 * p0 - 6 + qr;
@@ -1010,7 +1023,7 @@ __global__ void __launch_bounds__(kSub2Threads) subsample2_kernel(const SubK<ST>
     for (int ct = 0; ct < 2; ++ct) wop[ct] = *reinterpret_cast<const s16x4_t*>(&w0p[w0_index(g + ct * 16 + lr, 4 * lg)]);
 #pragma unroll
     for (int u = 0; u < G::T1W; ++u) {
-      const int mt = wave + kSub2Waves * u;
+      const int mt = wave + W * u;
       if (mt < G::T1) {
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) {
@@ -1028,7 +1041,7 @@ __global__ void __launch_bounds__(kSub2Threads) subsample2_kernel(const SubK<ST>
   // read of 16 channels' rows is conflict free, a 4-byte one at this stride
   // is not), and each tap pair is one fp32-accumulating dot2 (w0 w1 | w2 0)
   auto dwconv1 = [&](int g, const ST* a1, ST* a2) {
-    for (int it = tid; it < kSub2CG * G::R2 * G::JG; it += kSub2Threads) {
+    for (int it = tid; it < kSub2CG * G::R2 * G::JG; it += NTH) {
       const int c = it % kSub2CG, rest = it / kSub2CG;
       const int i2 = rest % G::R2, jg = rest / G::R2;
       const u32x4 wa = *reinterpret_cast<const u32x4*>(&w2p[0][g + c][0]);
@@ -1087,83 +1100,129 @@ __global__ void __launch_bounds__(kSub2Threads) subsample2_kernel(const SubK<ST>
     __syncthreads();  // the next group rewrites a1g / a2g
   }
 
-  // ---- conv.3 mask, ReLU -> a2out [position][C] (over the group buffers)
+  // ---- second stage, NH channel parts of CH channels one after the other:
+  //      conv.3's mask and ReLU -> a2out [position][CH] (over the group
+  //      buffers), the second depthwise conv -> a3 [frame * QT + column][CH],
+  //      and conv.6's k-steps over the part's channels, summed in d
+
+  // conv.3's outputs as 16-bit pairs (half the registers of the sums), zero
+  // outside the map
+  uint2 c3v[G::T2W][2];
 #pragma unroll
   for (int u = 0; u < G::T2W; ++u) {
-    const int mt = pg3 + G::P3 * u;
-    if (mt < G::T2) {
-      const int m = mt * 16 + lr;
-      const int i2 = m / G::C2, q2 = m - i2 * G::C2;
-      const int r2 = 2 * t0 - 2 + i2, c2 = 2 * p0 - 2 + q2;
-      const bool ok = m < G::M2 && r2 >= 0 && r2 < len2 && c2 >= 0 && c2 < F2;
+    const int m = (pg3 + G::P3 * u) * 16 + lr;
+    const int i2 = m / G::C2, q2 = m - i2 * G::C2;
+    const int r2 = 2 * t0 - 2 + i2, c2 = 2 * p0 - 2 + q2;
+    const bool ok = m < G::M2 && r2 >= 0 && r2 < len2 && c2 >= 0 && c2 < F2;
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const f32x4_t& a = acc[u][h];
-        const uint2 v = make_uint2(relu2(cvt2<ST>(a[0], a[1])), relu2(cvt2<ST>(a[2], a[3])));
-        *reinterpret_cast<uint2*>(&a2o[m * G::RS + (2 * np + h) * 16 + 4 * lg]) = ok ? v : make_uint2(0u, 0u);
+    for (int h = 0; h < 2; ++h) {
+      const f32x4_t& a = acc[u][h];
+      c3v[u][h] = ok ? make_uint2(relu2(cvt2<ST>(a[0], a[1])), relu2(cvt2<ST>(a[2], a[3]))) : make_uint2(0u, 0u);
+    }
+  }
+  f32x4_t d[G::T3W][G::CPW];
+#pragma unroll
+  for (int i = 0; i < G::CPW; ++i) {
+    const f32x4_t b6 = *reinterpret_cast<const f32x4_t*>(&bsm[3][(nt + i) * 16 + 4 * lg]);
+#pragma unroll
+    for (int u = 0; u < G::T3W; ++u) d[u][i] = b6;
+  }
+#pragma unroll
+  for (int hh = 0; hh < G::NH; ++hh) {
+    if (np / (G::NP / G::NH) == hh) {  // the wave's conv.3 channels lie in this part
+#pragma unroll
+      for (int u = 0; u < G::T2W; ++u) {
+        const int mt = pg3 + G::P3 * u;
+        if (mt < G::T2) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            *reinterpret_cast<uint2*>(&a2o[(mt * 16 + lr) * G::RS + (2 * np + h) * 16 - hh * G::CH + 4 * lg]) =
+                c3v[u][h];
+        }
+      }
+    }
+    // conv.6's weights for the wave's channel tiles and this part's k-steps:
+    // with one workgroup a CU they load while the second depthwise conv runs;
+    // with two (fewer registers a wave) after it, while the other workgroup runs
+    u32x4 w6q[G::CPW][G::KSH];
+    auto load_w6 = [&]() {
+#pragma unroll
+      for (int i = 0; i < G::CPW; ++i)
+#pragma unroll
+        for (int kk = 0; kk < G::KSH; ++kk)
+          w6q[i][kk] = ld16(p.w6 + (int64_t)((nt + i) * 16 + lr) * C + VEC * lg + (hh * G::KSH + kk) * 32);
+    };
+    if constexpr (G::NH == 1) load_w6();
+    __syncthreads();
+
+    // second depthwise conv, masked: a thread takes 8 channels of one
+    // position; per tap pair, the two taps' values of a channel are gathered
+    // into one dword (v_perm) for a dot2
+    for (int it = tid; it < G::T3 * 16 * (G::CH / VEC); it += NTH) {
+      const int m3 = it / (G::CH / VEC), cc = (it - m3 * (G::CH / VEC)) * VEC;
+      const int cw = hh * G::CH + cc;  // channel of the weights and bias
+      const int f = min(m3 / QT, NF - 1), q = m3 - (m3 / QT) * QT;
+      float sum[VEC];
+      {
+        const float4 x = *reinterpret_cast<const float4*>(&bsm[2][cw]);
+        const float4 y = *reinterpret_cast<const float4*>(&bsm[2][cw + 4]);
+        sum[0] = x.x, sum[1] = x.y, sum[2] = x.z, sum[3] = x.w;
+        sum[4] = y.x, sum[5] = y.y, sum[6] = y.z, sum[7] = y.w;
+      }
+      const ST* const src = &a2o[(2 * f * G::C2 + 2 * q) * G::RS + cc];
+#pragma unroll
+      for (int pp = 0; pp < 5; ++pp) {
+        const int ta = 2 * pp, tb = 2 * pp + 1;
+        const u32x4 A = ld16(src + ((ta / 3) * G::C2 + ta % 3) * G::RS);
+        const u32x4 B = tb < 9 ? ld16(src + ((tb / 3) * G::C2 + tb % 3) * G::RS) : u32x4{0u, 0u, 0u, 0u};
+        const u32x4 W0 = *reinterpret_cast<const u32x4*>(&w5p[w5_index<C>(pp, cw)]);
+        const u32x4 W1 = *reinterpret_cast<const u32x4*>(&w5p[w5_index<C>(pp, cw + 4)]);
+        const uint32_t a[4] = {A.x, A.y, A.z, A.w}, bb[4] = {B.x, B.y, B.z, B.w};
+        const uint32_t w[8] = {W0.x, W0.y, W0.z, W0.w, W1.x, W1.y, W1.z, W1.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          sum[2 * e] = dot2<ST>(lo2(a[e], bb[e]), w[2 * e], sum[2 * e]);
+          sum[2 * e + 1] = dot2<ST>(hi2(a[e], bb[e]), w[2 * e + 1], sum[2 * e + 1]);
+        }
+      }
+      const bool ok = m3 < G::M3 && t0 + f < len3;
+      const u32x4 o = {cvt2<ST>(sum[0], sum[1]), cvt2<ST>(sum[2], sum[3]), cvt2<ST>(sum[4], sum[5]),
+                       cvt2<ST>(sum[6], sum[7])};
+      *reinterpret_cast<u32x4*>(&a3[m3 * G::RS + cc]) = ok ? o : u32x4{0u, 0u, 0u, 0u};
+    }
+    if constexpr (G::NH > 1) load_w6();
+    __syncthreads();
+
+    // conv.6 k-steps over the part's channels
+#pragma unroll
+    for (int u = 0; u < G::T3W; ++u) {
+      const int mt = pg + G::PG * u;
+      if (mt < G::T3) {
+#pragma unroll
+        for (int kk = 0; kk < G::KSH; ++kk) {
+          const u32x4 x = *reinterpret_cast<const u32x4*>(&a3[(mt * 16 + lr) * G::RS + kk * 32 + VEC * lg]);
+#pragma unroll
+          for (int i = 0; i < G::CPW; ++i) d[u][i] = MmaK<ST>::step(w6q[i][kk], x, d[u][i]);
+        }
       }
     }
   }
-  // conv.6's weights for the wave's channel tile load while the second
-  // depthwise conv runs
-  u32x4 w6q[G::KS];
-#pragma unroll
-  for (int kk = 0; kk < G::KS; ++kk) w6q[kk] = ld16(p.w6 + (int64_t)(nt * 16 + lr) * C + VEC * lg + kk * 32);
-  __syncthreads();
 
-  // ---- second depthwise conv -> a3 [frame * QT + column][C], masked: a thread
-  //      takes 8 channels of one position; per tap pair, the two taps' values
-  //      of a channel are gathered into one dword (v_perm) for a dot2
-  for (int it = tid; it < G::T3 * 16 * (C / VEC); it += kSub2Threads) {
-    const int m3 = it / (C / VEC), cc = (it - m3 * (C / VEC)) * VEC;
-    const int f = min(m3 / QT, NF - 1), q = m3 - (m3 / QT) * QT;
-    float sum[VEC];
-    {
-      const float4 x = *reinterpret_cast<const float4*>(&bsm[2][cc]);
-      const float4 y = *reinterpret_cast<const float4*>(&bsm[2][cc + 4]);
-      sum[0] = x.x, sum[1] = x.y, sum[2] = x.z, sum[3] = x.w;
-      sum[4] = y.x, sum[5] = y.y, sum[6] = y.z, sum[7] = y.w;
-    }
-    const ST* const src = &a2o[(2 * f * G::C2 + 2 * q) * G::RS + cc];
-#pragma unroll
-    for (int pp = 0; pp < 5; ++pp) {
-      const int ta = 2 * pp, tb = 2 * pp + 1;
-      const u32x4 A = ld16(src + ((ta / 3) * G::C2 + ta % 3) * G::RS);
-      const u32x4 B = tb < 9 ? ld16(src + ((tb / 3) * G::C2 + tb % 3) * G::RS) : u32x4{0u, 0u, 0u, 0u};
-      const u32x4 W0 = *reinterpret_cast<const u32x4*>(&w5p[w5_index<C>(pp, cc)]);
-      const u32x4 W1 = *reinterpret_cast<const u32x4*>(&w5p[w5_index<C>(pp, cc + 4)]);
-      const uint32_t a[4] = {A.x, A.y, A.z, A.w}, bb[4] = {B.x, B.y, B.z, B.w};
-      const uint32_t w[8] = {W0.x, W0.y, W0.z, W0.w, W1.x, W1.y, W1.z, W1.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        sum[2 * e] = dot2<ST>(lo2(a[e], bb[e]), w[2 * e], sum[2 * e]);
-        sum[2 * e + 1] = dot2<ST>(hi2(a[e], bb[e]), w[2 * e + 1], sum[2 * e + 1]);
-      }
-    }
-    const bool ok = m3 < G::M3 && t0 + f < len3;
-    const u32x4 o = {cvt2<ST>(sum[0], sum[1]), cvt2<ST>(sum[2], sum[3]), cvt2<ST>(sum[4], sum[5]),
-                     cvt2<ST>(sum[6], sum[7])};
-    *reinterpret_cast<u32x4*>(&a3[m3 * G::RS + cc]) = ok ? o : u32x4{0u, 0u, 0u, 0u};
-  }
-  __syncthreads();
-
-  // ---- conv.6 + bias, ReLU, mask -> output tile [frame][channel][qv columns] (over a2out)
+  // ---- conv.6 ReLU and mask -> output tile [frame][channel][qv columns],
+  //      over a2out (no wave reads it after the last barrier)
 #pragma unroll
   for (int u = 0; u < G::T3W; ++u) {
     const int mt = pg + G::PG * u;
     if (mt < G::T3) {
-      f32x4_t d = *reinterpret_cast<const f32x4_t*>(&bsm[3][c3]);
-#pragma unroll
-      for (int kk = 0; kk < G::KS; ++kk) {
-        const u32x4 x = *reinterpret_cast<const u32x4*>(&a3[(mt * 16 + lr) * G::RS + kk * 32 + VEC * lg]);
-        d = MmaK<ST>::step(w6q[kk], x, d);
-      }
       const int m3 = mt * 16 + lr;
       const int f = m3 / QT, q = m3 - f * QT;
       if (m3 < G::M3 && q < qv) {
         const bool ok = t0 + f < len3;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) ot[(f * C + c3 + e) * qv + q] = to_st<ST>(ok ? fmaxf(d[e], 0.f) : 0.f);
+        for (int i = 0; i < G::CPW; ++i)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            ot[(f * C + (nt + i) * 16 + 4 * lg + e) * qv + q] = to_st<ST>(ok ? fmaxf(d[u][i][e], 0.f) : 0.f);
       }
     }
   }
@@ -1171,10 +1230,10 @@ __global__ void __launch_bounds__(kSub2Threads) subsample2_kernel(const SubK<ST>
   ST* const out = p.out + (int64_t)(s.out_row + j0) * C * F3;
   if (qv == F3 && (reinterpret_cast<uintptr_t>(p.out) & 15) == 0) {
     // the tile spans every column: its nf frames of [C][F3] are one run
-    for (int i = tid * VEC; i < nf * C * F3; i += kSub2Threads * VEC) st16(out + i, ld16(ot + i));
+    for (int i = tid * VEC; i < nf * C * F3; i += NTH * VEC) st16(out + i, ld16(ot + i));
   } else {
     for (int f = 0; f < nf; ++f)
-      for (int i = tid; i < C * qv; i += kSub2Threads) {
+      for (int i = tid; i < C * qv; i += NTH) {
         const int c = i / qv, q = i - c * qv;
         out[(int64_t)f * C * F3 + c * F3 + p0 + q] = ot[f * C * qv + i];
       }
@@ -1247,28 +1306,41 @@ static int cu_count() {
   return cached[dev];
 }
 
-// fp16 / bf16: NF output frames x QT columns per workgroup of 16 waves
-template <typename ST, int NF, int QT, int C>
+// fp16 / bf16: one tile of NF output frames x QT columns a workgroup of W
+// waves (one workgroup a CU for W 16, two for W 8)
+template <typename ST, int NF, int QT, int C, int W>
 static int launch_sub2(const pk_sub_args* a, hipStream_t st) {
   const SubK<ST> k = sub_args<ST>(a, C);
   const int F3 = half_up(half_up(half_up(a->n_mels)));
   const dim3 grid((a->max_out + NF - 1) / NF, (F3 + QT - 1) / QT, a->batch);
-  hipLaunchKernelGGL((subsample2_kernel<ST, NF, QT, C>), grid, dim3(kSub2Threads), 0, st, k);
+  hipLaunchKernelGGL((subsample2_kernel<ST, NF, QT, C, W>), grid, dim3(64 * W), 0, st, k);
   return check_launch("pk_subsample");
 }
+
+// two-frame tiles a CU (of 8 waves each) from which the paired form is used
+constexpr int kSub2PairTiles = 2;
 
 // Two frames a tile share the conv.0 / first depthwise rows their receptive
 // fields overlap in (about 0.6 of the one-frame tile's work per frame), but
 // when one-frame tiles fit on the CUs in one round they finish sooner, and
 // wide tiles (QT 17) of two frames do not fit in LDS with C of 128 or more.
+// With several two-frame tiles a CU to run, workgroups of 8 waves that fit
+// two a CU overlap one tile's depthwise convs with the other's pointwise ones.
 template <typename ST, int QT, int C>
 static int launch_sub2_nf(const pk_sub_args* a, hipStream_t st) {
   const int F3 = half_up(half_up(half_up(a->n_mels)));
-  const int64_t tiles1 = (int64_t)a->max_out * ((F3 + QT - 1) / QT) * a->batch;
-  if constexpr (Sub2Geom<ST, 2, QT, C>::FITS) {
-    if (tiles1 > cu_count()) return launch_sub2<ST, 2, QT, C>(a, st);
+  const int64_t yt = (F3 + QT - 1) / QT;
+  const int64_t tiles1 = (int64_t)a->max_out * yt * a->batch;
+  const int64_t tiles2 = (int64_t)((a->max_out + 1) / 2) * yt * a->batch;
+  if constexpr (Sub2Geom<ST, 2, QT, C, 16>::FITS) {
+    if (tiles1 > cu_count()) {
+      if constexpr (C == 256 && Sub2Geom<ST, 2, QT, C, 8>::FITS) {  // the models' channel count
+        if (tiles2 >= (int64_t)kSub2PairTiles * cu_count()) return launch_sub2<ST, 2, QT, C, 8>(a, st);
+      }
+      return launch_sub2<ST, 2, QT, C, 16>(a, st);
+    }
   }
-  return launch_sub2<ST, 1, QT, C>(a, st);
+  return launch_sub2<ST, 1, QT, C, 16>(a, st);
 }
 
 template <typename ST, int QT>
