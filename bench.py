@@ -569,6 +569,10 @@ def encoder_bench(args, device) -> int:
             "streams": B,
             "x_realtime": round(1000.0 * chunk / 16000.0 / ms, 2),
             "keeps_up": bool(ms <= 1000.0 * chunk / 16000.0),
+            # device memory at its peak in this run, and the part of it that is the
+            # bench's own pcm input for every step (not state a server would hold)
+            "device_gib_peak": round(torch.cuda.max_memory_allocated(device) / 2**30, 2),
+            "device_gib_bench_pcm": round(pcm.numel() * pcm.element_size() / 2**30, 2),
         },
         "decode": {
             "step_ms": round(dec_ms, 4),

@@ -788,6 +788,7 @@ __device__ static inline uint32_t lo2(uint32_t x, uint32_t y) { return __builtin
 __device__ static inline uint32_t hi2(uint32_t x, uint32_t y) { return __builtin_amdgcn_perm(y, x, 0x07060302u); }
 
 constexpr int kSub2CG = 32;  // channels per group: one k-step of conv.3
+constexpr int kMaxGridYZ = 65535;  // largest y or z extent of a launch grid
 
 // conv.0 weights in LDS as the MFMA B operand: tap k of channel c at lane
 // (c mod 16, k / 4) of channel tile c / 16, 4 taps a lane, so the 16 lanes of
@@ -1383,7 +1384,6 @@ extern "C" int pk_fe_step(const pk_fe_args* a, void* stream) {
     return fail(PK_ERR_INVALID, "pk_fe_step: pcm_dtype %d", a->pcm_dtype);
   if (a->num_slots < 1) return fail(PK_ERR_INVALID, "pk_fe_step: num_slots %d", a->num_slots);
   if (a->samples_stride < a->max_new) return fail(PK_ERR_INVALID, "pk_fe_step: samples_stride < max_new");
-  if (a->batch > 65535) return fail(PK_ERR_UNSUPPORTED, "pk_fe_step: batch %d > 65535", a->batch);
   if (a->batch == 0 || (a->max_new == 0 && a->max_frames == 0)) return PK_OK;
   if (!a->streams || !a->sample_ring || !a->mel_ring || !a->window || !a->fb || !a->fb_range ||
       (a->max_new > 0 && !a->samples))
@@ -1414,11 +1414,20 @@ extern "C" int pk_fe_step(const pk_fe_args* a, void* stream) {
   k.seed_lo = (uint32_t)a->seed;
   k.seed_hi = (uint32_t)(a->seed >> 32);
   const int gx = a->max_frames > 0 ? (a->max_frames + kFeWaves - 1) / kFeWaves : 1;
-  if (a->pcm_dtype == PK_PCM_S16)
-    hipLaunchKernelGGL(fe_kernel<PK_PCM_S16>, dim3(gx, a->batch), dim3(64 * kFeWaves), 0, (hipStream_t)stream, k);
-  else
-    hipLaunchKernelGGL(fe_kernel<PK_PCM_F32>, dim3(gx, a->batch), dim3(64 * kFeWaves), 0, (hipStream_t)stream, k);
-  return check_launch("pk_fe_step");
+  // the streams in launches of at most kMaxGridYZ (the grid's y extent)
+  const size_t pcm_bytes = a->pcm_dtype == PK_PCM_S16 ? 2 : 4;
+  for (int b0 = 0; b0 < a->batch; b0 += kMaxGridYZ) {
+    const int nb = a->batch - b0 < kMaxGridYZ ? a->batch - b0 : kMaxGridYZ;
+    k.streams = a->streams + b0;
+    k.samples = a->samples ? (const char*)a->samples + (size_t)b0 * (size_t)a->samples_stride * pcm_bytes : nullptr;
+    if (a->pcm_dtype == PK_PCM_S16)
+      hipLaunchKernelGGL(fe_kernel<PK_PCM_S16>, dim3(gx, nb), dim3(64 * kFeWaves), 0, (hipStream_t)stream, k);
+    else
+      hipLaunchKernelGGL(fe_kernel<PK_PCM_F32>, dim3(gx, nb), dim3(64 * kFeWaves), 0, (hipStream_t)stream, k);
+    const int rc = check_launch("pk_fe_step");
+    if (rc != PK_OK) return rc;
+  }
+  return PK_OK;
 }
 
 extern "C" int pk_subsample(const pk_sub_args* a, void* stream) {
@@ -1440,17 +1449,28 @@ extern "C" int pk_subsample(const pk_sub_args* a, void* stream) {
     return fail(PK_ERR_INVALID, "pk_subsample: NULL pointer");
   if (!aligned16(a->w3) || !aligned16(a->w6))
     return fail(PK_ERR_INVALID, "pk_subsample: pointwise weights must be 16-byte aligned");
-  if (a->batch > 65535) return fail(PK_ERR_UNSUPPORTED, "pk_subsample: batch %d > 65535", a->batch);
   DeviceGuard dg(a->device);
   if (!dg.ok) return fail(PK_ERR_HIP, "pk_subsample: cannot select device %d", a->device);
   const hipStream_t st = (hipStream_t)stream;
   const int F3 = half_up(half_up(half_up(a->n_mels)));
-  switch (a->dtype) {
-    case PK_DTYPE_F16:
-      return F3 <= 11 ? launch_sub2_c<_Float16, 11>(a, st) : launch_sub2_c<_Float16, 17>(a, st);
-    case PK_DTYPE_BF16:
-      return F3 <= 11 ? launch_sub2_c<bf16_t, 11>(a, st) : launch_sub2_c<bf16_t, 17>(a, st);
-    default:
-      return launch_sub_c<float, 6>(a, st);
+  // the stream records in launches of at most kMaxGridYZ (the grid's z extent);
+  // every output row is addressed through its record
+  pk_sub_args part = *a;
+  for (int b0 = 0; b0 < a->batch; b0 += kMaxGridYZ) {
+    part.streams = a->streams + b0;
+    part.batch = a->batch - b0 < kMaxGridYZ ? a->batch - b0 : kMaxGridYZ;
+    int rc;
+    switch (a->dtype) {
+      case PK_DTYPE_F16:
+        rc = F3 <= 11 ? launch_sub2_c<_Float16, 11>(&part, st) : launch_sub2_c<_Float16, 17>(&part, st);
+        break;
+      case PK_DTYPE_BF16:
+        rc = F3 <= 11 ? launch_sub2_c<bf16_t, 11>(&part, st) : launch_sub2_c<bf16_t, 17>(&part, st);
+        break;
+      default:
+        rc = launch_sub_c<float, 6>(&part, st);
+    }
+    if (rc != PK_OK) return rc;
   }
+  return PK_OK;
 }

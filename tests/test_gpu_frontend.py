@@ -309,3 +309,55 @@ def test_pre_encoder_rejects_oversized_pushes(cuda):
     pcm = torch.zeros((1, 8000), dtype=torch.int16, device=cuda)
     with pytest.raises(RuntimeError, match="ring"):
         pre._features(np.array([0]), pcm, 8000, False)
+
+
+def test_front_end_batch_over_one_launch(cuda):
+    """65,540 streams in one step: pk_fe_step and pk_subsample take more
+    streams than one launch grid holds (65,535 along its y / z extent) in
+    several launches.  Every stream gets the same pcm without dither, so every
+    stream's log-mel rows and subsampling output rows (before the ``out``
+    Linear, whose library GEMM may round differently at another row count)
+    equal those of the same signal run alone (4 streams in a batch), the
+    streams past the first launch included."""
+    from parakeet_amd import ops
+
+    B, Fm, D, C = 65540, 80, 64, 256
+    dt = torch.float16
+    m = _module(C, Fm, D, dt, cuda, seed=5)
+    sig = _pcm(1440 + 2 * 2560, seed=31)
+    chunks = [sig[:1440], sig[1440:4000], sig[4000:6560]]
+
+    def run(n):
+        fx = FeatureExtractor(n_mels=Fm, dither=0.0, device=cuda)
+        pre = PreEncoder(fx, m, num_slots=n, device=cuda)
+        slots = np.arange(n)
+        for s in slots:
+            pre.reset_slot(s)
+        out = []
+        for ch in chunks:
+            pcm = torch.from_numpy(np.ascontiguousarray(np.broadcast_to(ch, (n, len(ch))))).to(cuda)
+            plan, sel, out_row = pre._features(slots, pcm, len(ch), False)
+            n_out = plan[6]
+            R = int(n_out.sum())
+            flat = torch.empty((R, C * m.final_freq_dim), dtype=dt, device=cuda)
+            if R:
+                ops.subsample(pre.hdr[32 * n :], len(sel), pre.mel_ring, True, m.conv_weights(), flat,
+                              max_out=int(n_out.max()))
+            out.append((flat, n_out.copy(), out_row.copy()))
+        torch.cuda.synchronize()
+        return pre, out
+
+    small_pre, small = run(4)
+    big_pre, big = run(B)
+    n_rows = 0
+    for (fs_, cs, rs), (fb_, cb, rb) in zip(small, big):
+        assert (cb == cs[0]).all()
+        ref = fs_[rs[0] : rs[0] + cs[0]].view(torch.int16)
+        for b in (0, 1, 65534, 65535, 65536, B - 1):
+            got = fb_[rb[b] : rb[b] + cb[b]].view(torch.int16)
+            assert torch.equal(got, ref), f"stream {b}: subsampling rows differ"
+        n_rows += int(cs[0])
+    assert n_rows > 0
+    ref_mel = small_pre.mel_ring[0]
+    for b in (65534, 65535, B - 1):
+        assert torch.equal(big_pre.mel_ring[b], ref_mel), f"stream {b}: log-mel ring differs"
