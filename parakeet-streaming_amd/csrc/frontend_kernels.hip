@@ -1294,18 +1294,6 @@ static int launch_sub_c(const pk_sub_args* a, hipStream_t st) {
   }
 }
 
-// CUs of the current device, read once per device
-static int cu_count() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] <= 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
-}
 
 // fp16 / bf16: one tile of NF output frames x QT columns a workgroup of W
 // waves (one workgroup a CU for W 16, two for W 8)

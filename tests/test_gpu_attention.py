@@ -210,3 +210,49 @@ def test_state_mask_identical_to_mask_tensor(cuda, left, right, dtype):
     out_s1 = ops.paged_relpos_attn(q, k, v, pos, bu, bv, None, num_heads=H, left=left, pages=pages, append=False, mask_state=st1)
     assert torch.equal(out_m1, out_s1)
     torch.cuda.synchronize()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B", [130, 200, 256])
+def test_batch_split_is_bit_exact(cuda, B):
+    """At head_dim 128 (two streams a workgroup) every stream's output of a
+    launch over the whole batch equals, bit for bit, that of the same streams
+    launched 64 at a time (odd block sizes included: 130 = 2 x 64 + 2), and
+    the oracle's within tolerance; the fused append writes exactly the
+    frames."""
+    dtype, H, dk, left, right, P = torch.bfloat16, 8, 128, 70, 1, 16
+    print(f"\n[attn batch split] B={B}", flush=True)
+    sc = PagedScenario(cuda, dtype, B=B, layers=1, d_model=H * dk, left=left, right=right, page_size=P, seed=B)
+    pos, bu, bv = _relpos(sc, H, B)
+    T = sc.T
+    proc = np.zeros(B, dtype=np.int64)
+    for step in range(40):
+        sc.open_step()
+        cl = np.minimum(proc, left)
+        _, mask_np = om.create_streaming_masks(T, cl, proc, np.full(B, T), (left, right))
+        mask = torch.from_numpy(mask_np).to(cuda)
+        x, (q, k, v) = sc.frames()
+        args = dict(num_heads=H, left=left, layer=0)
+        if step % 8 == 7:  # the whole batch against blocks of 64 streams, nothing appended
+            whole = ops.paged_relpos_attn(q, k, v, pos, bu, bv, mask, pages=sc.pages, append=False, **args)
+            for b0 in range(0, B, 64):
+                b1 = min(B, b0 + 64)
+                part_pages = ops.PagedKV(sc.k_pages, sc.v_pages, sc.rows[b0:b1], sc.M)
+                part = ops.paged_relpos_attn(q[b0:b1], k[b0:b1], v[b0:b1], pos, bu, bv, mask[b0:b1],
+                                             pages=part_pages, append=False, **args)
+                assert torch.equal(_bits16(whole[b0:b1]), _bits16(part)), f"step {step}: streams {b0}..{b1 - 1} differ"
+        out = ops.paged_relpos_attn(q, k, v, pos, bu, bv, mask, pages=sc.pages, append=True, **args)
+        dk_win, dv_win = sc.dense_update(0, k, v)
+        if step in (0, 39):
+            ref = oa.relpos_attention(to_np64(q), dk_win, dv_win, to_np64(pos), to_np64(bu), to_np64(bv), mask_np, H)
+            err = np.abs(to_np64(out) - ref).max()
+            assert err <= TOL[dtype], f"step {step}: max abs err {err:.3e}"
+        gk, gv = ops.kv_gather(sc.pages, 0, B, sc.L, T)
+        assert torch.equal(gk.cpu(), torch.from_numpy(np.ascontiguousarray(dk_win)).to(dtype))
+        assert torch.equal(gv.cpu(), torch.from_numpy(np.ascontiguousarray(dv_win)).to(dtype))
+        proc += T
+    torch.cuda.synchronize()
+
+
+def _bits16(t: torch.Tensor) -> torch.Tensor:
+    return t.contiguous().view(torch.int16)
