@@ -36,6 +36,7 @@ constexpr int kNfft = 512;
 constexpr int kCplx = kNfft / 2;  // complex FFT points
 constexpr int kBins = kNfft / 2 + 1;
 constexpr int kFeWaves = 4;  // frames per workgroup
+constexpr int kMaxGridYZ = 65535;  // largest y or z extent of a launch grid
 constexpr int kMaxMels = 128;
 
 struct FeK {
@@ -788,7 +789,6 @@ __device__ static inline uint32_t lo2(uint32_t x, uint32_t y) { return __builtin
 __device__ static inline uint32_t hi2(uint32_t x, uint32_t y) { return __builtin_amdgcn_perm(y, x, 0x07060302u); }
 
 constexpr int kSub2CG = 32;  // channels per group: one k-step of conv.3
-constexpr int kMaxGridYZ = 65535;  // largest y or z extent of a launch grid
 
 // conv.0 weights in LDS as the MFMA B operand: tap k of channel c at lane
 // (c mod 16, k / 4) of channel tile c / 16, 4 taps a lane, so the 16 lanes of
