@@ -103,11 +103,21 @@ __device__ static inline void dft4(float2* v) {
 
 constexpr int kMaxWin = kNfft;
 constexpr int kMaxHop = kNfft;
-constexpr int kSpanMax = (kFeWaves - 1) * kMaxHop + kMaxWin + 1;  // samples the frames of a workgroup read
 constexpr int kBand = 32;  // filterbank weights per band staged in LDS
+// FPW frames a wave: 1, or 4 at large batches (the workgroup's staging of
+// twiddles, window and filterbank then serves 16 frames), which stages the
+// samples of 16 frames and so takes hops up to kFeHopWide
+constexpr int kFeHopWide = 192;
+constexpr int kFeWideRounds = 8;  // workgroups a CU from which the 4-frames-a-wave form is used
+template <int FPW>
+struct FeGeom {
+  static constexpr int HOP = FPW == 1 ? kMaxHop : kFeHopWide;
+  static constexpr int SPAN = (kFeWaves * FPW - 1) * HOP + kMaxWin + 1;  // samples the frames of a workgroup read
+};
 
-template <int PCM>
+template <int PCM, int FPW>
 __global__ void __launch_bounds__(64 * kFeWaves) fe_kernel(const FeK p) {
+  constexpr int kSpanMax = FeGeom<FPW>::SPAN;
   __shared__ float2 tw[kCplx];   // e^{-2 pi i m / 256}
   __shared__ float2 tw2[kBins];  // e^{-2 pi i k / 512}, k <= 256
   __shared__ float2 buf[kFeWaves][kCplx];
@@ -148,9 +158,9 @@ __global__ void __launch_bounds__(64 * kFeWaves) fe_kernel(const FeK p) {
     for (int u = 0; u < kCopy; ++u)
       if (i0 + u * stride < s.n_new) ring[(s.sample_base + i0 + u * stride) & rmask] = x[u];
   }
-  const int j0 = blockIdx.x * kFeWaves;
+  const int j0 = blockIdx.x * kFeWaves * FPW;
   if (j0 >= s.n_frames) return;  // no frame for this workgroup
-  const int nf = min(kFeWaves, s.n_frames - j0);
+  const int nf = min(kFeWaves * FPW, s.n_frames - j0);
   const int wl = (kNfft - p.win) / 2;
   const int64_t f0 = (int64_t)s.frame0 + j0;
   const int64_t span0 = f0 * p.hop - kNfft / 2 + wl - 1;  // global index of xs[0]
@@ -222,64 +232,69 @@ __global__ void __launch_bounds__(64 * kFeWaves) fe_kernel(const FeK p) {
   __syncthreads();
 
   const int wave = tid >> 6, lane = tid & 63;
-  if (wave >= nf) return;  // no barrier below this point
-  const int64_t f = f0 + wave;
-  const int64_t base = f * p.hop - kNfft / 2;
-  const int off = wave * p.hop - wl + 1;  // xs index of frame sample n is off + n
-  // windowed, pre-emphasised frame sample n (0 <= n < 512)
-  auto frame_val = [&](int n) -> float {
-    if (n < wl || n >= wl + p.win) return 0.f;
-    const int64_t i = base + n;
-    if (i < 0 || i >= total) return 0.f;
-    return (xs[off + n] - p.preemph * xs[off + n - 1]) * win_s[n - wl];
-  };
+  // the wave's frames fw = wave + kFeWaves r of the workgroup's nf; no barrier
+  // below this point
+#pragma unroll 1
+  for (int fw = wave; fw < nf; fw += kFeWaves) {
+    const int64_t f = f0 + fw;
+    const int64_t base = f * p.hop - kNfft / 2;
+    const int off = fw * p.hop - wl + 1;  // xs index of frame sample n is off + n
+    // windowed, pre-emphasised frame sample n (0 <= n < 512)
+    auto frame_val = [&](int n) -> float {
+      if (n < wl || n >= wl + p.win) return 0.f;
+      const int64_t i = base + n;
+      if (i < 0 || i >= total) return 0.f;
+      return (xs[off + n] - p.preemph * xs[off + n - 1]) * win_s[n - wl];
+    };
 
-  // z[n] = v[2n] + i v[2n+1]; lane holds z[lane + 64 r]
-  float2 v[4];
+    // z[n] = v[2n] + i v[2n+1]; lane holds z[lane + 64 r]
+    float2 v[4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int n = 2 * (lane + 64 * r);
-    v[r] = make_float2(frame_val(n), frame_val(n + 1));
-  }
-  float2* bw = buf[wave];
-  // radix-4 Stockham passes: span Ns = 1, 4, 16, 64
-#pragma unroll
-  for (int pass = 0; pass < 4; ++pass) {
-    const int Ns = 1 << (2 * pass);
-    const int k = lane & (Ns - 1);
-    if (pass) {
-#pragma unroll
-      for (int r = 1; r < 4; ++r) v[r] = cmul(v[r], tw[(r * k * 64) >> (2 * pass)]);
+    for (int r = 0; r < 4; ++r) {
+      const int n = 2 * (lane + 64 * r);
+      v[r] = make_float2(frame_val(n), frame_val(n + 1));
     }
-    dft4(v);
-    const int d = ((lane >> (2 * pass)) << (2 * pass + 2)) + k;
-    wave_lds_sync();  // the previous pass's reads of bw are done
+    float2* bw = buf[wave];
+    // radix-4 Stockham passes: span Ns = 1, 4, 16, 64
 #pragma unroll
-    for (int r = 0; r < 4; ++r) bw[d + r * Ns] = v[r];
+    for (int pass = 0; pass < 4; ++pass) {
+      const int Ns = 1 << (2 * pass);
+      const int k = lane & (Ns - 1);
+      if (pass) {
+#pragma unroll
+        for (int r = 1; r < 4; ++r) v[r] = cmul(v[r], tw[(r * k * 64) >> (2 * pass)]);
+      }
+      dft4(v);
+      const int d = ((lane >> (2 * pass)) << (2 * pass + 2)) + k;
+      wave_lds_sync();  // the previous pass's reads of bw are done
+#pragma unroll
+      for (int r = 0; r < 4; ++r) bw[d + r * Ns] = v[r];
+      wave_lds_sync();
+      if (pass < 3) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = bw[lane + 64 * r];
+      }
+    }
+    // real-input bins: X[k] = E[k] + W^k O[k], E/O from Z[k] and conj(Z[256-k])
+    float* pwv = pw[wave];
+    for (int kk = lane; kk < kBins; kk += 64) {
+      const float2 zk = bw[kk & (kCplx - 1)], zm = bw[(kCplx - kk) & (kCplx - 1)];
+      const float er = 0.5f * (zk.x + zm.x), ei = 0.5f * (zk.y - zm.y);
+      const float orr = 0.5f * (zk.y + zm.y), oi = -0.5f * (zk.x - zm.x);
+      const float2 w = tw2[kk];
+      const float xr = er + (w.x * orr - w.y * oi), xi = ei + (w.x * oi + w.y * orr);
+      pwv[kk] = xr * xr + xi * xi;
+    }
     wave_lds_sync();
-    if (pass < 3) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) v[r] = bw[lane + 64 * r];
+    float* mrow = p.mel + ((int64_t)s.slot * p.mel_rows + (f & (p.mel_rows - 1))) * p.n_mels;
+    for (int m = lane; m < p.n_mels; m += 64) {
+      const int lo = rng_s[m].x, hi = rng_s[m].y;
+      float acc = 0.f;
+      for (int kk = lo; kk < hi; ++kk)
+        acc += (kk - lo < kBand ? fbw[m][kk - lo] : p.fb[(int64_t)m * kBins + kk]) * pwv[kk];
+      mrow[m] = logf(acc + p.guard);
     }
-  }
-  // real-input bins: X[k] = E[k] + W^k O[k], E/O from Z[k] and conj(Z[256-k])
-  float* pwv = pw[wave];
-  for (int kk = lane; kk < kBins; kk += 64) {
-    const float2 zk = bw[kk & (kCplx - 1)], zm = bw[(kCplx - kk) & (kCplx - 1)];
-    const float er = 0.5f * (zk.x + zm.x), ei = 0.5f * (zk.y - zm.y);
-    const float orr = 0.5f * (zk.y + zm.y), oi = -0.5f * (zk.x - zm.x);
-    const float2 w = tw2[kk];
-    const float xr = er + (w.x * orr - w.y * oi), xi = ei + (w.x * oi + w.y * orr);
-    pwv[kk] = xr * xr + xi * xi;
-  }
-  wave_lds_sync();
-  float* mrow = p.mel + ((int64_t)s.slot * p.mel_rows + (f & (p.mel_rows - 1))) * p.n_mels;
-  for (int m = lane; m < p.n_mels; m += 64) {
-    const int lo = rng_s[m].x, hi = rng_s[m].y;
-    float acc = 0.f;
-    for (int kk = lo; kk < hi; ++kk)
-      acc += (kk - lo < kBand ? fbw[m][kk - lo] : p.fb[(int64_t)m * kBins + kk]) * pwv[kk];
-    mrow[m] = logf(acc + p.guard);
+    wave_lds_sync();  // this frame's reads of bw and pwv before the next frame's writes
   }
 }
 
@@ -1401,17 +1416,31 @@ extern "C" int pk_fe_step(const pk_fe_args* a, void* stream) {
   k.guard = a->log_guard;
   k.seed_lo = (uint32_t)a->seed;
   k.seed_hi = (uint32_t)(a->seed >> 32);
-  const int gx = a->max_frames > 0 ? (a->max_frames + kFeWaves - 1) / kFeWaves : 1;
+  // four frames a wave when the batch fills the CUs several times over with
+  // such workgroups (and the hop fits their sample staging), one otherwise
+  const int wide_frames = 4 * kFeWaves;
+  const int64_t gx4 = a->max_frames > 0 ? (a->max_frames + wide_frames - 1) / wide_frames : 1;
+  const bool wide = a->hop <= kFeHopWide && gx4 * a->batch >= (int64_t)kFeWideRounds * cu_count();
+  const int gx = a->max_frames > 0 ? (a->max_frames + (wide ? wide_frames : kFeWaves) - 1) / (wide ? wide_frames : kFeWaves) : 1;
   // the streams in launches of at most kMaxGridYZ (the grid's y extent)
   const size_t pcm_bytes = a->pcm_dtype == PK_PCM_S16 ? 2 : 4;
   for (int b0 = 0; b0 < a->batch; b0 += kMaxGridYZ) {
     const int nb = a->batch - b0 < kMaxGridYZ ? a->batch - b0 : kMaxGridYZ;
     k.streams = a->streams + b0;
     k.samples = a->samples ? (const char*)a->samples + (size_t)b0 * (size_t)a->samples_stride * pcm_bytes : nullptr;
-    if (a->pcm_dtype == PK_PCM_S16)
-      hipLaunchKernelGGL(fe_kernel<PK_PCM_S16>, dim3(gx, nb), dim3(64 * kFeWaves), 0, (hipStream_t)stream, k);
-    else
-      hipLaunchKernelGGL(fe_kernel<PK_PCM_F32>, dim3(gx, nb), dim3(64 * kFeWaves), 0, (hipStream_t)stream, k);
+    const dim3 grid(gx, nb), block(64 * kFeWaves);
+    const hipStream_t st = (hipStream_t)stream;
+    if (a->pcm_dtype == PK_PCM_S16) {
+      if (wide)
+        hipLaunchKernelGGL((fe_kernel<PK_PCM_S16, 4>), grid, block, 0, st, k);
+      else
+        hipLaunchKernelGGL((fe_kernel<PK_PCM_S16, 1>), grid, block, 0, st, k);
+    } else {
+      if (wide)
+        hipLaunchKernelGGL((fe_kernel<PK_PCM_F32, 4>), grid, block, 0, st, k);
+      else
+        hipLaunchKernelGGL((fe_kernel<PK_PCM_F32, 1>), grid, block, 0, st, k);
+    }
     const int rc = check_launch("pk_fe_step");
     if (rc != PK_OK) return rc;
   }

@@ -361,3 +361,34 @@ def test_front_end_batch_over_one_launch(cuda):
     ref_mel = small_pre.mel_ring[0]
     for b in (65534, 65535, B - 1):
         assert torch.equal(big_pre.mel_ring[b], ref_mel), f"stream {b}: log-mel ring differs"
+
+
+@pytest.mark.parametrize("dither", [0.0, 1e-5])
+def test_features_four_frames_a_wave_form(cuda, dither):
+    """With several workgroups a CU of 16 frames (here 2,100 streams of 16
+    frames), pk_fe_step takes four frames a wave, so a workgroup stages its
+    twiddles, window and filterbank once for 16 frames.  The log-mel rows of
+    four streams equal, bit for bit, those of the same four streams stepped
+    alone (one frame a wave), dither included (every stream's noise is a
+    function of its own sample indices)."""
+    S, Fm = 2100, 80
+    sig = _pcm(1440 + 2 * 2560, seed=41)
+    chunks = [sig[:1440], sig[1440:4000], sig[4000:6560]]
+    probe = np.array([0, 1, 1000, S - 1])
+
+    def run(slots):
+        fx = FeatureExtractor(n_mels=Fm, dither=dither, seed=9, device=cuda)
+        pre = PreEncoder(fx, None, num_slots=S, device=cuda)
+        for s in range(S):
+            pre.reset_slot(s)
+        for ch in chunks:
+            pcm = torch.from_numpy(np.ascontiguousarray(np.broadcast_to(ch, (len(slots), len(ch))))).to(cuda)
+            plan, _, _ = pre._features(slots, pcm, len(ch), False)
+        torch.cuda.synchronize()
+        return pre
+
+    big = run(np.arange(S))
+    small = run(probe)
+    assert int(big.emitted[0]) > 16  # three pushes emitted more frames than one
+    for s in probe:
+        assert torch.equal(big.mel_ring[s], small.mel_ring[s]), f"stream {s}: log-mel rows differ"
