@@ -554,18 +554,24 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
   typedef typename Mma<ST>::H H;
 
   // The staged position rows are dead once the dot products are in LDS (the
-  // second barrier of a pass); the P.V staging (V tiles and the 16-bit high
-  // and low parts of the probabilities, [hi|lo][query][slot]) reuses their
-  // space.
+  // second barrier of a pass, when a stream's waves exchange their partial
+  // dot products); there the P.V staging (V tiles and the 16-bit high and low
+  // parts of the probabilities, [hi|lo][query][slot]) reuses their space.
+  // With one wave a stream (head_dim 64) the waves of a workgroup share only
+  // the position rows, so the P.V staging gets its own space and the waves go
+  // on without that barrier.
   constexpr int POS_BYTES = PROWS * PSTRIDE;
   constexpr int PV_BYTES = NW * 16 * VSTRIDE + NW * 2 * TQ * KT * 2;
-  __shared__ __attribute__((aligned(16))) uint8_t stage_lds[POS_BYTES > PV_BYTES ? POS_BYTES : PV_BYTES];
+  constexpr bool PV_OWN = SPLIT == 1;
+  constexpr int PV_OFF = PV_OWN ? POS_BYTES : 0;
+  constexpr int STAGE_BYTES = PV_OWN ? POS_BYTES + PV_BYTES : (POS_BYTES > PV_BYTES ? POS_BYTES : PV_BYTES);
+  __shared__ __attribute__((aligned(16))) uint8_t stage_lds[STAGE_BYTES];
   __shared__ float bd_lds[NW][TQ][PROWS];
   __shared__ float ac_lds[NW][TQ][KT];
   uint8_t* const pos_lds = stage_lds;
-  uint8_t (*const v_lds)[16 * VSTRIDE] = reinterpret_cast<uint8_t (*)[16 * VSTRIDE]>(stage_lds);
+  uint8_t (*const v_lds)[16 * VSTRIDE] = reinterpret_cast<uint8_t (*)[16 * VSTRIDE]>(stage_lds + PV_OFF);
   uint16_t (*const p_lds)[2][TQ][KT] =
-      reinterpret_cast<uint16_t (*)[2][TQ][KT]>(stage_lds + NW * 16 * VSTRIDE);
+      reinterpret_cast<uint16_t (*)[2][TQ][KT]>(stage_lds + PV_OFF + NW * 16 * VSTRIDE);
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -841,7 +847,10 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    __syncthreads();  // partial dot products of the stream's waves in LDS
+    if constexpr (PV_OWN)
+      wave_lds_sync();  // the wave's own dot products in LDS
+    else
+      __syncthreads();  // partial dot products of the stream's waves in LDS
 
     // ---- scores: lane handles slots lane + 64*r; online softmax
     float s[SK][TQ];
