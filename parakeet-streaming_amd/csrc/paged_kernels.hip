@@ -462,21 +462,23 @@ __device__ static inline V split16(const float* x, bool low) {
   return __builtin_bit_cast(V, out);
 }
 
-__device__ static inline float lane0(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
+__device__ static inline float lane_at(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
 }
-
-// Max / sum over all 64 lanes, result in every lane.
+// Max / sum over all 64 lanes as a wave-uniform value: within each row of 16
+// lanes by DPP, then the rows' lanes 0, 16, 32 and 48 read as scalars (no LDS
+// round trip); the sum adds (row 0 + row 1) + (row 2 + row 3).
 __device__ static inline float wave_max(float v) {
   v = fmaxf(v, dpp_f<0xB1>(v));
   v = fmaxf(v, dpp_f<0x4E>(v));
   v = fmaxf(v, dpp_f<0x141>(v));
   v = fmaxf(v, dpp_f<0x140>(v));
-  v = fmaxf(v, __shfl_xor(v, 16));
-  v = fmaxf(v, __shfl_xor(v, 32));
-  return lane0(v);
+  return fmaxf(fmaxf(lane_at(v, 0), lane_at(v, 16)), fmaxf(lane_at(v, 32), lane_at(v, 48)));
 }
-__device__ static inline float wave_sum(float v) { return lane0(group_sum<64>(v)); }
+__device__ static inline float wave_sum(float v) {
+  v = group_sum<16>(v);
+  return (lane_at(v, 0) + lane_at(v, 16)) + (lane_at(v, 32) + lane_at(v, 48));
+}
 
 // Index-mode buffer access: a resource describes `nrows` rows of `stride`
 // bytes; a row index >= nrows reads zeros and drops stores (the hardware range
@@ -792,6 +794,25 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
         else
           kr[kt][ks] = pk_buffer_load_x4(r_kp, prow[kt], kg * 16, blk_soff + ks * blk_step, 0);
       }
+    // which scores of the pass take no value (a slot past the window or the
+    // pass, a query past the chunk: bit r * TQ + ii of neg_bits) or the mask's
+    // -1e5 term (the streaming rule: msk_bits), for slot lane + 64 r of query
+    // ii: none of it waits for the K rows, so it is done while they are in flight
+    static_assert(SK * TQ <= 32, "score bits");
+    uint32_t neg_bits = 0u, msk_bits = 0u;
+#pragma unroll
+    for (int r = 0; r < SK; ++r) {
+      const int sl = lane + 64 * r;
+      const int j = jb + min(sl, KT - 1);
+      const bool valid = sl < KT && j < p.Lk;
+#pragma unroll
+      for (int ii = 0; ii < TQ; ++ii) {
+        const uint32_t bit = 1u << (r * TQ + ii);
+        if (!(valid && ii < nq)) neg_bits |= bit;
+        if (mask_mode == 2 && sm.masked(i0 + ii, qchunk[ii], j)) msk_bits |= bit;
+      }
+    }
+    asm volatile("" ::"v"(neg_bits), "v"(msk_bits));
     // the wave's position-row loads (issued before any K row, and at least
     // NT*KS vector loads ago) are in LDS: wait for them, not for the K rows,
     // before the barrier that makes every wave's part visible
@@ -852,46 +873,58 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
     else
       __syncthreads();  // partial dot products of the stream's waves in LDS
 
-    // ---- scores: lane handles slots lane + 64*r; online softmax
-    float s[SK][TQ];
+    // ---- scores: lane handles slots lane + 64*r; online softmax.  Every LDS
+    //      read of the partial products is issued first, then selects (the
+    //      conditions are the bits computed above), so no read waits behind a
+    //      branch; the queries' reductions run side by side
+    float acv[SK][TQ], bdv[SK][TQ];
 #pragma unroll
     for (int r = 0; r < SK; ++r) {
-      const int sl = lane + 64 * r;
-      const int slc = min(sl, KT - 1);
-      const int j = jb + slc;
-      const bool valid = sl < KT && j < p.Lk;
+      const int slc = min(lane + 64 * r, KT - 1);
 #pragma unroll
       for (int ii = 0; ii < TQ; ++ii) {
-        float ac = 0.f, bd = 0.f;
-        // (q+v).pos row of column j for query i0 + ii, relative to the staged rows
+        // (q+v).pos row of column jb + slc for query i0 + ii, relative to the staged rows
         const int prw = min(slc + TQ - 1 - ii, PROWS - 1);
+        float ac = 0.f, bd = 0.f;
 #pragma unroll
         for (int x = 0; x < SPLIT; ++x) {
           ac += ac_lds[w0 + x][ii][slc];
           bd += bd_lds[w0 + x][ii][prw];
         }
-        bool msk = false;
-        if (mask_mode == 1) msk = mk[r][ii] != 0;
-        if (mask_mode == 2) msk = sm.masked(i0 + ii, qchunk[ii], j);
-        const float sc = msk ? fmaf(ac, p.scale, MASKED) : (ac + bd) * p.scale;
-        s[r][ii] = (valid && ii < nq) ? sc : NEG;
+        acv[r][ii] = ac;
+        bdv[r][ii] = bd;
       }
     }
-    float corr[TQ];
+    float s[SK][TQ];
+#pragma unroll
+    for (int r = 0; r < SK; ++r)
+#pragma unroll
+      for (int ii = 0; ii < TQ; ++ii) {
+        const uint32_t bit = 1u << (r * TQ + ii);
+        const bool msk = mask_mode == 1 ? mk[r][ii] != 0 : (msk_bits & bit) != 0u;
+        const float sc = msk ? fmaf(acv[r][ii], p.scale, MASKED) : (acv[r][ii] + bdv[r][ii]) * p.scale;
+        s[r][ii] = (neg_bits & bit) != 0u ? NEG : sc;
+      }
+    float corr[TQ], mnew[TQ], lsum[TQ];
 #pragma unroll
     for (int ii = 0; ii < TQ; ++ii) {
       float tmax = NEG;
 #pragma unroll
       for (int r = 0; r < SK; ++r) tmax = fmaxf(tmax, s[r][ii]);
-      const float mnew = fmaxf(m_run[ii], wave_max(tmax));
-      corr[ii] = __builtin_amdgcn_exp2f(m_run[ii] - mnew);
-      m_run[ii] = mnew;
-      float lsum = 0.f;
+      mnew[ii] = tmax;
+    }
+#pragma unroll
+    for (int ii = 0; ii < TQ; ++ii) mnew[ii] = fmaxf(m_run[ii], wave_max(mnew[ii]));
+#pragma unroll
+    for (int ii = 0; ii < TQ; ++ii) {
+      corr[ii] = __builtin_amdgcn_exp2f(m_run[ii] - mnew[ii]);
+      m_run[ii] = mnew[ii];
+      lsum[ii] = 0.f;
 #pragma unroll
       for (int r = 0; r < SK; ++r) {
         const int sl = lane + 64 * r;
-        const float e = s[r][ii] > 0.5f * NEG ? __builtin_amdgcn_exp2f(s[r][ii] - mnew) : 0.f;
-        lsum += e;
+        const float e = s[r][ii] > 0.5f * NEG ? __builtin_amdgcn_exp2f(s[r][ii] - mnew[ii]) : 0.f;
+        lsum[ii] += e;
         if (sl < KT) {  // e = hi + lo in the operand type, exact to ~2^-17
           const H hi = (H)e;
           const H lo = (H)(e - (float)hi);
@@ -899,8 +932,9 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
           p_lds[wave][1][ii][sl] = __builtin_bit_cast(uint16_t, lo);
         }
       }
-      l_run[ii] = l_run[ii] * corr[ii] + wave_sum(lsum);
     }
+#pragma unroll
+    for (int ii = 0; ii < TQ; ++ii) l_run[ii] = l_run[ii] * corr[ii] + wave_sum(lsum[ii]);
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
       oacc[nt][0] *= corr[0];
