@@ -620,8 +620,10 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
   // ---------------- prologue: every load independent of the page table,
   //                  issued branch-free (absent inputs read a valid stand-in
   //                  address and are replaced afterwards)
-  const int32_t* hdr = paged ? p.pg.rows + (int64_t)b * p.pg.rows_stride
-                             : reinterpret_cast<const int32_t*>(p.q);
+  // (branch-free, so the row stride loads with the other kernel arguments
+  // rather than in a second round trip before the header's address is known)
+  const int64_t hdr_off = (int64_t)b * p.pg.rows_stride;
+  const int32_t* hdr = paged ? p.pg.rows + hdr_off : reinterpret_cast<const int32_t*>(p.q);
   const int hdr_a = hdr[0];
   int ring_lane = hdr[paged ? 1 + min(lane, M - 1) : 0];
   const int64_t* stp = mask_mode == 2 ? p.st_proc + b : reinterpret_cast<const int64_t*>(p.q);
