@@ -540,9 +540,13 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
   constexpr int TQ = 2;
   constexpr int KS = 2;            // 16x16x32 k-steps over the wave's 64 columns
   constexpr int KT = 16 * NT;      // slots (window columns) per pass
-  constexpr int NPT = NT + 1;      // position-row tiles: slot s of query ii reads row s + TQ-1-ii
-  constexpr int PROWS = 16 * NPT;
   constexpr int CHR = DK / 8;                   // 16-byte chunks per staged position row
+  // position-row tiles: slot s of query ii reads row s + TQ-1-ii.  A single
+  // pass holds at most KT - 1 keys (the host takes the multi-pass form for
+  // more), so its rows stay below KT, which at head_dim 128 are whole staging
+  // instructions: one tile fewer to stage ahead of the K rows
+  constexpr int NPT = (!MULTI && (16 * NT * CHR) % (64 * NW) == 0) ? NT : NT + 1;
+  constexpr int PROWS = 16 * NPT;
   constexpr int PSTRIDE = CHR * 16;             // bytes per staged position row (unpadded)
   constexpr int RPB = 16 / CHR;                 // staged rows per 256 bytes (all 64 banks)
   constexpr int PCH = (PROWS * CHR + NTH - 1) / NTH;  // staged chunks per thread
@@ -1255,7 +1259,9 @@ int launch_attn_mfma_t(const pk_attn_args* a, const AttnK<ST>& k, hipStream_t s)
 
 template <typename ST, int DK, int MODE>
 int launch_attn_mfma_mode(const pk_attn_args* a, const AttnK<ST>& k, hipStream_t s) {
-  if (k.tiles > 1) return launch_attn_mfma_t<ST, DK, MODE, true>(a, k, s);
+  // the single-pass form holds at most 16 * kMfmaTiles - 1 keys (its staged
+  // position rows stop at 16 * kMfmaTiles)
+  if (k.tiles > 1 || k.Lk > 16 * kMfmaTiles - 1) return launch_attn_mfma_t<ST, DK, MODE, true>(a, k, s);
   return launch_attn_mfma_t<ST, DK, MODE, false>(a, k, s);
 }
 

@@ -115,6 +115,16 @@ def test_random_masks_and_ragged_lengths(cuda):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("dk", [64, 128])
+def test_window_of_one_pass_edge(cuda, dk):
+    """Windows of 79 and 80 keys at T = 2: the single-pass form holds at most
+    79 (its staged position rows stop at 80); 80 keys go to the multi-pass
+    form in one pass."""
+    for left in (77, 78):
+        _run(cuda, torch.bfloat16, B=5, H=4, dk=dk, left=left, right=1, P=16, steps=45)
+
+
+@pytest.mark.gpu
 def test_long_window_multi_tile(cuda):
     # left context long enough that the window needs several tiles
     _run(cuda, torch.float16, B=2, H=8, dk=64, left=600, right=1, P=16, steps=6, layers=1)
