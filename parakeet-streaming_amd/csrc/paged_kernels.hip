@@ -624,20 +624,11 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
   // ---------------- prologue: every load independent of the page table,
   //                  issued branch-free (absent inputs read a valid stand-in
   //                  address and are replaced afterwards)
-  // (branch-free, so the row stride loads with the other kernel arguments
-  // rather than in a second round trip before the header's address is known)
-  const int64_t hdr_off = (int64_t)b * p.pg.rows_stride;
-  const int32_t* hdr = paged ? p.pg.rows + hdr_off : reinterpret_cast<const int32_t*>(p.q);
-  const int hdr_a = hdr[0];
-  int ring_lane = hdr[paged ? 1 + min(lane, M - 1) : 0];
-  const int64_t* stp = mask_mode == 2 ? p.st_proc + b : reinterpret_cast<const int64_t*>(p.q);
-  const int64_t* stc = mask_mode == 2 ? p.st_cl + b : stp;
-  const int64_t* stn = (mask_mode == 2 && p.st_len) ? p.st_len + b : stp;
-  const int64_t st_pr_v = *stp, st_cl_v = *stc, st_n_v = *stn;
-  const int32_t nact_v = p.nact ? *p.nact : p.B;
   // A operand source: row m = q16 is (q+u)_hi, (q+u)_lo, (q+v)_hi, (q+v)_lo of
   // query m & 1 for m < 8, zero above; element e of k-step ks is column
-  // ks*32 + kg*8 + e of the wave's 64
+  // ks*32 + kg*8 + e of the wave's 64.  Loaded first: vector loads complete in
+  // issue order, so q and the biases are in when the block-table header is,
+  // and the operand is built as soon as the header allows the K rows
   const int a_ii = q16 & 1;
   const int a_kind = q16 >> 1;  // 0 u-hi, 1 u-lo, 2 v-hi, 3 v-lo, >= 4 zero
   u32x4 qraw[KS], braw[KS];
@@ -651,6 +642,17 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
       braw[ks] = ld16(brow + ks * 32);
     }
   }
+  // (branch-free, so the row stride loads with the other kernel arguments
+  // rather than in a second round trip before the header's address is known)
+  const int64_t hdr_off = (int64_t)b * p.pg.rows_stride;
+  const int32_t* hdr = paged ? p.pg.rows + hdr_off : reinterpret_cast<const int32_t*>(p.q);
+  const int hdr_a = hdr[0];
+  int ring_lane = hdr[paged ? 1 + min(lane, M - 1) : 0];
+  const int64_t* stp = mask_mode == 2 ? p.st_proc + b : reinterpret_cast<const int64_t*>(p.q);
+  const int64_t* stc = mask_mode == 2 ? p.st_cl + b : stp;
+  const int64_t* stn = (mask_mode == 2 && p.st_len) ? p.st_len + b : stp;
+  const int64_t st_pr_v = *stp, st_cl_v = *stc, st_n_v = *stn;
+  const int32_t nact_v = p.nact ? *p.nact : p.B;
   // the last slot any query of the pass at jb reads, and the position-row
   // tiles it needs (slot s of query ii reads staged row s + TQ - 1 - ii)
   auto pass_tiles = [&](int jb) {
