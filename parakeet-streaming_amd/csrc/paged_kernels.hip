@@ -526,8 +526,10 @@ __device__ static inline __amdgpu_buffer_rsrc_t rows_rsrc(const void* base, int 
 //     parts), B = 16 V rows x 16 columns transposed on the way out of LDS by
 //     ds_read_b64_tr_b16 (the wave writes its V tile row-major and each 16-lane
 //     group reads 4 rows x 16 columns back transposed);
-//   * the fused append stores the lanes holding this step's frames into their
-//     pages (query group 0).
+//   * the fused append stores this step's frame rows into their pages (query
+//     group 0): a lane holds at most one frame column a pass (chunks of at
+//     most 16 frames), loaded once and selected into the tile that holds it,
+//     so every load and store is branch-free.
 // Pages hold 64-byte column blocks ([page][block][page_size][32 elements]),
 // so one k-step load of a 16-slot tile reads 16 rows x 64 bytes of one block:
 // 1 KB of contiguous memory when the 16 slots share a page.
@@ -775,33 +777,47 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
     if (MULTI && pass > 0) load_pass_shared(jb);
 
     // ---- K and V rows, lane = slot 16*kt + q16 (window column jb + slot),
-    //      columns ks*32 + kg*8 .. + 7 of the wave's 64: block rows and frame
-    //      rows first, then the K loads.  In a tile that holds one of this
-    //      step's frames, the frame lanes load from the projection output and
-    //      the others from the pages (an exec-masked pair of loads into one
-    //      register), so nothing waits for the loads until their first use.
-    uint32_t prow[NT], frow[NT], arow[NT];
+    //      columns ks*32 + kg*8 .. + 7 of the wave's 64.  Cached columns
+    //      (j < left) load from the pages, this step's frames (left <= j < Lk,
+    //      at most 16 of them) from the projection output.  With at most 16
+    //      frames a lane holds at most one frame column in a pass, the one
+    //      congruent to its slot mod 16: its frame row is a single load per
+    //      k-step, selected in when its tile is consumed (the select reads it
+    //      for every tile, so it is issued ahead of the page rows).  Every
+    //      load is unconditional (absent rows read zeros), so the compiler
+    //      counts them exactly when it places its waits: a load under a
+    //      branch would have it wait for every outstanding load at the first
+    //      use of any of them.
+    uint32_t prow[NT];
 #pragma unroll
     for (int kt = 0; kt < NT; ++kt) {
       const int j = jb + 16 * kt + q16;
       const uint32_t r = page_row(j);
-      const bool frame = j >= p.left && j < p.Lk;
       prow[kt] = j < p.left ? r : kNoRow;
-      frow[kt] = frame ? (uint32_t)(j - p.left) : kNoRow;
-      arow[kt] = frame ? r : kNoRow;  // append target of a frame
     }
+    const int fbase = max(p.left, jb);
+    const int jf = fbase + ((jb + q16 - fbase) & 15);  // the lane's frame column
+    const bool fvalid = jf < p.Lk && jf < jb + KT;
+    const int ftile = fvalid ? (jf - jb) >> 4 : -1;  // tile that holds it
+    const uint32_t frow = fvalid ? (uint32_t)(jf - p.left) : kNoRow;
+    const uint32_t arow_f = page_row(jf);
+    const uint32_t arow = fvalid && do_append ? arow_f : kNoRow;  // its append target
     // tile kt holds a frame of this step (workgroup-uniform)
     auto has_frames = [&](int kt) { return jb + 16 * kt + 15 >= p.left && jb + 16 * kt < p.Lk; };
-    u32x4 kr[NT][KS], vr[NT][KS];
+    // the operand rows of tile kt: page rows, with the lane's frame row in
+    // place of the (zero) page row where the tile holds it
+    auto with_frame = [&](int kt, u32x4 v, u32x4 f) {
+      if (has_frames(kt) && ftile == kt) v = f;
+      return v;
+    };
+    u32x4 kr[NT][KS], vr[NT][KS], kf[KS], vf[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) kf[ks] = pk_buffer_load_x4(r_kn, frow, cbyte + ks * KSB, 0, 0);
 #pragma unroll
     for (int kt = 0; kt < NT; ++kt)
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        if (has_frames(kt) && frow[kt] != kNoRow)
-          kr[kt][ks] = pk_buffer_load_x4(r_kn, frow[kt], cbyte + ks * KSB, 0, 0);
-        else
-          kr[kt][ks] = pk_buffer_load_x4(r_kp, prow[kt], kg * 16, blk_soff + ks * blk_step, 0);
-      }
+      for (int ks = 0; ks < KS; ++ks)
+        kr[kt][ks] = pk_buffer_load_x4(r_kp, prow[kt], kg * 16, blk_soff + ks * blk_step, 0);
     // which scores of the pass take no value (a slot past the window or the
     // pass, a query past the chunk: bit r * TQ + ii of neg_bits) or the mask's
     // -1e5 term (the streaming rule: msk_bits), for slot lane + 64 r of query
@@ -821,11 +837,11 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
       }
     }
     asm volatile("" ::"v"(neg_bits), "v"(msk_bits));
-    // the wave's position-row loads (issued before any K row, and at least
-    // NT*KS vector loads ago) are in LDS: wait for them, not for the K rows,
-    // before the barrier that makes every wave's part visible
-    static_assert(NT * KS <= 15, "vmcnt");
-    __builtin_amdgcn_s_waitcnt(0x0f70 | (NT * KS));
+    // the wave's position-row loads (issued before any K row, and exactly
+    // (NT + 1)*KS vector loads ago) are in LDS: wait for them, not for the K
+    // rows, before the barrier that makes every wave's part visible
+    static_assert((NT + 1) * KS <= 15, "vmcnt");
+    __builtin_amdgcn_s_waitcnt(0x0f70 | ((NT + 1) * KS));
     __syncthreads();  // position rows in LDS
 
     // ---- (q+v).pos over the wave's columns: D rows 4..7 (lanes 16..31)
@@ -846,36 +862,34 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
       }
     }
     // ---- (q+u).k over the wave's columns, D rows 0..3 (lanes 0..15), tile by
-    //      tile.  Once a tile's K rows are consumed (and, for a tile holding
-    //      this step's frames, appended to their pages by query group 0: the
-    //      row index is valid only for the frames' lanes), the tile's V rows
-    //      are issued into the registers it frees: no more registers in flight
+    //      tile.  Once a tile's K rows are consumed, the tile's V page rows are
+    //      issued into the registers it frees: no more registers in flight
     //      than the K rows alone, and the V round trip overlaps the rest of the
-    //      K phase, the scores and the softmax
+    //      K phase, the scores and the softmax (the frames' V rows go first,
+    //      ahead of tile 0's).  Then the frames' K rows go to their pages
+    //      (query group 0 only: the row index is valid only for the frames'
+    //      lanes).
 #pragma unroll
     for (int kt = 0; kt < NT; ++kt) {
       f32x4_t d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) d = Mma<ST>::k32(aop[ks], kr[kt][ks], d);
+      for (int ks = 0; ks < KS; ++ks) d = Mma<ST>::k32(aop[ks], with_frame(kt, kr[kt][ks], kf[ks]), d);
       if (kg == 0) {
         ac_lds[wave][0][16 * kt + q16] = d[0] + d[2];
         ac_lds[wave][1][16 * kt + q16] = d[1] + d[3];
       }
-      if (do_append && has_frames(kt)) {
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-          pk_buffer_store_x4(kr[kt][ks], r_kp, arow[kt], kg * 16, blk_soff + ks * blk_step, 0);
-      }
       __builtin_amdgcn_sched_barrier(0);
+      if (kt == 0) {
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        if (has_frames(kt) && frow[kt] != kNoRow)
-          vr[kt][ks] = pk_buffer_load_x4(r_vn, frow[kt], cbyte + ks * KSB, 0, 0);
-        else
-          vr[kt][ks] = pk_buffer_load_x4(r_vp, prow[kt], kg * 16, blk_soff + ks * blk_step, 0);
+        for (int ks = 0; ks < KS; ++ks) vf[ks] = pk_buffer_load_x4(r_vn, frow, cbyte + ks * KSB, 0, 0);
       }
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        vr[kt][ks] = pk_buffer_load_x4(r_vp, prow[kt], kg * 16, blk_soff + ks * blk_step, 0);
       __builtin_amdgcn_sched_barrier(0);
     }
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) pk_buffer_store_x4(kf[ks], r_kp, arow, kg * 16, blk_soff + ks * blk_step, 0);
     if constexpr (PV_OWN)
       wave_lds_sync();  // the wave's own dot products in LDS
     else
@@ -952,15 +966,6 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
     }
     wave_lds_sync();
 
-    // ---- fused append of this step's V rows
-    if (do_append) {
-#pragma unroll
-      for (int kt = 0; kt < NT; ++kt)
-        if (has_frames(kt))
-#pragma unroll
-          for (int ks = 0; ks < KS; ++ks)
-            pk_buffer_store_x4(vr[kt][ks], r_vp, arow[kt], kg * 16, blk_soff + ks * blk_step, 0);
-    }
 
     // ---- P.V, 16 slots at a time: stage the V rows, read them back
     //      transposed; A row m = q16 & 3 holds the high (m < 2) or low part of
@@ -971,8 +976,8 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
 #pragma unroll
     for (int kt = 0; kt < NT; ++kt) {
       uint8_t* vrow = vl + q16 * VSTRIDE + kg * 16;
-      *reinterpret_cast<u32x4*>(vrow) = vr[kt][0];
-      *reinterpret_cast<u32x4*>(vrow + KSB) = vr[kt][1];
+      *reinterpret_cast<u32x4*>(vrow) = with_frame(kt, vr[kt][0], vf[0]);
+      *reinterpret_cast<u32x4*>(vrow + KSB) = with_frame(kt, vr[kt][1], vf[1]);
       const i16x4_t pop = *reinterpret_cast<const i16x4_t*>(p_arow + 16 * kt + 4 * kg);
       wave_lds_sync();
 #pragma unroll
@@ -984,6 +989,9 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
       }
       wave_lds_sync();  // the next 16 rows overwrite the staging rows
     }
+    // ---- the frames' V rows to their pages
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) pk_buffer_store_x4(vf[ks], r_vp, arow, kg * 16, blk_soff + ks * blk_step, 0);
     if (MULTI) __syncthreads();  // the next pass restages pos_lds and rewrites bd / ac
   }
 
