@@ -125,6 +125,18 @@ def test_window_of_one_pass_edge(cuda, dk):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("left,right,dk", [(8, 15, 128), (33, 15, 64), (62, 15, 128), (70, 15, 64), (79, 1, 128)])
+def test_frames_across_tiles_and_passes(cuda, left, right, dk):
+    """The matrix-core kernel takes chunks of at most 16 frames, so a lane holds
+    at most one of the step's frames in a pass (the one congruent to its slot
+    mod 16).  16-frame chunks whose frames straddle a 16-slot tile (left 8, 33,
+    62: single pass), and frames on both sides of the 80-slot pass boundary of
+    the multi-pass form (left 70 with 16 frames, left 79 with 2)."""
+    steps = max(8, (left + right) // (right + 1) + 3)
+    _run(cuda, torch.bfloat16, B=3, H=4, dk=dk, left=left, right=right, P=16, steps=steps)
+
+
+@pytest.mark.gpu
 def test_long_window_multi_tile(cuda):
     # left context long enough that the window needs several tiles
     _run(cuda, torch.float16, B=2, H=8, dk=64, left=600, right=1, P=16, steps=6, layers=1)
