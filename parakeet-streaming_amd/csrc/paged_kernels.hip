@@ -628,13 +628,25 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
   //                  address and are replaced afterwards)
   // A operand source: row m = q16 is (q+u)_hi, (q+u)_lo, (q+v)_hi, (q+v)_lo of
   // query m & 1 for m < 8, zero above; element e of k-step ks is column
-  // ks*32 + kg*8 + e of the wave's 64.  Loaded first: vector loads complete in
-  // issue order, so q and the biases are in when the block-table header is,
-  // and the operand is built as soon as the header allows the K rows
+  // ks*32 + kg*8 + e of the wave's 64.  The wave needs 256 bytes of q (its 64
+  // columns of two query rows) and 256 of the biases (u and v).
+  //  * Q_GATHER (head_dim 128, the launches that queue on the CUs' load path):
+  //    one dword a lane of each, lane l holding dword l & 31 of row l >> 5,
+  //    loaded after the block table's ring entries (which the K rows'
+  //    addresses need first) and gathered into the operand layout across lanes
+  //    after the K rows are issued, while they are in flight.  Four 16-byte
+  //    loads a lane read each byte eight times over, all queued ahead of the K
+  //    rows on the CU.
+  //  * otherwise (head_dim 64, latency-bound launches, where the gather's LDS
+  //    round trips cost more than the loads): each lane loads its own 16-byte
+  //    operand chunks first, ahead of the header, and the operand is built
+  //    before the K rows are issued (after them it would hold the 16 registers
+  //    of the raw rows through the K loads).
+  constexpr bool Q_GATHER = DK == 128;
   const int a_ii = q16 & 1;
   const int a_kind = q16 >> 1;  // 0 u-hi, 1 u-lo, 2 v-hi, 3 v-lo, >= 4 zero
   u32x4 qraw[KS], braw[KS];
-  {
+  if constexpr (!Q_GATHER) {
     const int ic = min(i0 + a_ii, p.T - 1);
     const ST* qrow = p.q + b * p.q_sb + (int64_t)ic * p.q_st + hcol + kg * 8;
     const ST* brow = (a_kind < 2 ? p.bu : p.bv) + hcol + kg * 8;
@@ -650,6 +662,13 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
   const int32_t* hdr = paged ? p.pg.rows + hdr_off : reinterpret_cast<const int32_t*>(p.q);
   const int hdr_a = hdr[0];
   int ring_lane = hdr[paged ? 1 + min(lane, M - 1) : 0];
+  uint32_t q_dw = 0u, b_dw = 0u;
+  if constexpr (Q_GATHER) {
+    const int rr = lane >> 5, cd = lane & 31;
+    const int ic = min(i0 + rr, p.T - 1);
+    q_dw = reinterpret_cast<const uint32_t*>(p.q + b * p.q_sb + (int64_t)ic * p.q_st + hcol)[cd];
+    b_dw = reinterpret_cast<const uint32_t*>((rr ? p.bv : p.bu) + hcol)[cd];
+  }
   const int64_t* stp = mask_mode == 2 ? p.st_proc + b : reinterpret_cast<const int64_t*>(p.q);
   const int64_t* stc = mask_mode == 2 ? p.st_cl + b : stp;
   const int64_t* stn = (mask_mode == 2 && p.st_len) ? p.st_len + b : stp;
@@ -741,20 +760,34 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
 
   // ---------------- A operand (high / low parts of the fp32 sums)
   u32x4 aop[KS];
+  auto build_aop = [&]() {
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    float qf[8], bf[8], x[8];
-    Tr<ST>::unpack(qraw[ks], qf);
-    Tr<ST>::unpack(braw[ks], bf);
+    for (int ks = 0; ks < KS; ++ks) {
+      if constexpr (Q_GATHER) {
+        // the lane's 8 columns ks*32 + kg*8 .. are dwords ks*16 + kg*4 .. + 3
+        // of its query row (lanes 32 a_ii ..) and of its bias row (u: lanes
+        // 0 .., v: lanes 32 ..); every lane is active here
+        const int dw0 = ks * 16 + kg * 4;
+        const int bsel = a_kind >= 2 ? 32 : 0;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = (a_ii < nq ? qf[e] : 0.f) + bf[e];
-    aop[ks] = split16<ST, 8, u32x4>(x, a_kind & 1);
-    if (a_kind >= 4) aop[ks] = u32x4{0u, 0u, 0u, 0u};
-    // built here, before the K rows are issued: q and the biases are in by
-    // now (they were loaded ahead of the header's wait), whereas after the K
-    // loads the build would wait for all of them
-    asm volatile("" ::"v"(aop[ks]));
-  }
+        for (int e = 0; e < 4; ++e) {
+          qraw[ks][e] = (uint32_t)__builtin_amdgcn_ds_bpermute((a_ii * 32 + dw0 + e) * 4, (int)q_dw);
+          braw[ks][e] = (uint32_t)__builtin_amdgcn_ds_bpermute((bsel + dw0 + e) * 4, (int)b_dw);
+        }
+      }
+      float qf[8], bf[8], x[8];
+      Tr<ST>::unpack(qraw[ks], qf);
+      Tr<ST>::unpack(braw[ks], bf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = (a_ii < nq ? qf[e] : 0.f) + bf[e];
+      aop[ks] = split16<ST, 8, u32x4>(x, a_kind & 1);
+      if (a_kind >= 4) aop[ks] = u32x4{0u, 0u, 0u, 0u};
+      asm volatile("" ::"v"(aop[ks]));  // built where it is called
+    }
+  };
+  // otherwise built here, before the K rows are issued: q and the biases are
+  // in by now (they were loaded ahead of the header's wait)
+  if constexpr (!Q_GATHER) build_aop();
 
   f32x4_t oacc[4];  // P.V: D rows (hi q0, hi q1, lo q0, lo q1), 4 column tiles of 16
 #pragma unroll
@@ -837,6 +870,10 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
       }
     }
     asm volatile("" ::"v"(neg_bits), "v"(msk_bits));
+    // Q_GATHER: the A operand is built once the first pass's K rows are
+    // issued (waits are counted exactly, so this waits for q and the biases
+    // only, not for the K rows)
+    if (Q_GATHER && pass == 0) build_aop();
     // the wave's position-row loads (issued before any K row, and exactly
     // (NT + 1)*KS vector loads ago) are in LDS: wait for them, not for the K
     // rows, before the barrier that makes every wave's part visible
