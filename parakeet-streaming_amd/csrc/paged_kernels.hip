@@ -529,7 +529,8 @@ __device__ static inline __amdgpu_buffer_rsrc_t rows_rsrc(const void* base, int 
 //   * the fused append stores this step's frame rows into their pages (query
 //     group 0): a lane holds at most one frame column a pass (chunks of at
 //     most 16 frames), loaded once and selected into the tile that holds it,
-//     so every load and store is branch-free.
+//     so every load and store is branch-free; the stores are the wave's last
+//     instructions, non-temporal.
 // Pages hold 64-byte column blocks ([page][block][page_size][32 elements]),
 // so one k-step load of a 16-slot tile reads 16 rows x 64 bytes of one block:
 // 1 KB of contiguous memory when the 16 slots share a page.
@@ -804,6 +805,15 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
   // MULTI: windows longer than one pass (the single-pass form is straight-line
   // code, with nothing carried around a loop)
   const int npass = MULTI ? p.tiles : 1;
+  // The fused append stores this step's frame rows as the wave's last
+  // instructions, non-temporal (cache policy nt): scattered 128-byte writes
+  // into the page blocks the launch streams its reads from, issued mid-wave
+  // and cached, took 4% of the launch at 230 streams (either change alone
+  // gained under 1%).  The multi-pass form stores each pass's frames after
+  // that pass.
+  constexpr int kAppendPolicy = 2;  // nt
+  u32x4 app_rows[2 * KS];           // K then V frame rows of the single pass
+  uint32_t app_row = kNoRow;
   for (int pass = 0; pass < npass; ++pass) {
     const int jb = pass * KT;
     const int npt = pass_tiles(jb);
@@ -903,7 +913,7 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
     //      issued into the registers it frees: no more registers in flight
     //      than the K rows alone, and the V round trip overlaps the rest of the
     //      K phase, the scores and the softmax (the frames' V rows go first,
-    //      ahead of tile 0's).  Then the frames' K rows go to their pages
+    //      ahead of tile 0's).  The frames' K rows go to their pages later
     //      (query group 0 only: the row index is valid only for the frames'
     //      lanes).
 #pragma unroll
@@ -925,8 +935,11 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
         vr[kt][ks] = pk_buffer_load_x4(r_vp, prow[kt], kg * 16, blk_soff + ks * blk_step, 0);
       __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (MULTI) {
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) pk_buffer_store_x4(kf[ks], r_kp, arow, kg * 16, blk_soff + ks * blk_step, 0);
+      for (int ks = 0; ks < KS; ++ks)
+        pk_buffer_store_x4(kf[ks], r_kp, arow, kg * 16, blk_soff + ks * blk_step, kAppendPolicy);
+    }
     if constexpr (PV_OWN)
       wave_lds_sync();  // the wave's own dot products in LDS
     else
@@ -1027,8 +1040,18 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
       wave_lds_sync();  // the next 16 rows overwrite the staging rows
     }
     // ---- the frames' V rows to their pages
+    if constexpr (MULTI) {
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) pk_buffer_store_x4(vf[ks], r_vp, arow, kg * 16, blk_soff + ks * blk_step, 0);
+      for (int ks = 0; ks < KS; ++ks)
+        pk_buffer_store_x4(vf[ks], r_vp, arow, kg * 16, blk_soff + ks * blk_step, kAppendPolicy);
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        app_rows[ks] = kf[ks];
+        app_rows[KS + ks] = vf[ks];
+      }
+      app_row = arow;
+    }
     if (MULTI) __syncthreads();  // the next pass restages pos_lds and rewrites bd / ac
   }
 
@@ -1050,6 +1073,15 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
     if (lane < 16 && oi < nq)
       *reinterpret_cast<u32x4*>(p.out + b * p.o_sb + (int64_t)(i0 + oi) * p.o_st + hcol + (lane & 7) * 8) =
           *reinterpret_cast<const u32x4*>(vl + oi * VSTRIDE + (lane & 7) * 16);
+  }
+  // ---- the single pass's fused append (row kNoRow where there is nothing to store)
+  if constexpr (!MULTI) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      pk_buffer_store_x4(app_rows[ks], r_kp, app_row, kg * 16, blk_soff + ks * blk_step, kAppendPolicy);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      pk_buffer_store_x4(app_rows[KS + ks], r_vp, app_row, kg * 16, blk_soff + ks * blk_step, kAppendPolicy);
   }
 }
 
