@@ -534,7 +534,7 @@ __device__ static inline __amdgpu_buffer_rsrc_t rows_rsrc(const void* base, int 
 // Pages hold 64-byte column blocks ([page][block][page_size][32 elements]),
 // so one k-step load of a 16-slot tile reads 16 rows x 64 bytes of one block:
 // 1 KB of contiguous memory when the 16 slots share a page.
-template <typename ST, int DK, int NT, int MODE, bool MULTI>
+template <typename ST, int DK, int NT, int MODE, bool MULTI, bool STREAM>
 __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p) {
   constexpr int SPLIT = DK / 64;
   constexpr int NW = 4;
@@ -811,7 +811,11 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
   // and cached, took 4% of the launch at 230 streams (either change alone
   // gained under 1%).  The multi-pass form stores each pass's frames after
   // that pass.
-  constexpr int kAppendPolicy = 2;  // nt
+  // cache policy of the page rows' loads, the appends and the output: nt
+  // (streaming) when the step's windows outgrow the last-level cache (STREAM,
+  // chosen by the host), so they do not displace what is reused
+  constexpr int kPagePolicy = STREAM ? 2 : 0;
+  constexpr int kAppendPolicy = kPagePolicy;
   u32x4 app_rows[2 * KS];           // K then V frame rows of the single pass
   uint32_t app_row = kNoRow;
   for (int pass = 0; pass < npass; ++pass) {
@@ -860,7 +864,7 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
     for (int kt = 0; kt < NT; ++kt)
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
-        kr[kt][ks] = pk_buffer_load_x4(r_kp, prow[kt], kg * 16, blk_soff + ks * blk_step, 0);
+        kr[kt][ks] = pk_buffer_load_x4(r_kp, prow[kt], kg * 16, blk_soff + ks * blk_step, kPagePolicy);
     // which scores of the pass take no value (a slot past the window or the
     // pass, a query past the chunk: bit r * TQ + ii of neg_bits) or the mask's
     // -1e5 term (the streaming rule: msk_bits), for slot lane + 64 r of query
@@ -932,7 +936,7 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
       }
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
-        vr[kt][ks] = pk_buffer_load_x4(r_vp, prow[kt], kg * 16, blk_soff + ks * blk_step, 0);
+        vr[kt][ks] = pk_buffer_load_x4(r_vp, prow[kt], kg * 16, blk_soff + ks * blk_step, kPagePolicy);
       __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (MULTI) {
@@ -1070,9 +1074,15 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
     }
     wave_lds_sync();
     const int oi = lane >> 3;  // query of the lane's 16 bytes
-    if (lane < 16 && oi < nq)
-      *reinterpret_cast<u32x4*>(p.out + b * p.o_sb + (int64_t)(i0 + oi) * p.o_st + hcol + (lane & 7) * 8) =
-          *reinterpret_cast<const u32x4*>(vl + oi * VSTRIDE + (lane & 7) * 16);
+    if (lane < 16 && oi < nq) {
+      const u32x4 o = *reinterpret_cast<const u32x4*>(vl + oi * VSTRIDE + (lane & 7) * 16);
+      u32x4* const dst =
+          reinterpret_cast<u32x4*>(p.out + b * p.o_sb + (int64_t)(i0 + oi) * p.o_st + hcol + (lane & 7) * 8);
+      if constexpr (STREAM)
+        __builtin_nontemporal_store(o, dst);
+      else
+        *dst = o;
+    }
   }
   // ---- the single pass's fused append (row kNoRow where there is nothing to store)
   if constexpr (!MULTI) {
@@ -1320,28 +1330,46 @@ void pick_tiling(int Lk, int rlw, int hint, int* NR, int* tiles) {
 // pair of queries, key tiles of 16 * kMfmaTiles rows.
 constexpr int kMfmaTiles = 5;
 
-template <typename ST, int DK, int MODE, bool MULTI>
+template <typename ST, int DK, int MODE, bool MULTI, bool STREAM>
 int launch_attn_mfma_t(const pk_attn_args* a, const AttnK<ST>& k, hipStream_t s) {
   constexpr int SPW = 4 / (DK / 64);  // streams per workgroup
   dim3 grid((unsigned)((a->batch + SPW - 1) / SPW), (unsigned)a->num_heads,
             (unsigned)((a->chunk + 1) / 2));
   dim3 block(256u);
   if (a->start_event || a->stop_event) {
-    hipExtLaunchKernelGGL(relpos_attn_mfma_kernel<ST, DK, kMfmaTiles, MODE, MULTI>, grid, block,
+    hipExtLaunchKernelGGL(relpos_attn_mfma_kernel<ST, DK, kMfmaTiles, MODE, MULTI, STREAM>, grid, block,
                           0u, s, (hipEvent_t)a->start_event, (hipEvent_t)a->stop_event, 0u, k);
   } else {
-    hipLaunchKernelGGL((relpos_attn_mfma_kernel<ST, DK, kMfmaTiles, MODE, MULTI>), grid, block, 0,
+    hipLaunchKernelGGL((relpos_attn_mfma_kernel<ST, DK, kMfmaTiles, MODE, MULTI, STREAM>), grid, block, 0,
                        s, k);
   }
   return check_launch("pk_paged_relpos_attn");
 }
 
-template <typename ST, int DK, int MODE>
-int launch_attn_mfma_mode(const pk_attn_args* a, const AttnK<ST>& k, hipStream_t s) {
+// Page rows are read with the streaming cache policy once a step's windows
+// (every layer's K and V rows of the batch) outgrow this share of the 256 MB
+// last-level cache: below it the windows stay cached from one step to the
+// next and the cached policy reads them faster (64 streams of the small model,
+// 160 MB: 8,430 against 8,220 steps/s); above it cached reads only displace
+// what is reused (230 streams of the large model, 1.6 GB: 2,906 against
+// 2,641 steps/s; 1,024 streams of the small model: 1,903 against 1,742)
+constexpr int64_t kStreamingBytes = 192ll << 20;
+
+template <typename ST, int DK, int MODE, bool STREAM>
+int launch_attn_mfma_ms(const pk_attn_args* a, const AttnK<ST>& k, hipStream_t s) {
   // the single-pass form holds at most 16 * kMfmaTiles - 1 keys (its staged
   // position rows stop at 16 * kMfmaTiles)
-  if (k.tiles > 1 || k.Lk > 16 * kMfmaTiles - 1) return launch_attn_mfma_t<ST, DK, MODE, true>(a, k, s);
-  return launch_attn_mfma_t<ST, DK, MODE, false>(a, k, s);
+  if (k.tiles > 1 || k.Lk > 16 * kMfmaTiles - 1) return launch_attn_mfma_t<ST, DK, MODE, true, STREAM>(a, k, s);
+  return launch_attn_mfma_t<ST, DK, MODE, false, STREAM>(a, k, s);
+}
+
+template <typename ST, int DK, int MODE>
+int launch_attn_mfma_mode(const pk_attn_args* a, const AttnK<ST>& k, hipStream_t s) {
+  const int64_t layers = a->pages.num_layers > 1 ? a->pages.num_layers : 1;
+  const int64_t window_bytes = (int64_t)a->batch * k.Lk * a->num_heads * DK * (int64_t)sizeof(ST) * 2 * layers;
+  const bool stream = k.pg.rows != nullptr && window_bytes > kStreamingBytes;
+  if (stream) return launch_attn_mfma_ms<ST, DK, MODE, true>(a, k, s);
+  return launch_attn_mfma_ms<ST, DK, MODE, false>(a, k, s);
 }
 
 template <typename ST, int DK>

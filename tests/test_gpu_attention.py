@@ -241,10 +241,14 @@ def test_batch_split_is_bit_exact(cuda, B):
     launch over the whole batch equals, bit for bit, that of the same streams
     launched 64 at a time (odd block sizes included: 130 = 2 x 64 + 2), and
     the oracle's within tolerance; the fused append writes exactly the
-    frames."""
+    frames.  The pool has 4 layers, so a launch's windows over all of them
+    (B x 72 frames x 1024 x 2 bytes x K and V x 4 layers) pass the host's
+    192 MiB streaming threshold at B = 200 and 256 (236 and 302 MB): those
+    whole-batch launches read with the streaming cache policy, the 64-stream
+    blocks (75 MB) with the cached one, and the results must not differ."""
     dtype, H, dk, left, right, P = torch.bfloat16, 8, 128, 70, 1, 16
     print(f"\n[attn batch split] B={B}", flush=True)
-    sc = PagedScenario(cuda, dtype, B=B, layers=1, d_model=H * dk, left=left, right=right, page_size=P, seed=B)
+    sc = PagedScenario(cuda, dtype, B=B, layers=4, d_model=H * dk, left=left, right=right, page_size=P, seed=B)
     pos, bu, bv = _relpos(sc, H, B)
     T = sc.T
     proc = np.zeros(B, dtype=np.int64)
