@@ -125,7 +125,11 @@ int pk_kv_gather(const pk_kv_gather_args* args, void* stream);
  * Keys j >= left are this step's frames, read from key/value; keys j < left come
  * from the pages.  With append != 0 the new frames are also written to the pages
  * (pk_kv_append fused).  left == 0 with k_pool == NULL attends over the chunk only
- * (cache=None in the reference).
+ * (cache=None in the reference).  Cache policy (no effect on results): when a
+ * step's windows, batch * window * d_model * element size * 2 * pages.num_layers
+ * bytes, exceed 192 MiB, the page rows are read, and the appends and out written,
+ * with the streaming (non-temporal) policy, so a stream of windows larger than
+ * the last-level cache does not displace what the step reuses.
  * query/key/value: [batch][chunk][num_heads*head_dim], strides (b, t), last dim
  * contiguous.  pos: [pos_rows][num_heads*head_dim], row stride pos_stride; needs
  * pos_rows >= window + chunk - 1; pos_stride_b != 0 gives every stream its own
