@@ -530,7 +530,10 @@ __device__ static inline __amdgpu_buffer_rsrc_t rows_rsrc(const void* base, int 
 //     group 0): a lane holds at most one frame column a pass (chunks of at
 //     most 16 frames), loaded once and selected into the tile that holds it,
 //     so every load and store is branch-free; the stores are the wave's last
-//     instructions, non-temporal.
+//     instructions.
+//   * STREAM (host-chosen when a step's windows outgrow the last-level
+//     cache): page rows, appends and the output with the streaming cache
+//     policy.
 // Pages hold 64-byte column blocks ([page][block][page_size][32 elements]),
 // so one k-step load of a 16-slot tile reads 16 rows x 64 bytes of one block:
 // 1 KB of contiguous memory when the 16 slots share a page.
@@ -806,14 +809,13 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
   // code, with nothing carried around a loop)
   const int npass = MULTI ? p.tiles : 1;
   // The fused append stores this step's frame rows as the wave's last
-  // instructions, non-temporal (cache policy nt): scattered 128-byte writes
-  // into the page blocks the launch streams its reads from, issued mid-wave
-  // and cached, took 4% of the launch at 230 streams (either change alone
-  // gained under 1%).  The multi-pass form stores each pass's frames after
-  // that pass.
-  // cache policy of the page rows' loads, the appends and the output: nt
-  // (streaming) when the step's windows outgrow the last-level cache (STREAM,
-  // chosen by the host), so they do not displace what is reused
+  // instructions (the multi-pass form after each pass): scattered 128-byte
+  // writes into the page blocks the launch streams its reads from cost 4% of
+  // the launch at 230 streams more when issued mid-wave and cached.  The page
+  // rows' loads, the appends and the output take the streaming cache policy
+  // (nt) when the step's windows outgrow the last-level cache (STREAM, chosen
+  // by the host), so they do not displace what the step reuses; below that
+  // the windows stay cached from one step to the next.
   constexpr int kPagePolicy = STREAM ? 2 : 0;
   constexpr int kAppendPolicy = kPagePolicy;
   u32x4 app_rows[2 * KS];           // K then V frame rows of the single pass
