@@ -634,19 +634,21 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
   // query m & 1 for m < 8, zero above; element e of k-step ks is column
   // ks*32 + kg*8 + e of the wave's 64.  The wave needs 256 bytes of q (its 64
   // columns of two query rows) and 256 of the biases (u and v).
-  //  * Q_GATHER (head_dim 128, the launches that queue on the CUs' load path):
+  //  * Q_GATHER (head_dim 128, or a streaming launch: the launches that queue
+  //    on the CUs' load path):
   //    one dword a lane of each, lane l holding dword l & 31 of row l >> 5,
   //    loaded after the block table's ring entries (which the K rows'
   //    addresses need first) and gathered into the operand layout across lanes
   //    after the K rows are issued, while they are in flight.  Four 16-byte
   //    loads a lane read each byte eight times over, all queued ahead of the K
   //    rows on the CU.
-  //  * otherwise (head_dim 64, latency-bound launches, where the gather's LDS
-  //    round trips cost more than the loads): each lane loads its own 16-byte
+  //  * otherwise (head_dim 64 below the streaming size, latency-bound
+  //    launches, where the gather's LDS round trips cost more than the loads,
+  //    8,430 against 8,313-8,377 steps/s at 64 streams): each lane loads its own 16-byte
   //    operand chunks first, ahead of the header, and the operand is built
   //    before the K rows are issued (after them it would hold the 16 registers
   //    of the raw rows through the K loads).
-  constexpr bool Q_GATHER = DK == 128;
+  constexpr bool Q_GATHER = DK == 128 || STREAM;
   const int a_ii = q16 & 1;
   const int a_kind = q16 >> 1;  // 0 u-hi, 1 u-lo, 2 v-hi, 3 v-lo, >= 4 zero
   u32x4 qraw[KS], braw[KS];
