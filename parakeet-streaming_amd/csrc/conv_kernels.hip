@@ -61,7 +61,11 @@ __device__ static inline float block_sum(float v, float* red, int nw) {
 
 constexpr int kConvMaxWaves = 8;
 
-template <typename ST, int K>
+// STREAM (host-chosen when the conv caches of a step outgrow the last-level
+// cache): the cache rows and the GLU input, each read once a step, move with
+// the streaming (non-temporal) policy, so they do not displace what the
+// step's other kernels reuse
+template <typename ST, int K, bool STREAM>
 __global__ void __launch_bounds__(64 * kConvMaxWaves) conv_step_kernel(const ConvK<ST> p) {
   constexpr int VEC = Tr<ST>::VEC;
   constexpr int R = K - 1;  // cache rows
@@ -106,7 +110,8 @@ __global__ void __launch_bounds__(64 * kConvMaxWaves) conv_step_kernel(const Con
   // window rows 0..R-1: the cache (the R frames before this step's first)
   float win[K][VEC];
 #pragma unroll
-  for (int r = 0; r < R; ++r) Tr<ST>::unpack(ld16(crow + (int64_t)r * p.D), win[r]);
+  for (int r = 0; r < R; ++r)
+    Tr<ST>::unpack(STREAM ? ld16_stream(crow + (int64_t)r * p.D) : ld16(crow + (int64_t)r * p.D), win[r]);
 
   const uint8_t* padb = p.pad ? p.pad + (int64_t)b * p.T : nullptr;
   const int64_t len = p.lengths ? p.lengths[b] : p.len_scalar;
@@ -115,8 +120,8 @@ __global__ void __launch_bounds__(64 * kConvMaxWaves) conv_step_kernel(const Con
   for (int t = 0; t < p.T; ++t) {
     // this frame's GLU output (convolution.py:152-155), zero where padded
     float a[VEC], g[VEC];
-    Tr<ST>::unpack(ld16(hb + t * p.h_st), a);
-    Tr<ST>::unpack(ld16(hb + t * p.h_st + p.D), g);
+    Tr<ST>::unpack(STREAM ? ld16_stream(hb + t * p.h_st) : ld16(hb + t * p.h_st), a);
+    Tr<ST>::unpack(STREAM ? ld16_stream(hb + t * p.h_st + p.D) : ld16(hb + t * p.h_st + p.D), g);
     const bool valid = padb ? padb[t] == 0 : (int64_t)t < len;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
@@ -161,18 +166,31 @@ __global__ void __launch_bounds__(64 * kConvMaxWaves) conv_step_kernel(const Con
   // (convolution.py:46, next_cache = new_x[:, :, -(K-1):])
   if (own) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) st16(crow + (int64_t)r * p.D, Tr<ST>::pack(win[r]));
+    for (int r = 0; r < R; ++r) {
+      if constexpr (STREAM)
+        st16_stream(crow + (int64_t)r * p.D, Tr<ST>::pack(win[r]));
+      else
+        st16(crow + (int64_t)r * p.D, Tr<ST>::pack(win[r]));
+    }
   }
 }
 
 namespace {
+
+// a step's conv caches (every layer's rows of the batch) above this share of
+// the 256 MB last-level cache take the streaming policy
+constexpr int64_t kConvStreamingBytes = 192ll << 20;
 
 template <typename ST, int K>
 int launch_conv(const ConvK<ST>& k, int batch, hipStream_t s) {
   constexpr int VEC = Tr<ST>::VEC;
   const int nchunk = k.D / VEC;
   const int nw = (nchunk + 63) / 64;
-  hipLaunchKernelGGL((conv_step_kernel<ST, K>), dim3((unsigned)batch), dim3(64u * nw), 0, s, k);
+  const int64_t cache_bytes = (int64_t)batch * k.num_layers * (K - 1) * k.D * (int64_t)sizeof(ST);
+  if (cache_bytes > kConvStreamingBytes)
+    hipLaunchKernelGGL((conv_step_kernel<ST, K, true>), dim3((unsigned)batch), dim3(64u * nw), 0, s, k);
+  else
+    hipLaunchKernelGGL((conv_step_kernel<ST, K, false>), dim3((unsigned)batch), dim3(64u * nw), 0, s, k);
   return check_launch("pk_conv_step");
 }
 

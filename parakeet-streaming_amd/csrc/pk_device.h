@@ -156,6 +156,11 @@ __device__ static inline void st16(ST* p, const u32x4 v) {
   *reinterpret_cast<u32x4*>(p) = v;
 }
 
+template <typename ST>
+__device__ static inline void st16_stream(ST* p, const u32x4 v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+}
+
 // ---------------------------------------------------------------------------
 // lane-group all-reduce (sum) over G consecutive lanes with DPP row ops:
 // quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror, then

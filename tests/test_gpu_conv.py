@@ -190,3 +190,27 @@ def test_module_in_place_and_tensor_state_agree(cuda, dt):
     a.reset_slot(4)
     assert not a.conv_frames[4].any() and a.conv_frames[1].any()
     assert tuple(a.conv.shape) == (N, Ly, D, K - 1)
+
+
+def test_streaming_policy_is_bit_exact(cuda):
+    """A batch whose conv caches over all layers pass the host's 192 MiB
+    streaming threshold (2048 streams x 13 layers x 8 rows x 512 x 2 bytes =
+    218 MB) runs with the streaming cache policy; the same streams in blocks
+    of 256 (27 MB) run with the cached one.  Outputs and updated caches must
+    agree bit for bit."""
+    B, L, D, K, T, layer = 2048, 13, 512, 9, 2, 5
+    dt = torch.float16
+    w, _, lw, lb = _params(D, K, dt, 11, False)
+    wd, lwd, lbd = w.to(cuda), lw.to(cuda), lb.to(cuda)
+    g = torch.Generator().manual_seed(12)
+    h = torch.randn(B, T, 2 * D, generator=g).to(dt).to(cuda)
+    c1 = torch.randn(B, L, K - 1, D, generator=g).to(dt).to(cuda)
+    c2 = c1.clone()
+    y1 = ops.conv_step(h, c1, wd, lwd, lbd, layer=layer)
+    y2 = torch.empty_like(y1)
+    for b0 in range(0, B, 256):
+        slots = torch.arange(b0, b0 + 256, dtype=torch.int32, device=cuda)
+        y2[b0 : b0 + 256] = ops.conv_step(h[b0 : b0 + 256], c2, wd, lwd, lbd, layer=layer, slots=slots)
+    torch.cuda.synchronize()
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+    assert torch.equal(c1.view(torch.int16), c2.view(torch.int16))
