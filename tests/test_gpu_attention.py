@@ -235,19 +235,20 @@ def test_state_mask_identical_to_mask_tensor(cuda, left, right, dtype):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("B", [130, 200, 256])
-def test_batch_split_is_bit_exact(cuda, B):
-    """At head_dim 128 (two streams a workgroup) every stream's output of a
-    launch over the whole batch equals, bit for bit, that of the same streams
-    launched 64 at a time (odd block sizes included: 130 = 2 x 64 + 2), and
-    the oracle's within tolerance; the fused append writes exactly the
-    frames.  The pool has 4 layers, so a launch's windows over all of them
-    (B x 72 frames x 1024 x 2 bytes x K and V x 4 layers) pass the host's
-    192 MiB streaming threshold at B = 200 and 256 (236 and 302 MB): those
-    whole-batch launches read with the streaming cache policy, the 64-stream
-    blocks (75 MB) with the cached one, and the results must not differ."""
-    dtype, H, dk, left, right, P = torch.bfloat16, 8, 128, 70, 1, 16
-    print(f"\n[attn batch split] B={B}", flush=True)
+@pytest.mark.parametrize("B,dk", [(130, 128), (200, 128), (256, 128), (384, 64)])
+def test_batch_split_is_bit_exact(cuda, B, dk):
+    """Every stream's output of a launch over the whole batch equals, bit for
+    bit, that of the same streams launched 64 at a time (odd block sizes
+    included: 130 = 2 x 64 + 2), and the oracle's within tolerance; the fused
+    append writes exactly the frames.  The pool has 4 layers, so a launch's
+    windows over all of them (B x 72 frames x 8 x head_dim x 2 bytes x K and V
+    x 4 layers) pass the host's 192 MiB streaming threshold at B = 200 and 256
+    with head_dim 128 (236 and 302 MB) and at B = 384 with head_dim 64
+    (226 MB): those whole-batch launches read with the streaming cache policy
+    (with a mask tensor, the form the encoder step uses), the 64-stream blocks
+    with the cached one, and the results must not differ."""
+    dtype, H, left, right, P = torch.bfloat16, 8, 70, 1, 16
+    print(f"\n[attn batch split] B={B} dk={dk}", flush=True)
     sc = PagedScenario(cuda, dtype, B=B, layers=4, d_model=H * dk, left=left, right=right, page_size=P, seed=B)
     pos, bu, bv = _relpos(sc, H, B)
     T = sc.T
@@ -270,9 +271,17 @@ def test_batch_split_is_bit_exact(cuda, B):
         out = ops.paged_relpos_attn(q, k, v, pos, bu, bv, mask, pages=sc.pages, append=True, **args)
         dk_win, dv_win = sc.dense_update(0, k, v)
         if step in (0, 39):
+            # At step 0 a query sees two unit-variance frames, so outputs reach
+            # 4.2 here, where bf16 values lie 2**-5 apart: the nearest bf16 to
+            # the oracle's 4.2339 is already 0.0151 from it.  The bar applies
+            # to the oracle rounded to the output dtype, and the raw error may
+            # exceed it by no more than that rounding.
             ref = oa.relpos_attention(to_np64(q), dk_win, dv_win, to_np64(pos), to_np64(bu), to_np64(bv), mask_np, H)
-            err = np.abs(to_np64(out) - ref).max()
-            assert err <= TOL[dtype], f"step {step}: max abs err {err:.3e}"
+            ref_r = to_np64(torch.from_numpy(ref).to(dtype))
+            err = np.abs(to_np64(out) - ref_r).max()
+            assert err <= TOL[dtype], f"step {step}: max abs err {err:.3e} against the rounded oracle"
+            raw = np.abs(to_np64(out) - ref) - np.abs(ref_r - ref)
+            assert raw.max() <= TOL[dtype], f"step {step}: max abs err {raw.max():.3e} beyond rounding"
         gk, gv = ops.kv_gather(sc.pages, 0, B, sc.L, T)
         assert torch.equal(gk.cpu(), torch.from_numpy(np.ascontiguousarray(dk_win)).to(dtype))
         assert torch.equal(gv.cpu(), torch.from_numpy(np.ascontiguousarray(dv_win)).to(dtype))
