@@ -235,8 +235,10 @@ def test_state_mask_identical_to_mask_tensor(cuda, left, right, dtype):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("B,dk", [(130, 128), (200, 128), (256, 128), (384, 64)])
-def test_batch_split_is_bit_exact(cuda, B, dk):
+@pytest.mark.parametrize("B,dk,dtype", [(130, 128, torch.bfloat16), (200, 128, torch.bfloat16),
+                                        (256, 128, torch.bfloat16), (384, 64, torch.bfloat16),
+                                        (384, 64, torch.float16)])
+def test_batch_split_is_bit_exact(cuda, B, dk, dtype):
     """Every stream's output of a launch over the whole batch equals, bit for
     bit, that of the same streams launched 64 at a time (odd block sizes
     included: 130 = 2 x 64 + 2), and the oracle's within tolerance; the fused
@@ -244,11 +246,11 @@ def test_batch_split_is_bit_exact(cuda, B, dk):
     windows over all of them (B x 72 frames x 8 x head_dim x 2 bytes x K and V
     x 4 layers) pass the host's 192 MiB streaming threshold at B = 200 and 256
     with head_dim 128 (236 and 302 MB) and at B = 384 with head_dim 64
-    (226 MB): those whole-batch launches read with the streaming cache policy
+    (226 MB; bf16 and fp16): those whole-batch launches read with the streaming cache policy
     (with a mask tensor, the form the encoder step uses), the 64-stream blocks
     with the cached one, and the results must not differ."""
-    dtype, H, left, right, P = torch.bfloat16, 8, 70, 1, 16
-    print(f"\n[attn batch split] B={B} dk={dk}", flush=True)
+    H, left, right, P = 8, 70, 1, 16
+    print(f"\n[attn batch split] B={B} dk={dk} dtype={dtype}", flush=True)
     sc = PagedScenario(cuda, dtype, B=B, layers=4, d_model=H * dk, left=left, right=right, page_size=P, seed=B)
     pos, bu, bv = _relpos(sc, H, B)
     T = sc.T
@@ -275,7 +277,7 @@ def test_batch_split_is_bit_exact(cuda, B, dk):
             # 4.2 here, where bf16 values lie 2**-5 apart: the nearest bf16 to
             # the oracle's 4.2339 is already 0.0151 from it.  The bar applies
             # to the oracle rounded to the output dtype, and the raw error may
-            # exceed it by no more than that rounding.
+            # exceed it by no more than that rounding (fp16 or bf16 alike).
             ref = oa.relpos_attention(to_np64(q), dk_win, dv_win, to_np64(pos), to_np64(bu), to_np64(bv), mask_np, H)
             ref_r = to_np64(torch.from_numpy(ref).to(dtype))
             err = np.abs(to_np64(out) - ref_r).max()
