@@ -6,8 +6,12 @@ step (parakeet_amd.step.AttentionStep) with continuous arrivals and departures:
 * fragmentation stress: small shape (d_model 512, 8 x 64, fp16), 1024 slots,
   the page pool pre-shuffled by a seeded permutation, lifetimes log-U(1, 60) s.
 
-Two layers each, over enough steps that windows fill, pages are evicted and
-reused, and slots are reused by new streams.  Every step:
+Four layers for the large shape and two for the fragmentation stress, over
+enough steps that windows fill, pages are evicted and reused, and slots are
+reused by new streams.  A launch's windows over all layers pass the host's
+192 MiB streaming threshold in both (230 x 72 x 1024 x 2 bytes x K and V x 4
+layers = 271 MB; 1024 x 72 x 512 x 2 x 2 x 2 = 302 MB), so the kernels read
+with the streaming cache policy, as in the 24-layer benchmark.  Every step:
 * the block-table rows the host pool hands the kernels equal the oracle's FIFO
   page-pool model (oracle/paging.py, scheduler.py:84,97,104) fed the same slot
   sequence, bit for bit;
@@ -39,7 +43,7 @@ TOL = {torch.float16: 2e-3, torch.bfloat16: 1e-2}
 
 CASES = {
     # shape, slots, occupancy, lifetimes, shuffled pool, seed, steps
-    "large_256slots_bf16": (synth.Shape("large-2layer-bf16", 2, 1024, 8, dtype=torch.bfloat16), 256, 0.9,
+    "large_256slots_bf16": (synth.Shape("large-4layer-bf16", 4, 1024, 8, dtype=torch.bfloat16), 256, 0.9,
                             ("uniform", 2.0, 30.0), False, 3, 220),
     "frag_1024slots_fp16": (synth.Shape("small-2layer-fp16", 2, 512, 8, dtype=torch.float16), 1024, 1.0,
                             ("loguniform", 1.0, 60.0), True, 4, 300),
