@@ -31,10 +31,11 @@ sys.path.insert(0, os.path.join(HERE, "parakeet-streaming_amd"))
 sys.path.insert(0, HERE)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
-CHUNK_SECONDS = 0.16  # audio per step at 2 frames x 80 ms
+FRAME_SECONDS = 0.08  # audio per encoder frame (10 ms hop x 8x subsampling)
 
 CONFIGS = {
     "large": dict(shape="LARGE_BF16", slots=256, occupancy=0.9, durations=("uniform", 2.0, 30.0), shuffle=False, seed=3),
+    "large-t14": dict(shape="LARGE_BF16_T14", slots=256, occupancy=0.9, durations=("uniform", 2.0, 30.0), shuffle=False, seed=3),
     "small": dict(shape="SMALL_FP16", slots=64, occupancy=1.0, durations=("uniform", 2.0, 30.0), shuffle=False, seed=1),
     "frag": dict(shape="SMALL_FP16", slots=1024, occupancy=1.0, durations=("loguniform", 1.0, 60.0), shuffle=True, seed=4),
     "plumbing": dict(shape="SMALL_FP32", slots=4, occupancy=1.0, durations=("uniform", 1e9, 1e9), shuffle=False, seed=0),
@@ -716,7 +717,7 @@ def main() -> int:
     free_b, total_b = torch.cuda.mem_get_info(device)
     per_stream_pool = runner.pool.max_pages * Ly * shape.page_size * shape.d_model * shape.elem_bytes * 2
     pool_capacity = int((total_b * 0.9) // per_stream_pool)
-    realtime_capacity = int(avg_B * (CHUNK_SECONDS * 1000.0) / ms_per_step)
+    realtime_capacity = int(avg_B * (shape.chunk * FRAME_SECONDS * 1000.0) / ms_per_step)
 
     result = {
         "metric": "encoder attn steps/sec & max concurrent streams at 1 GPU; paged-attn HBM GB/s",

@@ -196,7 +196,11 @@ typedef struct pk_attn_args {
   void* out;
   int64_t out_stride_b;
   int64_t out_stride_t;
-  int32_t rows_per_lane; /* tuning: key rows per lane per tile, 0 = automatic */
+  int32_t rows_per_lane; /* kernel choice: 0 = automatic; 4, 9, 12, 18 = the vector-ALU
+                            kernel with that many key rows per lane; fp16/bf16 only:
+                            -1 = the two-query matrix-core kernel, -2 = the whole-chunk
+                            matrix-core kernel (chunk <= 14, window <= 96; automatic for
+                            chunks of 3..14 frames); fp32 ignores negative values */
   void* start_event;
   void* stop_event;
   const int32_t* live_streams;

@@ -1099,6 +1099,426 @@ __global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p
   }
 }
 
+// s_waitcnt that waits until at most n vector memory operations of the wave are
+// outstanding (vmcnt is 6 bits: [3:0] and [15:14]; expcnt and lgkmcnt left
+// at their no-wait maxima)
+#define PK_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(0x0f70 | ((n) & 15) | (((n) & 0x30) << 10))
+
+// DPP row_newbcast: every lane of a row of 16 reads lane `src` of its row
+template <int SRC>
+__device__ static inline float row_bcast(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x150 + SRC, 0xF, 0xF, false));
+}
+
+// ---------------------------------------------------------------------------
+// A whole chunk of queries (up to 14 frames a step, the large model's (70, 13)
+// context, parakeet/config.py:29) over one pass of the window.
+//
+// Workgroup of 4 waves: 2 streams of head h, each stream's window split by key
+// between 2 waves (wave kh takes window columns 48 kh .. 48 kh + 47), so every
+// K and V row of the window is read from HBM once for all of the chunk's
+// queries.  Each wave works on the whole head (head_dim columns).
+//
+// The matrix products are taken transposed, keys (or position rows) as the 16
+// M rows and queries as the 16 N columns, with one 16-bit operand for all of
+// them: row n < 14 of the query operand is q_n, row 14 is pos_bias_u, row 15 is
+// pos_bias_v.  So
+//   D = K_tile . Qop^T:    D[j][i] = q_i.k_j,   D[j][14] = u.k_j
+//   D = Pos_tile . Qop^T:  D[m][i] = q_i.pos_m, D[m][15] = v.pos_m
+// and (q_i + u).k_j = D[j][i] + D[j][14] exactly as the fp32 sum of products of
+// the stored 16-bit values, without splitting q + u into high and low parts.
+// The product's layout (lane = query column, registers = 4 consecutive keys) is
+// the A operand layout of the 16x16x16 P.V product: the probabilities go from
+// the softmax into P.V without a transpose.
+//   * position rows (shared by the workgroup's streams, rows 0 .. 16 * 7 - 1 of
+//     the table, slot j of query i reads row j + T - 1 - i) go straight to LDS;
+//     each wave multiplies the 4 tiles its keys read (rows 48 kh ..), adds
+//     v.pos with a row broadcast and leaves them in its LDS strip (after a
+//     workgroup barrier: the strip reuses the staging space), where the
+//     scores read them along the relative-position diagonal;
+//   * K rows as the A operand, from the pages (64-byte column blocks, one
+//     k-step of a tile is 16 rows x 64 bytes of one block) or, for this step's
+//     frames, from the projection output (one frame column per lane at most,
+//     selected in, every load unconditional); the V rows of a tile are issued
+//     into the registers its K rows free;
+//   * a softmax over the wave's keys (max and sum over the 4 lanes of a query
+//     column with two cross-row shuffles), probabilities split into high and
+//     low 16-bit parts, P.V on 16x16x16 MFMAs with V read back transposed from
+//     LDS (ds_read_b64_tr_b16);
+//   * the two key halves meet in LDS once, flash-style (each wave's running
+//     max, sum and the half of its output columns the other wave writes);
+//   * the fused append stores this step's frame rows into their pages as the
+//     wave's last instructions.
+template <typename ST, int DK, int MODE, bool STREAM>
+__global__ void __launch_bounds__(256) relpos_attn_chunk_kernel(const AttnK<ST> p) {
+  constexpr int NW = 4;
+  constexpr int NTH = 64 * NW;
+  constexpr int KS = DK / 32;       // 16x16x32 k-steps over the head
+  constexpr int NTW = 3;            // key tiles of 16 per wave
+  constexpr int KW = 16 * NTW;      // window columns per wave
+  constexpr int NPW = NTW + 1;      // position-row tiles per wave (rows KW*kh .. + 16*NPW - 1)
+  constexpr int CHR = DK / 8;       // 16-byte chunks per row
+  constexpr int RPB = 16 / CHR;     // staged rows per 256 bytes (all 64 banks)
+  constexpr int PSTRIDE = DK * 2;   // bytes per staged position row (unpadded, swizzled)
+  constexpr int PROWS_MIN = KW + 16 * NPW;  // rows the second wave's tiles reach
+  constexpr int PROWS = ((PROWS_MIN * CHR + NTH - 1) / NTH) * NTH / CHR;  // whole staging instructions
+  constexpr int PCH = PROWS * CHR / NTH;
+  constexpr int BDS = 20;           // floats per LDS row of a wave's position products (bank-conflict free)
+  constexpr int BD_BYTES = 16 * NPW * BDS * 4;
+  constexpr int VSTRIDE = DK * 2 + 16;  // bytes per staged V row
+  constexpr int WAVE_BYTES = BD_BYTES + 16 * VSTRIDE;
+  constexpr int NO = DK / 16;       // P.V output column tiles
+  constexpr int NOH = NO / 2;       // column tiles each wave writes
+  constexpr float NEG = -1e30f;
+  constexpr float MASKED = -1e5f * 1.4426950408889634f;  // -1e5 in log2 units
+  constexpr int ES = 2;
+  constexpr int BLK = 64;
+  constexpr int kPolicy = STREAM ? 2 : 0;
+  static_assert(PROWS * CHR % NTH == 0 && PROWS >= PROWS_MIN, "whole staging instructions");
+  static_assert(NO * 4 * 64 * 4 / 2 <= BD_BYTES, "output exchange fits the position strip");
+  static_assert(16 * (DK / 2) * 2 <= 16 * VSTRIDE, "output staging fits the V strip");
+  typedef typename Mma<ST>::H H;
+
+  constexpr int POS_BYTES = PROWS * PSTRIDE;
+  constexpr int STAGE_BYTES = POS_BYTES > NW * WAVE_BYTES ? POS_BYTES : NW * WAVE_BYTES;
+  __shared__ __attribute__((aligned(16))) uint8_t stage_lds[STAGE_BYTES];
+  __shared__ float ml_lds[NW][2][16];
+  uint8_t* const pos_lds = stage_lds;
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int q16 = lane & 15;
+  const int kg = lane >> 4;
+  const int sw = wave >> 1;  // stream slot in the workgroup
+  const int kh = wave & 1;   // key half
+  const int h = blockIdx.y;
+  const int b_raw = blockIdx.x * 2 + sw;
+  const int b = min(b_raw, p.B - 1);  // loads stay inside the batch arrays
+  const int hcol = h * DK;
+  const int jlo = KW * kh;            // first window column of the wave
+  const int M = p.pg.max_pages;
+  const bool paged = p.pg.rows != nullptr;
+  const int nblk = p.pg.D >> 5;
+  const int blk_soff = (hcol >> 5) << (p.pg.page_shift + 6);  // the head's first column block in a page
+  const int blk_step = 1 << (p.pg.page_shift + 6);
+  float* const bdl = reinterpret_cast<float*>(stage_lds + wave * WAVE_BYTES);
+  uint8_t* const vst = stage_lds + wave * WAVE_BYTES + BD_BYTES;
+
+  const int dmodel = p.H * DK;
+  const int st_q = (int)(p.q_st > 0 ? p.q_st : dmodel) * ES;
+  const int st_k = (int)(p.k_st > 0 ? p.k_st : dmodel) * ES;
+  const int st_v = (int)(p.v_st > 0 ? p.v_st : dmodel) * ES;
+  const int st_p = (int)(p.pos_sr > 0 ? p.pos_sr : dmodel) * ES;
+  const uint32_t pool_rows = paged ? ((uint32_t)p.pg.num_pages << p.pg.page_shift) * (uint32_t)nblk : 0u;
+  const __amdgpu_buffer_rsrc_t r_kp = rows_rsrc(paged ? (const void*)p.kp : (const void*)p.kn, BLK, pool_rows);
+  const __amdgpu_buffer_rsrc_t r_vp = rows_rsrc(paged ? (const void*)p.vp : (const void*)p.vn, BLK, pool_rows);
+  const __amdgpu_buffer_rsrc_t r_kn = rows_rsrc(p.kn + b * p.k_sb, st_k, (uint32_t)p.T);
+  const __amdgpu_buffer_rsrc_t r_vn = rows_rsrc(p.vn + b * p.v_sb, st_v, (uint32_t)p.T);
+  const __amdgpu_buffer_rsrc_t r_q = rows_rsrc(p.q + b * p.q_sb, st_q, (uint32_t)min(p.T, 14));
+  const __amdgpu_buffer_rsrc_t r_pos = rows_rsrc(p.pos, st_p, (uint32_t)p.pos_rows);
+
+  // ---------------- prologue: every load independent of the page table
+  // query operand: lane (kg, q16) holds row q16's columns ks*32 + kg*8 .. + 7
+  // (rows of queries past the chunk read zeros)
+  u32x4 qraw[KS], braw[KS];
+  {
+    const uint32_t qrow = q16 < 14 ? (uint32_t)q16 : kNoRow;
+    const ST* brow = (q16 == 15 ? p.bv : p.bu) + hcol + kg * 8;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      qraw[ks] = pk_buffer_load_x4(r_q, qrow, (hcol + ks * 32 + kg * 8) * ES, 0, 0);
+      braw[ks] = ld16(brow + ks * 32);
+    }
+  }
+  const int64_t hdr_off = (int64_t)b * p.pg.rows_stride;
+  const int32_t* hdr = paged ? p.pg.rows + hdr_off : reinterpret_cast<const int32_t*>(p.q);
+  const int hdr_a = hdr[0];
+  int ring_lane = hdr[paged ? 1 + min(lane, M - 1) : 0];
+  const int64_t* stp = MODE == 2 ? p.st_proc + b : reinterpret_cast<const int64_t*>(p.q);
+  const int64_t* stc = MODE == 2 ? p.st_cl + b : stp;
+  const int64_t* stn = (MODE == 2 && p.st_len) ? p.st_len + b : stp;
+  const int64_t st_pr_v = *stp, st_cl_v = *stc, st_n_v = *stn;
+  const int32_t nact_v = p.nact ? *p.nact : p.B;
+  // mask bytes of the lane's scores: query q16, window columns jlo + 16 kt + 4 kg + r
+  uint8_t mk[NTW][4];
+  if constexpr (MODE == 1) {
+    const int ic = min(q16, p.T - 1);
+#pragma unroll
+    for (int kt = 0; kt < NTW; ++kt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int jc = min(jlo + 16 * kt + 4 * kg + r, p.Lk - 1);
+        mk[kt][r] = p.mask[b * p.m_sb + h * p.m_sh + (int64_t)ic * p.m_st + jc];
+      }
+  }
+  // position rows 0 .. PROWS - 1 straight to LDS; chunk c of row r sits at
+  // chunk c ^ pkey(r), so the 16 rows of an operand read fall on distinct banks
+  auto pkey = [&](int row) { return (row / RPB) & (CHR - 1); };
+#pragma unroll
+  for (int c = 0; c < PCH; ++c) {
+    const int base = c * NTH + wave * 64;  // wave-uniform
+    const int idx = base + lane;
+    const int row = idx / CHR, cc = (idx % CHR) ^ pkey(row);
+    __builtin_amdgcn_struct_ptr_buffer_load_lds(r_pos, (__attribute__((address_space(3))) void*)(pos_lds + base * 16), 16,
+                                                row, (hcol + cc * 8) * ES, 0, 0, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // all of the above in flight before any use
+
+  // ---------------- live streams (workgroup-uniform exit; the staging into
+  //                  LDS completes before the workgroup leaves)
+  const int nact = min(__builtin_amdgcn_readfirstlane(nact_v), p.B);
+  if (blockIdx.x * 2 >= nact) {
+    PK_WAIT_VMCNT(0);
+    return;
+  }
+  const bool active = b_raw < nact;  // uniform per wave
+
+  // ---------------- per-stream scalars and the lane's page rows
+  const int A = paged ? __builtin_amdgcn_readfirstlane(hdr_a) : 0;
+  if (!paged) ring_lane = -1;
+  const int win0 = A - p.left;
+  const uint32_t lp0 = (uint32_t)max(win0, 0) >> p.pg.page_shift;
+  const int r0 = paged ? (int)(lp0 % (uint32_t)M) : 0;
+  const uint32_t pmask = (1u << p.pg.page_shift) - 1u;
+  const uint32_t page_blk_rows = (uint32_t)nblk << p.pg.page_shift;
+  auto page_row = [&](int j) {  // every lane active (ds_bpermute)
+    const int pos = win0 + j;
+    int ridx = r0 + (int)(((uint32_t)max(pos, 0) >> p.pg.page_shift) - lp0);
+    ridx = ridx >= M ? ridx - M : ridx;
+    const int page = __shfl(ring_lane, ridx);
+    return (paged && pos >= 0 && page >= 0) ? (uint32_t)page * page_blk_rows + ((uint32_t)pos & pmask) : kNoRow;
+  };
+  uint32_t prow[NTW];
+#pragma unroll
+  for (int kt = 0; kt < NTW; ++kt) {
+    const int j = jlo + 16 * kt + q16;
+    const uint32_t r = page_row(j);
+    prow[kt] = j < p.left ? r : kNoRow;
+  }
+  // the lane's frame column in the wave's range (the one congruent to its slot
+  // mod 16: chunks of at most 14 frames hold one), its tile and its page row
+  const bool do_append = p.append && active && paged;
+  const int fbase = max(p.left, jlo);
+  const int jf = fbase + ((jlo + q16 - fbase) & 15);
+  const bool fvalid = jf < p.Lk && jf < jlo + KW;
+  const int ftile = fvalid ? (jf - jlo) >> 4 : -1;
+  const uint32_t frow = fvalid ? (uint32_t)(jf - p.left) : kNoRow;
+  const uint32_t arow_f = page_row(jf);
+  const uint32_t arow = fvalid && do_append ? arow_f : kNoRow;
+  auto has_frames = [&](int kt) { return jlo + 16 * kt + 15 >= p.left && jlo + 16 * kt < p.Lk; };
+  auto with_frame = [&](int kt, u32x4 v, u32x4 f) {
+    if (has_frames(kt) && ftile == kt) v = f;
+    return v;
+  };
+
+  // ---------------- K rows (the frame row first: every tile's select reads it)
+  u32x4 kr[NTW][KS], vr[NTW][KS], kf[KS], vf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) kf[ks] = pk_buffer_load_x4(r_kn, frow, (hcol + ks * 32 + kg * 8) * ES, 0, 0);
+#pragma unroll
+  for (int kt = 0; kt < NTW; ++kt)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      kr[kt][ks] = pk_buffer_load_x4(r_kp, prow[kt], kg * 16, blk_soff + ks * blk_step, kPolicy);
+  __builtin_amdgcn_sched_barrier(0);  // exactly (1 + NTW) * KS loads after the staging
+
+  // score conditions while the K rows are in flight: bit kt*4 + r for window
+  // column jlo + 16 kt + 4 kg + r of query q16 (no value: past the window or
+  // the chunk; the mask's -1e5 term: the streaming rule)
+  StreamMask sm{};
+  uint32_t neg_bits = 0u, msk_bits = 0u;
+  if (MODE == 2) {
+    auto u64 = [](int64_t v) {
+      const int lo = __builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+      const int hi = __builtin_amdgcn_readfirstlane((int)(v >> 32));
+      return (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+    };
+    const int64_t n = p.st_len ? u64(st_n_v) : p.len_scalar;
+    sm.set(u64(st_pr_v), u64(st_cl_v), n, p.left, p.chunk_size, p.left_chunks, p.c_magic);
+  }
+  const int qchunk = MODE == 2 ? sm.query_chunk(q16) : 0;
+#pragma unroll
+  for (int kt = 0; kt < NTW; ++kt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int j = jlo + 16 * kt + 4 * kg + r;
+      const uint32_t bit = 1u << (kt * 4 + r);
+      if (!(j < p.Lk && q16 < p.T)) neg_bits |= bit;
+      if (MODE == 2 && sm.masked(q16, qchunk, j)) msk_bits |= bit;
+      if (MODE == 1 && mk[kt][r] != 0) msk_bits |= bit;
+    }
+  asm volatile("" ::"v"(neg_bits), "v"(msk_bits));
+
+  // query operand: q rows, u (row 14), v (row 15) as loaded
+  u32x4 qop[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) qop[ks] = q16 < 14 ? qraw[ks] : braw[ks];
+
+  // the position rows (issued before every K row) are in LDS
+  PK_WAIT_VMCNT((1 + NTW) * KS);
+  __syncthreads();
+
+  // ---- (q + v).pos: D[m][i] = q_i.pos_m, + v.pos_m from column 15
+  f32x4_t bdd[NPW];
+#pragma unroll
+  for (int pt = 0; pt < NPW; ++pt) {
+    f32x4_t d = {0.f, 0.f, 0.f, 0.f};
+    const int prw = jlo + 16 * pt + q16;
+    const uint8_t* src = pos_lds + prw * PSTRIDE;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int chunk = ks * 4 + kg;
+      d = Mma<ST>::k32(*reinterpret_cast<const u32x4*>(src + ((chunk ^ pkey(prw)) * 16)), qop[ks], d);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) d[r] += row_bcast<15>(d[r]);
+    bdd[pt] = d;
+  }
+  __syncthreads();  // every wave is done with the staged rows: the strips reuse them
+#pragma unroll
+  for (int pt = 0; pt < NPW; ++pt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) bdl[(16 * pt + 4 * kg + r) * BDS + q16] = bdd[pt][r];
+
+  // ---- (q + u).k: D[j][i] = q_i.k_j, + u.k_j from column 14; the V rows of a
+  //      tile go into the registers its K rows free (the frames' first)
+  f32x4_t acd[NTW];
+#pragma unroll
+  for (int kt = 0; kt < NTW; ++kt) {
+    f32x4_t d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) d = Mma<ST>::k32(with_frame(kt, kr[kt][ks], kf[ks]), qop[ks], d);
+    acd[kt] = d;
+    __builtin_amdgcn_sched_barrier(0);
+    if (kt == 0) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) vf[ks] = pk_buffer_load_x4(r_vn, frow, (hcol + ks * 32 + kg * 8) * ES, 0, 0);
+    }
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      vr[kt][ks] = pk_buffer_load_x4(r_vp, prow[kt], kg * 16, blk_soff + ks * blk_step, kPolicy);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  wave_lds_sync();  // the wave's position products in its strip
+
+  // ---- scores (window column j = jlo + 16 kt + 4 kg + r, query i = q16): the
+  //      position term of row j + T - 1 - i, local row 16 kt + 4 kg + r + T - 1 - i
+  float s[NTW][4];
+#pragma unroll
+  for (int kt = 0; kt < NTW; ++kt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int ml = min(max(16 * kt + 4 * kg + r + p.T - 1 - q16, 0), 16 * NPW - 1);
+      const float bd = bdl[ml * BDS + q16];
+      const float ac = acd[kt][r] + row_bcast<14>(acd[kt][r]);
+      const uint32_t bit = 1u << (kt * 4 + r);
+      const float sc = (msk_bits & bit) ? fmaf(ac, p.scale, MASKED) : (ac + bd) * p.scale;
+      s[kt][r] = (neg_bits & bit) ? NEG : sc;
+    }
+  // softmax over the wave's keys: a query's scores sit in the 4 lanes q16 + 16 kg
+  float mx = NEG;
+#pragma unroll
+  for (int kt = 0; kt < NTW; ++kt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[kt][r]);
+  mx = fmaxf(mx, __shfl_xor(mx, 16));
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  float lsum = 0.f;
+  i16x4_t phi[NTW], plo[NTW];
+#pragma unroll
+  for (int kt = 0; kt < NTW; ++kt) {
+    H hv[4], lv[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float e = s[kt][r] > 0.5f * NEG ? __builtin_amdgcn_exp2f(s[kt][r] - mx) : 0.f;
+      lsum += e;
+      hv[r] = (H)e;
+      lv[r] = (H)(e - (float)hv[r]);
+    }
+    phi[kt] = i16x4_t{__builtin_bit_cast(short, hv[0]), __builtin_bit_cast(short, hv[1]),
+                      __builtin_bit_cast(short, hv[2]), __builtin_bit_cast(short, hv[3])};
+    plo[kt] = i16x4_t{__builtin_bit_cast(short, lv[0]), __builtin_bit_cast(short, lv[1]),
+                      __builtin_bit_cast(short, lv[2]), __builtin_bit_cast(short, lv[3])};
+  }
+  lsum += __shfl_xor(lsum, 16);
+  lsum += __shfl_xor(lsum, 32);
+
+  // ---- P.V: D[i][c] over 16 keys a tile, V staged row-major and read back
+  //      transposed; p = hi + lo
+  f32x4_t oacc[NO];
+#pragma unroll
+  for (int nt = 0; nt < NO; ++nt) oacc[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int kt = 0; kt < NTW; ++kt) {
+    uint8_t* vrow = vst + q16 * VSTRIDE + kg * 16;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) *reinterpret_cast<u32x4*>(vrow + ks * 64) = with_frame(kt, vr[kt][ks], vf[ks]);
+    wave_lds_sync();
+#pragma unroll
+    for (int nt = 0; nt < NO; ++nt) {
+      const uint8_t* src = vst + (4 * kg + (q16 >> 2)) * VSTRIDE + (nt * 16 + 4 * (q16 & 3)) * 2;
+      const i16x4_t vt = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t*)src);
+      oacc[nt] = Mma<ST>::k16(phi[kt], vt, oacc[nt]);
+      oacc[nt] = Mma<ST>::k16(plo[kt], vt, oacc[nt]);
+    }
+    wave_lds_sync();  // the next tile overwrites the staging rows
+  }
+
+  // ---- the key halves meet: each wave leaves its max and sum per query and
+  //      the output columns the other wave writes (in its own strip)
+  if (kg == 0) {
+    ml_lds[wave][0][q16] = mx;
+    ml_lds[wave][1][q16] = lsum;
+  }
+  float* const xo_own = bdl;
+  const float* const xo_other = reinterpret_cast<const float*>(stage_lds + (wave ^ 1) * WAVE_BYTES);
+#pragma unroll
+  for (int n = 0; n < NOH; ++n)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) xo_own[(n * 4 + r) * 64 + lane] = oacc[(1 - kh) * NOH + n][r];
+  __syncthreads();
+  // lane (kg, q16) holds output rows (queries) 4 kg + r, column 16 nt + q16
+  H* const ost = reinterpret_cast<H*>(vst);  // [16 queries][DK / 2 columns]
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int qi = 4 * kg + r;
+    const float m0 = ml_lds[wave][0][qi], l0 = ml_lds[wave][1][qi];
+    const float m1 = ml_lds[wave ^ 1][0][qi], l1 = ml_lds[wave ^ 1][1][qi];
+    const float mm = fmaxf(m0, m1);
+    const float c0 = __builtin_amdgcn_exp2f(m0 - mm), c1 = __builtin_amdgcn_exp2f(m1 - mm);
+    const float den = c0 * l0 + c1 * l1;
+    const float inv = den > 0.f ? __builtin_amdgcn_rcpf(den) : 0.f;
+#pragma unroll
+    for (int n = 0; n < NOH; ++n) {
+      const float o = (c0 * oacc[kh * NOH + n][r] + c1 * xo_other[(n * 4 + r) * 64 + lane]) * inv;
+      ost[qi * (DK / 2) + n * 16 + q16] = (H)o;
+    }
+  }
+  wave_lds_sync();
+  if (active) {
+    constexpr int CPR = DK / 16;  // 16-byte chunks per output half-row
+#pragma unroll
+    for (int c = 0; c < DK / 64; ++c) {
+      const int idx = c * 64 + lane;
+      const int qi = idx / CPR, ch = idx % CPR;
+      if (qi < p.T) {
+        const u32x4 o = *reinterpret_cast<const u32x4*>(vst + qi * DK + ch * 16);
+        u32x4* const dst = reinterpret_cast<u32x4*>(p.out + b * p.o_sb + (int64_t)qi * p.o_st + hcol + kh * (DK / 2) + ch * 8);
+        if constexpr (STREAM)
+          __builtin_nontemporal_store(o, dst);
+        else
+          *dst = o;
+      }
+    }
+  }
+  // ---- fused append (row kNoRow where the lane holds no frame)
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) pk_buffer_store_x4(kf[ks], r_kp, arow, kg * 16, blk_soff + ks * blk_step, kPolicy);
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) pk_buffer_store_x4(vf[ks], r_vp, arow, kg * 16, blk_soff + ks * blk_step, kPolicy);
+}
+
 // ---------------------------------------------------------------------------
 // append / gather
 
@@ -1385,6 +1805,40 @@ int launch_attn_mfma(const pk_attn_args* a, AttnK<ST>& k, hipStream_t s) {
   return launch_attn_mfma_mode<ST, DK, 0>(a, k, s);
 }
 
+// Whole-chunk matrix-core path: workgroups of 2 streams x one head, the
+// window split by key between a stream's two waves (48 columns each).
+constexpr int kChunkMaxT = 14;      // query operand rows 0..13 (14: u, 15: v)
+constexpr int kChunkMaxWindow = 96;  // 2 waves x 3 tiles of 16 window columns
+
+template <typename ST, int DK, int MODE, bool STREAM>
+int launch_attn_chunk_t(const pk_attn_args* a, const AttnK<ST>& k, hipStream_t s) {
+  dim3 grid((unsigned)((a->batch + 1) / 2), (unsigned)a->num_heads);
+  dim3 block(256u);
+  if (a->start_event || a->stop_event) {
+    hipExtLaunchKernelGGL(relpos_attn_chunk_kernel<ST, DK, MODE, STREAM>, grid, block, 0u, s,
+                          (hipEvent_t)a->start_event, (hipEvent_t)a->stop_event, 0u, k);
+  } else {
+    hipLaunchKernelGGL((relpos_attn_chunk_kernel<ST, DK, MODE, STREAM>), grid, block, 0, s, k);
+  }
+  return check_launch("pk_paged_relpos_attn");
+}
+
+template <typename ST, int DK, int MODE>
+int launch_attn_chunk_mode(const pk_attn_args* a, const AttnK<ST>& k, hipStream_t s) {
+  const int64_t layers = a->pages.num_layers > 1 ? a->pages.num_layers : 1;
+  const int64_t window_bytes = (int64_t)a->batch * k.Lk * a->num_heads * DK * (int64_t)sizeof(ST) * 2 * layers;
+  if (k.pg.rows != nullptr && window_bytes > kStreamingBytes) return launch_attn_chunk_t<ST, DK, MODE, true>(a, k, s);
+  return launch_attn_chunk_t<ST, DK, MODE, false>(a, k, s);
+}
+
+template <typename ST, int DK>
+int launch_attn_chunk(const pk_attn_args* a, AttnK<ST>& k, hipStream_t s) {
+  k.tiles = 1;
+  if (k.mask) return launch_attn_chunk_mode<ST, DK, 1>(a, k, s);
+  if (k.st_proc) return launch_attn_chunk_mode<ST, DK, 2>(a, k, s);
+  return launch_attn_chunk_mode<ST, DK, 0>(a, k, s);
+}
+
 template <typename ST>
 int attn_typed(const pk_attn_args* a, hipStream_t s) {
   constexpr int VEC = Tr<ST>::VEC;
@@ -1496,11 +1950,31 @@ int attn_typed(const pk_attn_args* a, hipStream_t s) {
                       row_bytes(a->pos_stride) <= kMaxBufferStride &&
                       (!need_pages || k.pg.cb_shift == 5);  // 64-byte page column blocks
     // per-stream position tables take the vector-ALU kernel: the matrix-core
-    // kernel stages one table per workgroup for all of its streams
-    if (a->rows_per_lane == 0 && fits && a->chunk <= 16 && a->pos_stride_b == 0) {
+    // kernels stage one table per workgroup for all of its streams
+    const bool mfma_ok = fits && a->pos_stride_b == 0;
+    // whole-chunk kernel: chunks of 3..14 frames over a window of at most 96
+    // (the query operand's row stride is a buffer stride too); rows_per_lane
+    // -2 asks for it at any chunk it supports, -1 for the two-query kernel
+    const bool chunk_ok = mfma_ok && a->chunk <= kChunkMaxT && Lk <= kChunkMaxWindow &&
+                          row_bytes(a->query_stride_t) <= kMaxBufferStride;
+    if (a->rows_per_lane == -2) {
+      if (!chunk_ok)
+        return fail(PK_ERR_UNSUPPORTED, "%s: the whole-chunk kernel needs chunk <= %d, window <= %d, one position table",
+                    what, kChunkMaxT, kChunkMaxWindow);
+      if (DK == 64) return launch_attn_chunk<ST, 64>(a, k, s);
+      return launch_attn_chunk<ST, 128>(a, k, s);
+    }
+    if (a->rows_per_lane == 0 && chunk_ok && a->chunk >= 3) {
+      if (DK == 64) return launch_attn_chunk<ST, 64>(a, k, s);
+      return launch_attn_chunk<ST, 128>(a, k, s);
+    }
+    if ((a->rows_per_lane == 0 || a->rows_per_lane == -1) && mfma_ok && a->chunk <= 16) {
       if (DK == 64) return launch_attn_mfma<ST, 64>(a, k, s);
       return launch_attn_mfma<ST, 128>(a, k, s);
     }
+    if (a->rows_per_lane < 0)
+      return fail(PK_ERR_UNSUPPORTED, "%s: rows_per_lane %d asks for a matrix-core kernel this call cannot take", what,
+                  a->rows_per_lane);
   }
   const int G = DK / VEC;
   const int rlw = 64 / G;

@@ -52,6 +52,9 @@ class Shape:
 SMALL_FP32 = Shape("small-1layer-fp32", 1, 512, 8, dtype=torch.float32)
 SMALL_FP16 = Shape("small-17layer-fp16", 17, 512, 8, dtype=torch.float16)
 LARGE_BF16 = Shape("large-24layer-bf16", 24, 1024, 8, dtype=torch.bfloat16)
+# the large model's own attention context (70, 13): 14 frames per step, an
+# 84-frame window (parakeet/config.py:29, parakeet/modules/cache.py:22)
+LARGE_BF16_T14 = Shape("large-24layer-bf16-t14", 24, 1024, 8, right=13, dtype=torch.bfloat16)
 
 
 def sinusoid_slice(d_model: int, left: int, chunk: int, max_len: int = 5000) -> torch.Tensor:

@@ -137,6 +137,30 @@ def test_frames_across_tiles_and_passes(cuda, left, right, dk):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize(
+    "left,right,dk,dtype,kind",
+    [
+        (70, 13, 128, torch.bfloat16, "engine"),
+        (70, 13, 64, torch.float16, "state-ragged"),
+        (40, 13, 128, torch.bfloat16, "ragged"),  # frames 40..53 straddle the waves' key ranges (48)
+        (34, 13, 64, torch.float16, "random"),  # frames end at window column 47
+        (82, 13, 128, torch.bfloat16, "state"),  # a window of 96, the most one pass holds
+        (70, 0, 128, torch.bfloat16, "engine"),  # 1 and 2 frames through the whole-chunk kernel
+        (70, 1, 64, torch.float16, "random"),
+        (20, 8, 128, torch.float16, "state-ragged"),
+        (5, 4, 64, torch.bfloat16, "ragged"),
+    ],
+)
+def test_whole_chunk_kernel(cuda, left, right, dk, dtype, kind):
+    """The whole-chunk matrix-core kernel (rows_per_lane -2): every query of a
+    chunk over one pass of the window, the window split by key between two
+    waves; frames on either side of and across the split, windows up to the
+    96 columns one pass holds, every mask source, against the oracle."""
+    steps = max(8, (left + right) // (right + 1) + 4)
+    _run(cuda, dtype, B=3, H=4, dk=dk, left=left, right=right, P=16, steps=steps, mask_kind=kind, rows_per_lane=-2)
+
+
+@pytest.mark.gpu
 def test_long_window_multi_tile(cuda):
     # left context long enough that the window needs several tiles
     _run(cuda, torch.float16, B=2, H=8, dk=64, left=600, right=1, P=16, steps=6, layers=1)
@@ -235,10 +259,11 @@ def test_state_mask_identical_to_mask_tensor(cuda, left, right, dtype):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("B,dk,dtype", [(130, 128, torch.bfloat16), (200, 128, torch.bfloat16),
-                                        (256, 128, torch.bfloat16), (384, 64, torch.bfloat16),
-                                        (384, 64, torch.float16)])
-def test_batch_split_is_bit_exact(cuda, B, dk, dtype):
+@pytest.mark.parametrize("B,dk,dtype,right", [(130, 128, torch.bfloat16, 1), (200, 128, torch.bfloat16, 1),
+                                              (256, 128, torch.bfloat16, 1), (384, 64, torch.bfloat16, 1),
+                                              (384, 64, torch.float16, 1), (256, 128, torch.bfloat16, 13),
+                                              (131, 64, torch.float16, 13)])
+def test_batch_split_is_bit_exact(cuda, B, dk, dtype, right):
     """Every stream's output of a launch over the whole batch equals, bit for
     bit, that of the same streams launched 64 at a time (odd block sizes
     included: 130 = 2 x 64 + 2), and the oracle's within tolerance; the fused
@@ -249,13 +274,14 @@ def test_batch_split_is_bit_exact(cuda, B, dk, dtype):
     (226 MB; bf16 and fp16): those whole-batch launches read with the streaming cache policy
     (with a mask tensor, the form the encoder step uses), the 64-stream blocks
     with the cached one, and the results must not differ."""
-    H, left, right, P = 8, 70, 1, 16
-    print(f"\n[attn batch split] B={B} dk={dk} dtype={dtype}", flush=True)
+    H, left, P = 8, 70, 16
+    print(f"\n[attn batch split] B={B} dk={dk} dtype={dtype} right={right}", flush=True)
     sc = PagedScenario(cuda, dtype, B=B, layers=4, d_model=H * dk, left=left, right=right, page_size=P, seed=B)
     pos, bu, bv = _relpos(sc, H, B)
     T = sc.T
     proc = np.zeros(B, dtype=np.int64)
-    for step in range(40):
+    steps = 40 if right == 1 else 12
+    for step in range(steps):
         sc.open_step()
         cl = np.minimum(proc, left)
         _, mask_np = om.create_streaming_masks(T, cl, proc, np.full(B, T), (left, right))
@@ -272,7 +298,7 @@ def test_batch_split_is_bit_exact(cuda, B, dk, dtype):
                 assert torch.equal(_bits16(whole[b0:b1]), _bits16(part)), f"step {step}: streams {b0}..{b1 - 1} differ"
         out = ops.paged_relpos_attn(q, k, v, pos, bu, bv, mask, pages=sc.pages, append=True, **args)
         dk_win, dv_win = sc.dense_update(0, k, v)
-        if step in (0, 39):
+        if step in (0, steps - 1):
             # At step 0 a query sees two unit-variance frames, so outputs reach
             # 4.2 here, where bf16 values lie 2**-5 apart: the nearest bf16 to
             # the oracle's 4.2339 is already 0.0151 from it.  The bar applies

@@ -4,7 +4,9 @@ step (parakeet_amd.step.AttentionStep) with continuous arrivals and departures:
 * large shape (d_model 1024, 8 heads x 128, bf16) with 256 stream slots at 90%
   steady occupancy, lifetimes U(2, 30) s (the 256-stream benchmark workload);
 * fragmentation stress: small shape (d_model 512, 8 x 64, fp16), 1024 slots,
-  the page pool pre-shuffled by a seeded permutation, lifetimes log-U(1, 60) s.
+  the page pool pre-shuffled by a seeded permutation, lifetimes log-U(1, 60) s;
+* the large shape at the large model's own chunk of 14 frames (att_context
+  (70, 13), parakeet/config.py:29), 256 slots at 90% occupancy.
 
 Four layers for the large shape and two for the fragmentation stress, over
 enough steps that windows fill, pages are evicted and reused, and slots are
@@ -47,6 +49,10 @@ CASES = {
                             ("uniform", 2.0, 30.0), False, 3, 220),
     "frag_1024slots_fp16": (synth.Shape("small-2layer-fp16", 2, 512, 8, dtype=torch.float16), 1024, 1.0,
                             ("loguniform", 1.0, 60.0), True, 4, 300),
+    # the large model's own context (70, 13): 14 frames a step, 84-frame windows
+    # (the whole-chunk kernel; 230 x 84 x 1024 x 2 x 2 x 4 = 317 MB a launch, streaming)
+    "large_t14_256slots_bf16": (synth.Shape("large-4layer-bf16-t14", 4, 1024, 8, right=13, dtype=torch.bfloat16), 256,
+                                0.9, ("uniform", 2.0, 30.0), False, 3, 80),
 }
 
 
@@ -103,7 +109,8 @@ def test_full_size_churn_pages_and_attention(cuda, case):
         assert np.array_equal(st.rows[:B].cpu().numpy(), rows_ref), f"step {step}: block-table rows differ from the model"
         idx = torch.from_numpy(active.astype(np.int64)).to(cuda)
         pages = ops.PagedKV(st.k_pages, st.v_pages, st.rows[:B], st.pool.max_pages)
-        sample = rng.choice(B, size=min(4, B), replace=False) if step % 20 == 19 else None
+        every = 20 if T <= 2 else 10
+        sample = rng.choice(B, size=min(4, B), replace=False) if step % every == every - 1 else None
         if sample is not None:
             _, mask = om.create_streaming_masks(T, cl[active[sample]], proc[active[sample]], T, (left, shape.right))
         for layer in range(Ly):
