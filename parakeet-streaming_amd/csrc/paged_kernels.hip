@@ -1131,58 +1131,66 @@ __device__ static inline float row_bcast(float v) {
 // The product's layout (lane = query column, registers = 4 consecutive keys) is
 // the A operand layout of the 16x16x16 P.V product: the probabilities go from
 // the softmax into P.V without a transpose.
-//   * position rows (shared by the workgroup's streams, rows 0 .. 16 * 7 - 1 of
-//     the table, slot j of query i reads row j + T - 1 - i) go straight to LDS;
-//     each wave multiplies the 4 tiles its keys read (rows 48 kh ..), adds
-//     v.pos with a row broadcast and leaves them in its LDS strip (after a
-//     workgroup barrier: the strip reuses the staging space), where the
-//     scores read them along the relative-position diagonal;
+//   * position rows (shared by the workgroup's streams; slot j of query i reads
+//     row j + T - 1 - i) and this step's K frame rows go straight to LDS
+//     (buffer loads to LDS: no registers held); each wave multiplies the 4
+//     position tiles its keys read (rows 48 kh ..), adds v.pos with a row
+//     broadcast and leaves them in its LDS strip (after a workgroup barrier:
+//     the strips reuse the staging space), where the scores read them along
+//     the relative-position diagonal;
 //   * K rows as the A operand, from the pages (64-byte column blocks, one
-//     k-step of a tile is 16 rows x 64 bytes of one block) or, for this step's
-//     frames, from the projection output (one frame column per lane at most,
-//     selected in, every load unconditional); the V rows of a tile are issued
-//     into the registers its K rows free;
+//     k-step of a tile is 16 rows x 64 bytes of one block, absent rows read
+//     zeros through the buffer range check) or, for this step's frames, from
+//     the staged frame rows; the V rows of a tile are issued into the
+//     registers its K rows free, with the lane's V frame row (one at most);
 //   * a softmax over the wave's keys (max and sum over the 4 lanes of a query
 //     column with two cross-row shuffles), probabilities split into high and
 //     low 16-bit parts, P.V on 16x16x16 MFMAs with V read back transposed from
-//     LDS (ds_read_b64_tr_b16);
-//   * the two key halves meet in LDS once, flash-style (each wave's running
-//     max, sum and the half of its output columns the other wave writes);
-//   * the fused append stores this step's frame rows into their pages as the
-//     wave's last instructions.
+//     LDS (ds_read_b64_tr_b16), in two halves of the head's columns so the
+//     first half's V registers are free before the second's accumulators;
+//   * the two key halves meet in LDS once, flash-style: each wave's max and
+//     sum per query, and the column half the other wave writes out;
+//   * the fused append stores the frame rows into their pages (K after the K
+//     products, V after P.V).
+// 4 waves a SIMD: at most 128 registers a lane and 40 KB of LDS a workgroup.
 template <typename ST, int DK, int MODE, bool STREAM>
-__global__ void __launch_bounds__(256) relpos_attn_chunk_kernel(const AttnK<ST> p) {
+__global__ void __launch_bounds__(256, 4) relpos_attn_chunk_kernel(const AttnK<ST> p) {
   constexpr int NW = 4;
   constexpr int NTH = 64 * NW;
   constexpr int KS = DK / 32;       // 16x16x32 k-steps over the head
+  constexpr int KSH = KS / 2;       // k-steps (64-byte column blocks) per column half
   constexpr int NTW = 3;            // key tiles of 16 per wave
   constexpr int KW = 16 * NTW;      // window columns per wave
   constexpr int NPW = NTW + 1;      // position-row tiles per wave (rows KW*kh .. + 16*NPW - 1)
   constexpr int CHR = DK / 8;       // 16-byte chunks per row
   constexpr int RPB = 16 / CHR;     // staged rows per 256 bytes (all 64 banks)
-  constexpr int PSTRIDE = DK * 2;   // bytes per staged position row (unpadded, swizzled)
+  constexpr int RSTRIDE = DK * 2;   // bytes per staged row (unpadded, swizzled)
   constexpr int PROWS_MIN = KW + 16 * NPW;  // rows the second wave's tiles reach
   constexpr int PROWS = ((PROWS_MIN * CHR + NTH - 1) / NTH) * NTH / CHR;  // whole staging instructions
   constexpr int PCH = PROWS * CHR / NTH;
+  constexpr int FCH = CHR / 8;      // frame staging instructions per wave (16 rows of its stream, 2 waves)
   constexpr int BDS = 20;           // floats per LDS row of a wave's position products (bank-conflict free)
   constexpr int BD_BYTES = 16 * NPW * BDS * 4;
-  constexpr int VSTRIDE = DK * 2 + 16;  // bytes per staged V row
+  constexpr int HC = DK / 2;        // columns per half
+  constexpr int VSTRIDE = HC * 2 + 16;  // bytes per staged V row (one column half)
   constexpr int WAVE_BYTES = BD_BYTES + 16 * VSTRIDE;
-  constexpr int NO = DK / 16;       // P.V output column tiles
-  constexpr int NOH = NO / 2;       // column tiles each wave writes
+  constexpr int NOH = HC / 16;      // P.V output column tiles per half
   constexpr float NEG = -1e30f;
   constexpr float MASKED = -1e5f * 1.4426950408889634f;  // -1e5 in log2 units
   constexpr int ES = 2;
   constexpr int BLK = 64;
   constexpr int kPolicy = STREAM ? 2 : 0;
   static_assert(PROWS * CHR % NTH == 0 && PROWS >= PROWS_MIN, "whole staging instructions");
-  static_assert(NO * 4 * 64 * 4 / 2 <= BD_BYTES, "output exchange fits the position strip");
-  static_assert(16 * (DK / 2) * 2 <= 16 * VSTRIDE, "output staging fits the V strip");
+  static_assert(NOH * 4 * 64 * 4 <= BD_BYTES, "output exchange fits the position strip");
+  static_assert(16 * HC * 2 <= 16 * VSTRIDE, "output staging fits the V strip");
+  static_assert(FCH >= 1 && 16 * CHR == 2 * 64 * FCH, "a stream's 16 frame rows in 2 waves x FCH instructions");
   typedef typename Mma<ST>::H H;
 
-  constexpr int POS_BYTES = PROWS * PSTRIDE;
+  constexpr int POS_BYTES = PROWS * RSTRIDE;
   constexpr int STAGE_BYTES = POS_BYTES > NW * WAVE_BYTES ? POS_BYTES : NW * WAVE_BYTES;
+  constexpr int KFR_BYTES = 16 * RSTRIDE;  // a stream's frame rows 0..15 (rows >= T read zeros)
   __shared__ __attribute__((aligned(16))) uint8_t stage_lds[STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t kfr_lds[2 * KFR_BYTES];
   __shared__ float ml_lds[NW][2][16];
   uint8_t* const pos_lds = stage_lds;
 
@@ -1204,6 +1212,7 @@ __global__ void __launch_bounds__(256) relpos_attn_chunk_kernel(const AttnK<ST> 
   const int blk_step = 1 << (p.pg.page_shift + 6);
   float* const bdl = reinterpret_cast<float*>(stage_lds + wave * WAVE_BYTES);
   uint8_t* const vst = stage_lds + wave * WAVE_BYTES + BD_BYTES;
+  uint8_t* const kfr = kfr_lds + sw * KFR_BYTES;
 
   const int dmodel = p.H * DK;
   const int st_q = (int)(p.q_st > 0 ? p.q_st : dmodel) * ES;
@@ -1252,8 +1261,9 @@ __global__ void __launch_bounds__(256) relpos_attn_chunk_kernel(const AttnK<ST> 
         mk[kt][r] = p.mask[b * p.m_sb + h * p.m_sh + (int64_t)ic * p.m_st + jc];
       }
   }
-  // position rows 0 .. PROWS - 1 straight to LDS; chunk c of row r sits at
-  // chunk c ^ pkey(r), so the 16 rows of an operand read fall on distinct banks
+  // position rows 0 .. PROWS - 1 and the stream's K frame rows 0 .. 15 straight
+  // to LDS; chunk c of row r sits at chunk c ^ pkey(r), so the 16 rows of an
+  // operand read fall on distinct banks
   auto pkey = [&](int row) { return (row / RPB) & (CHR - 1); };
 #pragma unroll
   for (int c = 0; c < PCH; ++c) {
@@ -1261,6 +1271,14 @@ __global__ void __launch_bounds__(256) relpos_attn_chunk_kernel(const AttnK<ST> 
     const int idx = base + lane;
     const int row = idx / CHR, cc = (idx % CHR) ^ pkey(row);
     __builtin_amdgcn_struct_ptr_buffer_load_lds(r_pos, (__attribute__((address_space(3))) void*)(pos_lds + base * 16), 16,
+                                                row, (hcol + cc * 8) * ES, 0, 0, 0);
+  }
+#pragma unroll
+  for (int c = 0; c < FCH; ++c) {
+    const int base = (kh * FCH + c) * 64;  // wave-uniform chunk of the stream's frame rows
+    const int idx = base + lane;
+    const int row = idx / CHR, cc = (idx % CHR) ^ pkey(row);
+    __builtin_amdgcn_struct_ptr_buffer_load_lds(r_kn, (__attribute__((address_space(3))) void*)(kfr + base * 16), 16,
                                                 row, (hcol + cc * 8) * ES, 0, 0, 0);
   }
   __builtin_amdgcn_sched_barrier(0);  // all of the above in flight before any use
@@ -1273,6 +1291,13 @@ __global__ void __launch_bounds__(256) relpos_attn_chunk_kernel(const AttnK<ST> 
     return;
   }
   const bool active = b_raw < nact;  // uniform per wave
+
+  // query operand: q rows, u (row 14), v (row 15) as loaded (they were issued
+  // ahead of the block-table ring, which the page rows wait for anyway)
+  u32x4 qop[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) qop[ks] = q16 < 14 ? qraw[ks] : braw[ks];
+  asm volatile("" ::"v"(qop[0]));  // selected here, not where first used
 
   // ---------------- per-stream scalars and the lane's page rows
   const int A = paged ? __builtin_amdgcn_readfirstlane(hdr_a) : 0;
@@ -1303,25 +1328,24 @@ __global__ void __launch_bounds__(256) relpos_attn_chunk_kernel(const AttnK<ST> 
   const int jf = fbase + ((jlo + q16 - fbase) & 15);
   const bool fvalid = jf < p.Lk && jf < jlo + KW;
   const int ftile = fvalid ? (jf - jlo) >> 4 : -1;
-  const uint32_t frow = fvalid ? (uint32_t)(jf - p.left) : kNoRow;
+  const int ft = fvalid ? jf - p.left : 0;  // its frame (row of the staged frames)
+  const uint32_t frow = fvalid ? (uint32_t)ft : kNoRow;
   const uint32_t arow_f = page_row(jf);
   const uint32_t arow = fvalid && do_append ? arow_f : kNoRow;
   auto has_frames = [&](int kt) { return jlo + 16 * kt + 15 >= p.left && jlo + 16 * kt < p.Lk; };
-  auto with_frame = [&](int kt, u32x4 v, u32x4 f) {
-    if (has_frames(kt) && ftile == kt) v = f;
-    return v;
+  // the lane's staged K frame row, 16 bytes of k-step ks
+  auto kframe = [&](int ks) {
+    return *reinterpret_cast<const u32x4*>(kfr + ft * RSTRIDE + (((ks * 4 + kg) ^ pkey(ft)) * 16));
   };
 
-  // ---------------- K rows (the frame row first: every tile's select reads it)
-  u32x4 kr[NTW][KS], vr[NTW][KS], kf[KS], vf[KS];
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) kf[ks] = pk_buffer_load_x4(r_kn, frow, (hcol + ks * 32 + kg * 8) * ES, 0, 0);
+  // ---------------- K rows
+  u32x4 kr[NTW][KS], vr[NTW][KS], vf[KS];
 #pragma unroll
   for (int kt = 0; kt < NTW; ++kt)
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
       kr[kt][ks] = pk_buffer_load_x4(r_kp, prow[kt], kg * 16, blk_soff + ks * blk_step, kPolicy);
-  __builtin_amdgcn_sched_barrier(0);  // exactly (1 + NTW) * KS loads after the staging
+  __builtin_amdgcn_sched_barrier(0);  // exactly NTW * KS loads after the staging
 
   // score conditions while the K rows are in flight: bit kt*4 + r for window
   // column jlo + 16 kt + 4 kg + r of query q16 (no value: past the window or
@@ -1348,15 +1372,11 @@ __global__ void __launch_bounds__(256) relpos_attn_chunk_kernel(const AttnK<ST> 
       if (MODE == 2 && sm.masked(q16, qchunk, j)) msk_bits |= bit;
       if (MODE == 1 && mk[kt][r] != 0) msk_bits |= bit;
     }
-  asm volatile("" ::"v"(neg_bits), "v"(msk_bits));
+  // one register each from here on (not their partial products)
+  asm volatile("" : "+v"(neg_bits), "+v"(msk_bits));
 
-  // query operand: q rows, u (row 14), v (row 15) as loaded
-  u32x4 qop[KS];
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) qop[ks] = q16 < 14 ? qraw[ks] : braw[ks];
-
-  // the position rows (issued before every K row) are in LDS
-  PK_WAIT_VMCNT((1 + NTW) * KS);
+  // the position rows and frame rows (issued before every K row) are in LDS
+  PK_WAIT_VMCNT(NTW * KS);
   __syncthreads();
 
   // ---- (q + v).pos: D[m][i] = q_i.pos_m, + v.pos_m from column 15
@@ -1365,7 +1385,7 @@ __global__ void __launch_bounds__(256) relpos_attn_chunk_kernel(const AttnK<ST> 
   for (int pt = 0; pt < NPW; ++pt) {
     f32x4_t d = {0.f, 0.f, 0.f, 0.f};
     const int prw = jlo + 16 * pt + q16;
-    const uint8_t* src = pos_lds + prw * PSTRIDE;
+    const uint8_t* src = pos_lds + prw * RSTRIDE;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int chunk = ks * 4 + kg;
@@ -1381,14 +1401,24 @@ __global__ void __launch_bounds__(256) relpos_attn_chunk_kernel(const AttnK<ST> 
 #pragma unroll
     for (int r = 0; r < 4; ++r) bdl[(16 * pt + 4 * kg + r) * BDS + q16] = bdd[pt][r];
 
-  // ---- (q + u).k: D[j][i] = q_i.k_j, + u.k_j from column 14; the V rows of a
-  //      tile go into the registers its K rows free (the frames' first)
+  // ---- (q + u).k: D[j][i] = q_i.k_j, + u.k_j from column 14; the frame rows
+  //      (staged) in place of the page rows (zeros) where the tile holds
+  //      them; the V rows of a tile go into the registers its K rows free
   f32x4_t acd[NTW];
 #pragma unroll
   for (int kt = 0; kt < NTW; ++kt) {
     f32x4_t d = {0.f, 0.f, 0.f, 0.f};
+    if (has_frames(kt)) {  // wave-uniform
+      const bool mine = ftile == kt;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) d = Mma<ST>::k32(with_frame(kt, kr[kt][ks], kf[ks]), qop[ks], d);
+      for (int ks = 0; ks < KS; ++ks) {
+        const u32x4 f = kframe(ks);
+        d = Mma<ST>::k32(mine ? f : kr[kt][ks], qop[ks], d);
+      }
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) d = Mma<ST>::k32(kr[kt][ks], qop[ks], d);
+    }
     acd[kt] = d;
     __builtin_amdgcn_sched_barrier(0);
     if (kt == 0) {
@@ -1400,6 +1430,9 @@ __global__ void __launch_bounds__(256) relpos_attn_chunk_kernel(const AttnK<ST> 
       vr[kt][ks] = pk_buffer_load_x4(r_vp, prow[kt], kg * 16, blk_soff + ks * blk_step, kPolicy);
     __builtin_amdgcn_sched_barrier(0);
   }
+  // the frames' K rows to their pages (row kNoRow where the lane holds no frame)
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) pk_buffer_store_x4(kframe(ks), r_kp, arow, kg * 16, blk_soff + ks * blk_step, kPolicy);
   wave_lds_sync();  // the wave's position products in its strip
 
   // ---- scores (window column j = jlo + 16 kt + 4 kg + r, query i = q16): the
@@ -1443,43 +1476,60 @@ __global__ void __launch_bounds__(256) relpos_attn_chunk_kernel(const AttnK<ST> 
   }
   lsum += __shfl_xor(lsum, 16);
   lsum += __shfl_xor(lsum, 32);
-
-  // ---- P.V: D[i][c] over 16 keys a tile, V staged row-major and read back
-  //      transposed; p = hi + lo
-  f32x4_t oacc[NO];
-#pragma unroll
-  for (int nt = 0; nt < NO; ++nt) oacc[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int kt = 0; kt < NTW; ++kt) {
-    uint8_t* vrow = vst + q16 * VSTRIDE + kg * 16;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) *reinterpret_cast<u32x4*>(vrow + ks * 64) = with_frame(kt, vr[kt][ks], vf[ks]);
-    wave_lds_sync();
-#pragma unroll
-    for (int nt = 0; nt < NO; ++nt) {
-      const uint8_t* src = vst + (4 * kg + (q16 >> 2)) * VSTRIDE + (nt * 16 + 4 * (q16 & 3)) * 2;
-      const i16x4_t vt = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t*)src);
-      oacc[nt] = Mma<ST>::k16(phi[kt], vt, oacc[nt]);
-      oacc[nt] = Mma<ST>::k16(plo[kt], vt, oacc[nt]);
-    }
-    wave_lds_sync();  // the next tile overwrites the staging rows
-  }
-
-  // ---- the key halves meet: each wave leaves its max and sum per query and
-  //      the output columns the other wave writes (in its own strip)
   if (kg == 0) {
     ml_lds[wave][0][q16] = mx;
     ml_lds[wave][1][q16] = lsum;
   }
+
+  // ---- P.V in two column halves: D[i][c] over 16 keys a tile, V staged
+  //      row-major (the half's columns) and read back transposed; p = hi + lo.
+  //      Wave kh writes column half kh out; it leaves the other half's
+  //      partial sums for the other wave in its (dead) position strip.
   float* const xo_own = bdl;
-  const float* const xo_other = reinterpret_cast<const float*>(stage_lds + (wave ^ 1) * WAVE_BYTES);
+  f32x4_t keep[NOH];
 #pragma unroll
-  for (int n = 0; n < NOH; ++n)
+  for (int half = 0; half < 2; ++half) {
+    f32x4_t oacc[NOH];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) xo_own[(n * 4 + r) * 64 + lane] = oacc[(1 - kh) * NOH + n][r];
+    for (int n = 0; n < NOH; ++n) oacc[n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kt = 0; kt < NTW; ++kt) {
+      uint8_t* vrow = vst + q16 * VSTRIDE + kg * 16;
+      const bool mine = has_frames(kt) && ftile == kt;
+#pragma unroll
+      for (int x = 0; x < KSH; ++x) {
+        const int ks = half * KSH + x;
+        *reinterpret_cast<u32x4*>(vrow + x * 64) = mine ? vf[ks] : vr[kt][ks];
+      }
+      wave_lds_sync();
+#pragma unroll
+      for (int n = 0; n < NOH; ++n) {
+        const uint8_t* src = vst + (4 * kg + (q16 >> 2)) * VSTRIDE + (n * 16 + 4 * (q16 & 3)) * 2;
+        const i16x4_t vt = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t*)src);
+        oacc[n] = Mma<ST>::k16(phi[kt], vt, oacc[n]);
+        oacc[n] = Mma<ST>::k16(plo[kt], vt, oacc[n]);
+      }
+      wave_lds_sync();  // the next tile overwrites the staging rows
+    }
+    if (half == kh) {  // wave-uniform
+#pragma unroll
+      for (int n = 0; n < NOH; ++n) keep[n] = oacc[n];
+    } else {
+#pragma unroll
+      for (int n = 0; n < NOH; ++n)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) xo_own[(n * 4 + r) * 64 + lane] = oacc[n][r];
+    }
+  }
+  // the frames' V rows to their pages
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) pk_buffer_store_x4(vf[ks], r_vp, arow, kg * 16, blk_soff + ks * blk_step, kPolicy);
   __syncthreads();
-  // lane (kg, q16) holds output rows (queries) 4 kg + r, column 16 nt + q16
-  H* const ost = reinterpret_cast<H*>(vst);  // [16 queries][DK / 2 columns]
+
+  // ---- the key halves meet: lane (kg, q16) holds output rows (queries)
+  //      4 kg + r, column 16 n + q16 of the wave's half
+  const float* const xo_other = reinterpret_cast<const float*>(stage_lds + (wave ^ 1) * WAVE_BYTES);
+  H* const ost = reinterpret_cast<H*>(vst);  // [16 queries][HC columns]
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int qi = 4 * kg + r;
@@ -1491,20 +1541,20 @@ __global__ void __launch_bounds__(256) relpos_attn_chunk_kernel(const AttnK<ST> 
     const float inv = den > 0.f ? __builtin_amdgcn_rcpf(den) : 0.f;
 #pragma unroll
     for (int n = 0; n < NOH; ++n) {
-      const float o = (c0 * oacc[kh * NOH + n][r] + c1 * xo_other[(n * 4 + r) * 64 + lane]) * inv;
-      ost[qi * (DK / 2) + n * 16 + q16] = (H)o;
+      const float o = (c0 * keep[n][r] + c1 * xo_other[(n * 4 + r) * 64 + lane]) * inv;
+      ost[qi * HC + n * 16 + q16] = (H)o;
     }
   }
   wave_lds_sync();
   if (active) {
-    constexpr int CPR = DK / 16;  // 16-byte chunks per output half-row
+    constexpr int CPR = HC * 2 / 16;  // 16-byte chunks per output half-row
 #pragma unroll
     for (int c = 0; c < DK / 64; ++c) {
       const int idx = c * 64 + lane;
       const int qi = idx / CPR, ch = idx % CPR;
       if (qi < p.T) {
-        const u32x4 o = *reinterpret_cast<const u32x4*>(vst + qi * DK + ch * 16);
-        u32x4* const dst = reinterpret_cast<u32x4*>(p.out + b * p.o_sb + (int64_t)qi * p.o_st + hcol + kh * (DK / 2) + ch * 8);
+        const u32x4 o = *reinterpret_cast<const u32x4*>(vst + qi * (HC * 2) + ch * 16);
+        u32x4* const dst = reinterpret_cast<u32x4*>(p.out + b * p.o_sb + (int64_t)qi * p.o_st + hcol + kh * HC + ch * 8);
         if constexpr (STREAM)
           __builtin_nontemporal_store(o, dst);
         else
@@ -1512,11 +1562,6 @@ __global__ void __launch_bounds__(256) relpos_attn_chunk_kernel(const AttnK<ST> 
       }
     }
   }
-  // ---- fused append (row kNoRow where the lane holds no frame)
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) pk_buffer_store_x4(kf[ks], r_kp, arow, kg * 16, blk_soff + ks * blk_step, kPolicy);
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) pk_buffer_store_x4(vf[ks], r_vp, arow, kg * 16, blk_soff + ks * blk_step, kPolicy);
 }
 
 // ---------------------------------------------------------------------------
