@@ -82,7 +82,10 @@ def churn_step(runner, churn, events=None, graph=False) -> int:
     return int(active.shape[0])
 
 
-TRAFFIC_SUMMARY = os.path.join(HERE, "profiles", "relpos_attn_large_bf16_230streams_hbm_counters.md")
+TRAFFIC_SUMMARY = {
+    "large": os.path.join(HERE, "profiles", "relpos_attn_large_bf16_230streams_hbm_counters.md"),
+    "large-t14": os.path.join(HERE, "profiles", "relpos_attn_chunk_large_bf16_t14_230streams.md"),
+}
 
 
 def measured_traffic(config_name: str, avg_streams: float):
@@ -91,9 +94,10 @@ def measured_traffic(config_name: str, avg_streams: float):
     that summary covers the same configuration and batch; None otherwise."""
     import re
 
-    if config_name != "large" or not os.path.exists(TRAFFIC_SUMMARY):
+    path = TRAFFIC_SUMMARY.get(config_name)
+    if path is None or not os.path.exists(path):
         return None
-    txt = open(TRAFFIC_SUMMARY).read()
+    txt = open(path).read()
     m = re.search(r"^traffic_bytes_per_launch: (\d+)$", txt, re.M)
     n = re.search(r"^traffic_streams: (\d+)$", txt, re.M)
     if not m or not n or abs(avg_streams - int(n.group(1))) > 0.5:
