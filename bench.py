@@ -13,6 +13,13 @@ continuous arrivals/departures (lifetimes U(2, 30) s at 80 ms/frame), page size
 16 frames, left context 70, 2 frames per step.  Inputs are seeded synthetic
 tensors resident in HBM before timing.
 
+The default run then adds, each under its own key with its roofline and CPU
+baseline: the large model's own 14-frame chunk (``large_t14``), the small shape
+at 64 streams (``small_64streams``), the fragmentation stress at 1024 streams
+(``frag_1024streams``) and the end-to-end pcm16 -> tokens step at 128 streams
+(``e2e_pcm16_128streams``); and, under ``concurrent_streams.measured_max``, a
+timed run at the largest batch the GPU holds at the headline shape.
+
 Prints one JSON line on stdout; progress goes to stderr.
 """
 
@@ -146,7 +153,7 @@ def cpu_baseline(shape, streams: int, budget_s: float, seed: int) -> dict:
     from oracle.dense_path import DenseStatePool
     from parakeet_amd import synth
 
-    cores = min(16, len(os.sched_getaffinity(0)))
+    cores = len(os.sched_getaffinity(0))  # every core of the affinity mask
     torch.set_num_threads(cores)
     T, D = shape.chunk, shape.d_model
     g = torch.Generator().manual_seed(seed)
@@ -173,9 +180,9 @@ def cpu_baseline(shape, streams: int, budget_s: float, seed: int) -> dict:
         "cores": cores,
         "kind": "port",
         "sample": (
-            f"{n} steps x {streams} streams x {shape.layers} layers, d_model {D}, fp32 dense shift-buffer path "
-            "(pack/unpack index_select/index_copy_, per-stream mask loop, clone+copy shift, torch SDPA) "
-            f"in {el:.1f} s"
+            f"{n} steps x {streams} streams x {shape.layers} layers, d_model {D}, {T} frames a step, fp32 dense "
+            "shift-buffer path (pack/unpack index_select/index_copy_, per-stream mask loop, clone+copy shift, "
+            f"torch SDPA) in {el:.1f} s on {cores} threads, every core of the affinity mask"
         ),
         "ms_per_step": round(1000.0 * el / n, 2),
     }
@@ -279,7 +286,32 @@ def decode_cpu_baseline(pred, joint, vocab: int, budget_s: float, streams: int) 
     }
 
 
-def encoder_bench(args, device) -> int:
+def encoder_cpu_baseline(enc, budget_s: float, layers: int, heads: int, left: int, right: int, kernel: int,
+                         d_model: int) -> dict:
+    """The oracle's streaming encoder step (oracle/encoder.py: float64 numpy,
+    encoder.py:229-267 with dense caches) on one stream and one host core, on
+    random subsampled frames, for about ``budget_s`` seconds."""
+    import numpy as np
+
+    from oracle import encoder as oe
+    from oracle import relpos
+    from threadpoolctl import threadpool_limits
+
+    sd = {k: v.detach().double().cpu().numpy() for k, v in enc.state_dict().items()}
+    D, T = d_model, right + 1
+    pe = relpos.sinusoid_table(5000, D).astype(np.float64)
+    st = oe.EncoderState(1, layers, left, right, D, kernel)
+    g = np.random.default_rng(14)
+    n, t0 = 0, time.perf_counter()
+    with threadpool_limits(limits=1):
+        while time.perf_counter() - t0 < budget_s or n < 2:
+            oe.encoder_step(g.standard_normal((1, T, D)), sd, st, np.full(1, T), layers, heads, pe)
+            n += 1
+    el = time.perf_counter() - t0
+    return {"seconds_per_step": el / n, "steps": n}
+
+
+def encoder_bench(args, device) -> dict:
     """``--config e2e``: one streaming step of a random-init small FastConformer
     from pcm16 to tokens -- 128 streams, each fed a 160 ms chunk (2560 samples)
     per step: the batched front end (pk_fe_step: sample ring, dither,
@@ -489,16 +521,17 @@ def encoder_bench(args, device) -> int:
     max_pages = cache.max_pages
     att_bytes = B * (s * D * (2 * (left + T) + 4 * T) + 4 * (1 + max_pages) + T * (left + T)) + s * D * (left + 2 * T - 1) + 2 * s * D
     att_gbs = att_bytes / (att_us * 1e-6) / 1e9
-    cpu = dec_cpu = att_cpu = None
+    cpu = dec_cpu = att_cpu = step_cpu = None
     if not args.no_cpu_baseline:
         from parakeet_amd import synth
 
+        part_s = min(args.cpu_baseline_seconds, 10.0)
         att_cpu = cpu_baseline(synth.SMALL_FP16, B, args.cpu_baseline_seconds, seed=5)
         att_cpu["sample"] = ("the reference's dense encoder-attention path only (not the whole pcm16 -> tokens step): "
                              + att_cpu["sample"])
-        dec_cpu = decode_cpu_baseline(pred, joint, vocab, min(args.cpu_baseline_seconds, 10.0), B)
+        dec_cpu = decode_cpu_baseline(pred, joint, vocab, part_s, B)
         sd = {k: v.detach().double().cpu().numpy() for k, v in sub.state_dict().items()}
-        cb = front_end_cpu_baseline(sd, min(args.cpu_baseline_seconds, 10.0), seed=8)
+        cb = front_end_cpu_baseline(sd, part_s, seed=8)
         cpu = {
             "value": round(cb["chunks_per_s"] / B, 4),
             "unit": f"front-end steps/s ({B} streams x 160 ms)",
@@ -506,6 +539,20 @@ def encoder_bench(args, device) -> int:
             "kind": "port",
             "sample": f"{cb['chunks']} chunks of 160 ms of one stream through the oracle's FeatureExtractor.push + "
             f"ConvSubsampling (float64 numpy) in {cb['seconds']:.1f} s, scaled to {B} streams per step",
+        }
+        ec = encoder_cpu_baseline(enc, part_s, Ly, H, left, right, K, D)
+        # the whole pcm16 -> tokens step of one stream on one core: front end +
+        # encoder + greedy decode, each timed above, scaled to the batch
+        per_stream_s = 1.0 / cb["chunks_per_s"] + ec["seconds_per_step"] + 1.0 / (dec_cpu["value"] * B)
+        step_cpu = {
+            "value": round(1.0 / (per_stream_s * B), 5),
+            "unit": "steps/s",
+            "cores": 1,
+            "kind": "port",
+            "sample": f"one stream's pcm16 -> tokens step on one core, the sum of the oracle's front end "
+            f"({1000.0 / cb['chunks_per_s']:.2f} ms a 160 ms chunk), encoder step ({Ly} layers, float64 numpy, "
+            f"{1000.0 * ec['seconds_per_step']:.2f} ms over {ec['steps']} steps) and greedy decode "
+            f"({1000.0 / (dec_cpu['value'] * B):.2f} ms a 2-frame step), scaled to {B} streams per step",
         }
     result = {
         "metric": "streaming steps/sec from pcm16 to tokens (small FastConformer: front end + 17 layers + greedy RNNT) at 1 GPU",
@@ -567,8 +614,9 @@ def encoder_bench(args, device) -> int:
             "avg_kernel_us": round(att_us, 3),
             "bytes_per_launch": att_bytes,
             "launches_timed": len(att_ev),
+            "cpu_baseline_attention_only": att_cpu,
         },
-        "cpu_baseline": att_cpu,
+        "cpu_baseline": step_cpu,
         "realtime": {
             "audio_ms_per_step": 1000.0 * chunk / 16000.0,
             "streams": B,
@@ -595,147 +643,137 @@ def encoder_bench(args, device) -> int:
         },
         "wall_s": round(wall, 3),
     }
-    print(json.dumps(result), flush=True)
-    return 0
+    return result
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", choices=sorted(CONFIGS) + ["e2e"], default="large")
-    ap.add_argument("--preroll", type=int, default=60, help="untimed steps before warmup to reach steady-state windows")
-    ap.add_argument("--rows-per-lane", type=int, default=0)
-    ap.add_argument("--no-kernel-events", action="store_true")
-    ap.add_argument("--kernel-event-steps", type=int, default=50, help="eager steps timed per kernel for the roofline")
-    ap.add_argument("--graph", action="store_true", help="replay every step's launches from one HIP graph (grid sized for all slots)")
-    ap.add_argument("--streams", type=int, default=128, help="e2e: streams in the batch (all live)")
-    ap.add_argument("--eager-encoder", action="store_true", help="e2e: issue the encoder's ops from Python instead of replaying a recorded step")
-    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB", help="only run a device copy of MIB MiB (counter calibration)")
-    ap.add_argument("--cpu-baseline-seconds", type=float, default=15.0)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-copy-ceiling", action="store_true", help="skip the same-bytes device copy timing")
-    args = ap.parse_args()
+def read_probe(nbytes: int, reps: int) -> dict:
+    """One launch of ``pk_hbm_read_probe`` reading ``nbytes`` (a launch's bytes),
+    from buffers cycled past the 256 MB last-level cache (>= 1 GiB of them), each
+    launch between HIP events on its stream: the read ceiling of a launch of that
+    size on this GPU."""
+    import torch
 
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print(
-            "bench.py measures one GPU: the paged encoder-attention path has no cross-GPU work "
-            "(streams are sharded per GPU with no per-step exchange); run with --gpus 1",
-            file=sys.stderr,
-        )
-        return 2
+    from parakeet_amd import ops
 
+    n = max(16, (int(nbytes) + 15) // 16 * 16)
+    nbuf = max(2, -(-(1 << 30) // n))
+    dev = torch.device("cuda:0")
+    bufs = [torch.ones(n // 2, dtype=torch.bfloat16, device=dev) for _ in range(nbuf)]
+    out = torch.empty(64 * 8 * torch.cuda.get_device_properties(dev).multi_processor_count, dtype=torch.uint8, device=dev)
+    for b in bufs:  # warm
+        ops.hbm_read_probe(b, out)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for a, b in ev:
+        a.record()
+        b.record()
+    torch.cuda.synchronize()
+    for r in range(reps):
+        ops.hbm_read_probe(bufs[r % nbuf], out, start_event=ev[r][0], stop_event=ev[r][1])
+    torch.cuda.synchronize()
+    us = 1000.0 * sum(a.elapsed_time(b) for a, b in ev) / reps
+    del bufs
+    gbs = n / (us * 1e-6) / 1e9
+    return {"bytes": n, "launches": reps, "buffers": nbuf, "avg_us": round(us, 3), "gbs": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def _release(device) -> None:
+    import torch
+
+    gc.collect()
+    torch.cuda.synchronize(device)
+    torch.cuda.empty_cache()
+
+
+def paged_bench(config_name: str, device, args, steps: int, warmup: int, event_steps: int, cpu_seconds: float,
+                probes: bool = True) -> dict:
+    """The encoder-attention step of one workload (CONFIGS): ``steps`` timed steps
+    of host page work + upload + every layer's launch (replayed from a HIP graph
+    with --graph), then ``event_steps`` steps with every kernel between HIP events
+    for the roofline, the same-bytes read and copy probes and the CPU baseline."""
     import numpy as np
     import torch
 
     from parakeet_amd import ops
 
-    if not torch.cuda.is_available():
-        print("bench.py needs a HIP device", file=sys.stderr)
-        return 1
-    device = torch.device("cuda:0")
-    if args.copy_probe:
-        print(json.dumps(copy_probe(args.copy_probe, max(1, args.steps))), flush=True)
-        return 0
-    if args.config == "e2e":
-        return encoder_bench(args, device)
-    cfg = CONFIGS[args.config]
-    log(f"config {args.config}: building workload")
+    cfg = CONFIGS[config_name]
+    log(f"config {config_name}: building workload")
     shape, runner, churn = build_runner(cfg, device, args.rows_per_lane)
     Ly = shape.layers
     # the objects built so far live for the whole run: keep them out of the
     # collector's scans, so a full collection in the step loop stays short
     gc.collect()
     gc.freeze()
-
     with torch.inference_mode():
         for _ in range(args.preroll):
             churn_step(runner, churn)
-        torch.cuda.synchronize()
-        log(f"preroll {args.preroll} steps done")
-        for _ in range(args.warmup):
+        for _ in range(warmup):
             churn_step(runner, churn)
         torch.cuda.synchronize()
-        log(f"warmup {args.warmup} steps done")
-
+        log(f"{config_name}: preroll {args.preroll} + warmup {warmup} steps done")
         use_graph = args.graph
         if use_graph:
             runner.capture()
-            for _ in range(max(1, args.warmup // 2)):
+            for _ in range(max(1, warmup // 2)):
                 churn_step(runner, churn, graph=True)
             torch.cuda.synchronize()
-            log("graph captured and replayed")
-
-        # timed pass 1: the step loop as it serves (host page work + one upload +
-        # every layer's launch; replayed from one HIP graph with --graph)
-        K = args.steps
+        # timed pass 1: the step loop as it serves
         batches = []
-        step_ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
+        step_ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         start.record()
-        for k in range(K):
+        for k in range(steps):
             step_ev[k][0].record()
             batches.append(churn_step(runner, churn, graph=use_graph))
             step_ev[k][1].record()
         stop.record()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-        log(f"timed {K} steps done")
-
-        # timed pass 2: every kernel between its own HIP events (eager launches),
-        # for the roofline
-        use_ev = not args.no_kernel_events
-        K2 = min(K, args.kernel_event_steps)
+        log(f"{config_name}: timed {steps} steps")
+        # timed pass 2: every kernel between its own HIP events (eager launches)
         ev_pairs, ev_batches = [], []
-        if use_ev:
-            for _ in range(K2):
-                pairs = []
-                for _ in range(Ly):
-                    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                    a.record()
-                    b.record()
-                    pairs.append((a, b))
-                ev_pairs.append(pairs)
-            torch.cuda.synchronize()
-            handles = [[(ops._event_handle(a), ops._event_handle(b)) for a, b in pairs] for pairs in ev_pairs]
-            for k in range(K2):
-                ev_batches.append(churn_step(runner, churn, handles[k]))
-            torch.cuda.synchronize()
-            log(f"timed {K2} steps with per-kernel events done")
+        for _ in range(event_steps):
+            pairs = []
+            for _ in range(Ly):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                b.record()
+                pairs.append((a, b))
+            ev_pairs.append(pairs)
+        torch.cuda.synchronize()
+        handles = [[(ops._event_handle(a), ops._event_handle(b)) for a, b in pairs] for pairs in ev_pairs]
+        for k in range(event_steps):
+            ev_batches.append(churn_step(runner, churn, handles[k]))
+        torch.cuda.synchronize()
+        log(f"{config_name}: {event_steps} steps with per-kernel events")
+    gc.unfreeze()
 
-    ms_total = start.elapsed_time(stop)
-    ms_per_step = ms_total / K
-    gpu_ms_per_step = sum(a.elapsed_time(b) for a, b in step_ev) / K
+    ms_per_step = start.elapsed_time(stop) / steps
+    gpu_ms_per_step = sum(a.elapsed_time(b) for a, b in step_ev) / steps
     per_stream = runner.bytes_per_stream()
     shared = runner.bytes_shared_per_launch()
     total_bytes = sum(B * Ly * per_stream + Ly * shared for B in ev_batches)
-    kern_ms = None
-    if use_ev:
-        kern_ms = sum(a.elapsed_time(b) for pairs in ev_pairs for a, b in pairs)
+    kern_ms = sum(a.elapsed_time(b) for pairs in ev_pairs for a, b in pairs)
+    n_launch = max(1, len(ev_batches) * Ly)
+    avg_us = 1000.0 * kern_ms / n_launch
     avg_B = float(np.mean(batches))
-    steps_per_s = 1000.0 / ms_per_step
-
-    free_b, total_b = torch.cuda.mem_get_info(device)
+    ev_B = float(np.mean(ev_batches)) if ev_batches else avg_B
     per_stream_pool = runner.pool.max_pages * Ly * shape.page_size * shape.d_model * shape.elem_bytes * 2
-    pool_capacity = int((total_b * 0.9) // per_stream_pool)
-    realtime_capacity = int(avg_B * (shape.chunk * FRAME_SECONDS * 1000.0) / ms_per_step)
-
-    result = {
-        "metric": "encoder attn steps/sec & max concurrent streams at 1 GPU; paged-attn HBM GB/s",
-        "value": round(steps_per_s, 2),
+    free_b, total_b = torch.cuda.mem_get_info(device)
+    audio_ms = shape.chunk * FRAME_SECONDS * 1000.0
+    kernel = ("relpos_attn_chunk_kernel (whole chunk; fused append + paged rel-pos attention)"
+              if (3 <= shape.chunk <= 14 and args.rows_per_lane == 0) or args.rows_per_lane == -2
+              else "relpos_attn_mfma_kernel (fused append + paged rel-pos attention)")
+    out = {
+        "value": round(1000.0 / ms_per_step, 2),
         "unit": "steps/s",
-        "n_gpus": 1,
-        "steps": K,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": round(ms_per_step, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
+        "gpu_ms_per_step": round(gpu_ms_per_step, 4),
         "dtype": {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[shape.dtype],
-        "data": "synthetic (seeded N(0,1) Q/K/V, N(0,0.02) biases, linear_pos of the sinusoid table)",
         "config": {
             "workload": f"{shape.name}: paged append+attention+eviction, {cfg['slots']} stream slots at "
             f"{int(cfg['occupancy'] * 100)}% occupancy with churn",
@@ -751,49 +789,216 @@ def main() -> int:
             "parallelism": "single GPU",
             "launch": "one HIP graph replay per step (all layers)" if use_graph else "one host launch per layer",
         },
-        "gpu_ms_per_step": round(gpu_ms_per_step, 4),
-        "concurrent_streams": {
-            "measured_batch": round(avg_B, 1),
-            "pool_capacity_hbm": pool_capacity,
-            "realtime_attention_only_extrapolated": realtime_capacity,
+        "realtime": {
+            "audio_ms_per_step": audio_ms,
+            "x_realtime": round(audio_ms / ms_per_step, 1),
+            "pool_capacity_hbm_streams": int((total_b * 0.9) // per_stream_pool),
+            "pool_bytes_per_stream": per_stream_pool,
         },
         "wall_s": round(wall, 3),
     }
-    if use_ev and kern_ms:
-        achieved = total_bytes / (kern_ms * 1e-3) / 1e9
-        result["roofline"] = {
-            "bound": "hbm",
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(args.config, float(np.mean(ev_batches))),
-            "kernel": "relpos_attn_mfma_kernel (fused append + paged rel-pos attention)",
-            "avg_kernel_us": round(1000.0 * kern_ms / (len(ev_batches) * Ly), 3),
-            "kernel_event_steps": len(ev_batches),
-            "bytes_per_stream_layer": per_stream,
-        }
-        result["paged_attn_hbm_gbs"] = round(achieved, 1)
-        if not args.no_copy_ceiling:
-            # the same bytes moved by one plain device copy launch (half read,
-            # half written): what one launch of this size reaches on this GPU
-            launch_bytes = total_bytes / max(1, len(ev_batches) * Ly)
-            mib = max(1, int(round(launch_bytes / 2 / (1 << 20))))
-            cp = copy_probe(mib, 100)
-            result["roofline"]["copy_same_bytes"] = {
-                "bytes": 2 * cp["copy_probe_bytes_read"],
-                "avg_us": cp["avg_us"],
-                "gbs": cp["gbs"],
-                "frac": cp["frac_of_peak"],
-            }
-            log(f"same-bytes copy: {cp['avg_us']} us, {cp['gbs']} GB/s")
-    if not args.no_cpu_baseline:
-        log("cpu baseline ...")
+    achieved = total_bytes / (kern_ms * 1e-3) / 1e9
+    traffic = measured_traffic(config_name, ev_B) if args.rows_per_lane == 0 else None
+    roof = {
+        "bound": "hbm",
+        "achieved": round(achieved, 1),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "traffic": traffic,
+        "kernel": kernel,
+        "avg_kernel_us": round(avg_us, 3),
+        "kernel_event_steps": len(ev_batches),
+        "bytes_per_stream_layer": per_stream,
+        "bytes_shared_per_launch": shared,
+        "bytes_per_launch": int(round(total_bytes / n_launch)),
+    }
+    if traffic:
+        # the same launch time over the bytes the HBM counters read
+        roof["frac_counter_bytes"] = round(traffic / (avg_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+    if probes and not args.no_copy_ceiling:
+        launch_bytes = total_bytes / n_launch
+        rp = read_probe(int(launch_bytes), 100)
+        roof["read_same_bytes"] = rp
+        roof["frac_of_read_ceiling"] = round(achieved / rp["gbs"], 4)
+        log(f"{config_name}: same-bytes read {rp['avg_us']} us, {rp['gbs']} GB/s")
+        mib = max(1, int(round(launch_bytes / 2 / (1 << 20))))
+        cp = copy_probe(mib, 100)
+        roof["copy_same_bytes"] = {"bytes": 2 * cp["copy_probe_bytes_read"], "avg_us": cp["avg_us"], "gbs": cp["gbs"],
+                                   "frac": cp["frac_of_peak"]}
+    out["roofline"] = roof
+    out["paged_attn_hbm_gbs"] = round(achieved, 1)
+    del runner, churn
+    _release(device)
+    if cpu_seconds > 0:
+        log(f"{config_name}: cpu baseline ...")
         try:
-            result["cpu_baseline"] = cpu_baseline(shape, max(1, int(round(avg_B))), args.cpu_baseline_seconds, cfg["seed"])
+            out["cpu_baseline"] = cpu_baseline(shape, max(1, int(round(avg_B))), cpu_seconds, cfg["seed"])
         except Exception as e:  # report, never hide
-            result["cpu_baseline"] = {"error": repr(e)}
-        log("cpu baseline done")
+            out["cpu_baseline"] = {"error": repr(e)}
+    return out
+
+
+def capacity_bench(device, config_name: str, steps: int) -> dict:
+    """The largest batch the GPU holds at a workload's shape, all streams live:
+    the page pool sized to the free HBM (one qkv input shared by the layers),
+    windows filled, then ``steps`` timed steps (host page work, upload, every
+    layer's launch).  The step time against the chunk's audio says whether that
+    batch keeps up with real time."""
+    import numpy as np
+    import torch
+
+    from parakeet_amd import synth
+    from parakeet_amd.pool import pages_per_slot
+    from parakeet_amd.step import AttentionStep
+
+    cfg = CONFIGS[config_name]
+    shape = getattr(synth, cfg["shape"])
+    Ly, T, D, s = shape.layers, shape.chunk, shape.d_model, shape.elem_bytes
+    M = pages_per_slot(shape.left, T, shape.page_size)
+    per_stream_pool = Ly * M * shape.page_size * D * s * 2
+    per_stream_io = Ly * T * D * s + 3 * T * D * s  # outputs of every layer + the shared qkv input
+    _release(device)
+    free_b, total_b = torch.cuda.mem_get_info(device)
+    reserve = 6 << 30
+    S = int((free_b - reserve) // (per_stream_pool + per_stream_io)) // 256 * 256
+    log(f"capacity {config_name}: {S} streams ({S * per_stream_pool / 2**30:.1f} GiB of pages, {free_b / 2**30:.1f} GiB free)")
+    qkv = synth.qkv_frames(S, shape, device, seed=21)
+    pos, bu, bv = synth.relpos_inputs(shape, device, seed=22)
+    runner = AttentionStep(shape, S, device, [qkv] * Ly, pos, [bu] * Ly, [bv] * Ly)
+    active = np.arange(S, dtype=np.int32)
+    fill = -(-(shape.left + T) // T) + 1  # steps until every window is full
+    with torch.inference_mode():
+        for _ in range(fill):
+            runner.step(active)
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        start.record()
+        for _ in range(steps):
+            runner.step(active)
+        stop.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    ms = start.elapsed_time(stop) / steps
+    nbytes = Ly * (S * runner.bytes_per_stream() + runner.bytes_shared_per_launch())
+    audio_ms = T * FRAME_SECONDS * 1000.0
+    peak_gib = torch.cuda.max_memory_allocated(device) / 2**30
+    del runner, qkv
+    _release(device)
+    return {
+        "workload": f"{shape.name}: {S} streams, all live, windows full",
+        "streams": S,
+        "steps": steps,
+        "ms_per_step": round(ms, 3),
+        "steps_per_s": round(1000.0 / ms, 2),
+        "audio_ms_per_step": audio_ms,
+        "x_realtime": round(audio_ms / ms, 2),
+        "keeps_up": bool(ms <= audio_ms),
+        "attention_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+        "pool_gib": round(S * per_stream_pool / 2**30, 1),
+        "device_gib_total": round(total_b / 2**30, 1),
+        "device_gib_peak": round(peak_gib, 1),
+        "bound_by": "HBM capacity of the page pool" if ms <= audio_ms else "attention step time",
+        "wall_s": round(wall, 2),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", choices=sorted(CONFIGS) + ["e2e"], default="large")
+    ap.add_argument("--preroll", type=int, default=60, help="untimed steps before warmup to reach steady-state windows")
+    ap.add_argument("--rows-per-lane", type=int, default=0, help="kernel choice (0 automatic; see pk_attn_args)")
+    ap.add_argument("--kernel-event-steps", type=int, default=50, help="eager steps timed per kernel for the roofline")
+    ap.add_argument("--graph", action="store_true", help="replay every step's launches from one HIP graph (grid sized for all slots)")
+    ap.add_argument("--streams", type=int, default=128, help="e2e: streams in the batch (all live)")
+    ap.add_argument("--eager-encoder", action="store_true", help="e2e: issue the encoder's ops from Python instead of replaying a recorded step")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB", help="only run a device copy of MIB MiB (counter calibration)")
+    ap.add_argument("--cpu-baseline-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-copy-ceiling", action="store_true", help="skip the same-bytes read and copy probes")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="default config only: skip the other workloads and the capacity run")
+    ap.add_argument("--no-kernel-events", action="store_true", help="no per-kernel event pass (for counter runs)")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(
+            "bench.py measures one GPU: the paged encoder-attention path has no cross-GPU work "
+            "(streams are sharded per GPU with no per-step exchange); run with --gpus 1",
+            file=sys.stderr,
+        )
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        return 1
+    device = torch.device("cuda:0")
+    if args.copy_probe:
+        print(json.dumps(copy_probe(args.copy_probe, max(1, args.steps))), flush=True)
+        return 0
+    if args.config == "e2e":
+        print(json.dumps(encoder_bench(args, device)), flush=True)
+        return 0
+    cpu_s = 0.0 if args.no_cpu_baseline else args.cpu_baseline_seconds
+    ev_steps = 0 if args.no_kernel_events else min(args.steps, args.kernel_event_steps)
+    head = paged_bench(args.config, device, args, args.steps, args.warmup, ev_steps, cpu_s, probes=ev_steps > 0)
+    result = {
+        "metric": "encoder attn steps/sec & max concurrent streams at 1 GPU; paged-attn HBM GB/s",
+        "value": head.pop("value"),
+        "unit": head.pop("unit"),
+        "n_gpus": 1,
+        "steps": head.pop("steps"),
+        "warmup": head.pop("warmup"),
+        "ms_per_step": head.pop("ms_per_step"),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": head.pop("dtype"),
+        "data": "synthetic (seeded N(0,1) Q/K/V, N(0,0.02) biases, linear_pos of the sinusoid table)",
+        "config": head.pop("config"),
+    }
+    result.update(head)
+    default_run = args.config == "large" and not args.no_extras and ev_steps > 0
+    if default_run:
+        # the other workloads, each with its roofline and CPU baseline, and the
+        # largest batch the GPU holds at the headline shape
+        extra_s = min(cpu_s, 8.0)
+        extras = [
+            ("large_t14", lambda: paged_bench("large-t14", device, args, 100, 10, 30, extra_s)),
+            ("small_64streams", lambda: paged_bench("small", device, args, 100, 10, 30, extra_s)),
+            ("frag_1024streams", lambda: paged_bench("frag", device, args, 100, 10, 30, extra_s)),
+        ]
+        for key, fn in extras:
+            try:
+                result[key] = fn()
+            except Exception as e:  # report, never hide
+                result[key] = {"error": repr(e)}
+        try:
+            cap = capacity_bench(device, "large", 10)
+        except Exception as e:
+            cap = {"error": repr(e)}
+        result["concurrent_streams"] = {
+            "measured_max": cap,
+            "headline_batch": result["config"]["avg_active_streams"],
+            "reference_claim": "around 80 (small) / 60 (large) concurrent streams on an A100 (README.md:26-27)",
+        }
+        try:
+            e2e_args = argparse.Namespace(**vars(args))
+            e2e_args.steps, e2e_args.warmup = 20, 5
+            e2e_args.cpu_baseline_seconds = extra_s
+            e2e_args.streams = 128
+            e2e = encoder_bench(e2e_args, device)
+            for k in ("metric", "n_gpus", "higher_is_better", "scaling", "vs_baseline"):
+                e2e.pop(k, None)
+            result["e2e_pcm16_128streams"] = e2e
+        except Exception as e:
+            result["e2e_pcm16_128streams"] = {"error": repr(e)}
     print(json.dumps(result), flush=True)
     return 0
 

@@ -576,6 +576,19 @@ int pk_pool_free_pages(const pk_pool* pool);
 int pk_pool_slot_info(const pk_pool* pool, int32_t slot, int64_t* appended, int32_t* ring_out);
 int pk_pool_free_list(const pk_pool* pool, int32_t* out, int32_t capacity);
 
+/* ---------------------------------------------------------------------------
+ * pk_hbm_read_probe -- measurement only; it has no counterpart in the reference.
+ * Reads `bytes` (a positive multiple of 16) from the device buffer `src` once,
+ * 16 bytes a lane with the streaming cache policy, and writes to out[4 w + x]
+ * (16 bytes each, device memory of workgroups * 64 bytes) the XOR of what wave x of
+ * workgroup w read, so no read can be dropped.  workgroups: the grid (4 waves of 64
+ * lanes each); 0 = 8 per CU.
+ * start_event/stop_event: optional hipEvent_t pair timing the launch alone.
+ * For a benchmark: the read ceiling of one launch that moves a kernel's bytes.
+ */
+int pk_hbm_read_probe(const void* src, int64_t bytes, void* out, int32_t workgroups, void* start_event,
+                      void* stop_event, void* stream);
+
 /* Message for the last failed call on this thread ("" if none). */
 const char* pk_last_error(void);
 int pk_abi_version(void);

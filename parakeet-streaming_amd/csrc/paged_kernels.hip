@@ -1565,6 +1565,41 @@ __global__ void __launch_bounds__(256, 4) relpos_attn_chunk_kernel(const AttnK<S
 }
 
 // ---------------------------------------------------------------------------
+// read probe: one pass over a buffer, the read ceiling of a launch of its size
+
+__global__ void __launch_bounds__(256) read_probe_kernel(const u32x4* src, int64_t n16, u32x4* out) {
+  constexpr int U = 8;  // loads in flight per lane
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  // workgroup w reads blocks of 32 KB: w, w + grid, ...; within a block, load u
+  // of the workgroup reads 4 KB at u * 4 KB (lane = 16 bytes).  Of the forms
+  // measured for one launch of 72 MB to 1 GB (grid-stride or blocked, 4 to 16
+  // loads a lane, cached or streaming, 512 to 16,384 workgroups) this one, at 8
+  // workgroups a CU, read fastest at every size.
+  for (int64_t blk = blockIdx.x; blk * (256 * U) < n16; blk += gridDim.x) {
+    const int64_t base = blk * (256 * U) + threadIdx.x;
+    if (base + (U - 1) * 256 < n16) {
+      u32x4 v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(src + base + u * 256);
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc ^= v[u];
+    } else {
+      for (int u = 0; u < U; ++u)
+        if (base + u * 256 < n16) acc ^= __builtin_nontemporal_load(src + base + u * 256);
+    }
+  }
+  // XOR over the wave, lane 0 writes the wave's 16 bytes
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    acc.x ^= (uint32_t)__shfl_xor((int)acc.x, off);
+    acc.y ^= (uint32_t)__shfl_xor((int)acc.y, off);
+    acc.z ^= (uint32_t)__shfl_xor((int)acc.z, off);
+    acc.w ^= (uint32_t)__shfl_xor((int)acc.w, off);
+  }
+  if ((threadIdx.x & 63) == 0) out[blockIdx.x * 4 + (threadIdx.x >> 6)] = acc;
+}
+
+// ---------------------------------------------------------------------------
 // append / gather
 
 template <typename ST>
@@ -2171,6 +2206,27 @@ int pk_streaming_mask(const pk_mask_args* a, void* stream) {
   hipLaunchKernelGGL(pk::stream_mask_kernel, dim3(pk::grid_for(total, 256)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), p);
   return pk::check_launch("pk_streaming_mask");
+}
+
+int pk_hbm_read_probe(const void* src, int64_t bytes, void* out, int32_t workgroups, void* start_event,
+                      void* stop_event, void* stream) {
+  pk::clear_error();
+  if (!src || !out || !pk::aligned16(src) || !pk::aligned16(out))
+    return pk::fail(PK_ERR_INVALID, "pk_hbm_read_probe: src and out must be non-NULL and 16-byte aligned");
+  if (bytes <= 0 || bytes % 16 != 0)
+    return pk::fail(PK_ERR_INVALID, "pk_hbm_read_probe: bytes must be a positive multiple of 16");
+  if (workgroups < 0) return pk::fail(PK_ERR_INVALID, "pk_hbm_read_probe: workgroups must be >= 0");
+  const int wg = workgroups > 0 ? workgroups : 8 * pk::cu_count();
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const pk::u32x4* in = static_cast<const pk::u32x4*>(src);
+  pk::u32x4* o = static_cast<pk::u32x4*>(out);
+  if (start_event || stop_event) {
+    hipExtLaunchKernelGGL(pk::read_probe_kernel, dim3(wg), dim3(256), 0u, s, (hipEvent_t)start_event,
+                          (hipEvent_t)stop_event, 0u, in, bytes / 16, o);
+  } else {
+    hipLaunchKernelGGL(pk::read_probe_kernel, dim3(wg), dim3(256), 0, s, in, bytes / 16, o);
+  }
+  return pk::check_launch("pk_hbm_read_probe");
 }
 
 }  // extern "C"

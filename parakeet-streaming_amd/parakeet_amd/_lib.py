@@ -317,6 +317,7 @@ SIGNATURES = {
     "pk_pool_free_pages": (c_int, [c_void_p]),
     "pk_pool_slot_info": (c_int, [c_void_p, c_int32, POINTER(c_int64), POINTER(c_int32)]),
     "pk_pool_free_list": (c_int, [c_void_p, POINTER(c_int32), c_int32]),
+    "pk_hbm_read_probe": (c_int, [c_void_p, c_int64, c_void_p, c_int32, c_void_p, c_void_p, c_void_p]),
     "pk_last_error": (c_char_p, []),
     "pk_abi_version": (c_int, []),
 }

@@ -362,6 +362,24 @@ def streaming_mask(
     return pad, att
 
 
+def hbm_read_probe(src: torch.Tensor, out: torch.Tensor, workgroups: int = 0, start_event=None, stop_event=None) -> None:
+    """One launch that reads all of ``src`` once (streaming policy) and writes a
+    16-byte XOR per wave to ``out`` (uint8, >= 64 * workgroups bytes): the read
+    ceiling of a launch moving that many bytes.  Measurement only."""
+    dev = _require_device(src, out)
+    if not src.is_contiguous() or not out.is_contiguous():
+        raise ValueError("src and out must be contiguous")
+    nbytes = src.numel() * src.element_size()
+    wg = int(workgroups)
+    need = 64 * (wg if wg > 0 else 8 * torch.cuda.get_device_properties(dev).multi_processor_count)
+    if out.numel() * out.element_size() < need:
+        raise ValueError(f"out holds {out.numel() * out.element_size()} bytes, needs {need}")
+    a_ev = _event_handle(start_event) if start_event is not None else None
+    b_ev = _event_handle(stop_event) if stop_event is not None else None
+    check(lib().pk_hbm_read_probe(src.data_ptr(), nbytes, out.data_ptr(), wg, a_ev, b_ev, _stream(dev)),
+          "pk_hbm_read_probe")
+
+
 def conv_step(
     glu_in: torch.Tensor,
     cache: torch.Tensor,

@@ -79,6 +79,18 @@ def test_null_args_rejected_without_gpu():
     assert lib.pk_fe_step(None, None) == _lib.PK_ERR_INVALID
     assert lib.pk_subsample(None, None) == _lib.PK_ERR_INVALID
     assert lib.pk_rnnt_greedy_step(None, None) == _lib.PK_ERR_INVALID
+    assert lib.pk_hbm_read_probe(None, 16, None, 0, None, None, None) == _lib.PK_ERR_INVALID
+
+
+def test_read_probe_args_validated_before_launch():
+    L = _lib.lib()
+    buf = ctypes.create_string_buffer(64)
+    addr = (ctypes.addressof(buf) + 15) & ~15  # 16-byte aligned, never dereferenced on a failed check
+    assert L.pk_hbm_read_probe(addr, 24, addr, 1, None, None, None) == _lib.PK_ERR_INVALID  # not a multiple of 16
+    assert "multiple of 16" in _lib.last_error()
+    assert L.pk_hbm_read_probe(addr, 0, addr, 1, None, None, None) == _lib.PK_ERR_INVALID
+    assert L.pk_hbm_read_probe(addr, 16, addr, -1, None, None, None) == _lib.PK_ERR_INVALID
+    assert L.pk_hbm_read_probe(addr + 8, 16, addr, 1, None, None, None) == _lib.PK_ERR_INVALID  # misaligned
 
 
 def test_mask_args_validated_before_launch():
