@@ -533,7 +533,10 @@ int pk_rnnt_greedy_step(const pk_rnnt_args* args, void* stream);
  * streams).  The kernels initialise every scratch word they read, so nothing
  * needs clearing between calls.  Every call on one GPU shares that GPU's
  * array: calls that overlap on one GPU (different streams, different threads)
- * race and must be serialised by the caller. */
+ * race and must be serialised by the caller.  The array's address is looked up
+ * once per device, outside stream capture: by the first call of either entry
+ * point on the device; a first call made under capture is refused
+ * (PK_ERR_STATE), so make one eager call before recording steps in a graph. */
 #define PK_RNNT_STATIC_SCRATCH_BYTES (8 << 20)
 int pk_rnnt_greedy_step_static(const pk_rnnt_args* args, void* stream);
 

@@ -646,6 +646,50 @@ extern "C" int64_t pk_rnnt_workspace_bytes(int32_t dtype, int32_t batch, int32_t
   return ws_int_bytes(batch, vocab1) + (int64_t)batch * layers * hidden * es;
 }
 
+// ---------------------------------------------------------------------------
+// Allocation-free decode step: the step's workspace is a static device array,
+// one per GPU, held until the process ends.  Its device address is looked up
+// once per device (with that device current) and passed to the kernels like a
+// caller's workspace; the array's name is never used as an address on the host.
+
+static __device__ __align__(256) uint8_t scratch[PK_RNNT_STATIC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// This device's scratch address; the device must be current.  The lookup
+// (which may load the code object) runs once per device and never under stream
+// capture: a first call made while `stream` is capturing is refused, and the
+// workspace entry point looks the address up on its first call on a device, so
+// a decoder that has run one eager step can record static steps in a graph.
+int scratch_address(void** out, hipStream_t stream, bool quiet = false) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return quiet ? PK_ERR_HIP : fail(PK_ERR_HIP, "pk_rnnt_greedy_step_static: no usable current device (%d)", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)
+      return quiet ? PK_ERR_STATE : fail(PK_ERR_STATE,
+                  "pk_rnnt_greedy_step_static: first call on device %d is under stream capture; make one call "
+                  "(or one pk_rnnt_greedy_step call) outside capture first, which looks up the static scratch",
+                  dev);
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return quiet ? PK_ERR_HIP : fail(PK_ERR_HIP, "pk_rnnt_greedy_step_static: hipGetSymbolAddress on device %d: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return PK_OK;
+}
+
+}  // namespace
+
 extern "C" int pk_rnnt_greedy_step(const pk_rnnt_args* a, void* stream) {
   clear_error();
   if (!a) return fail(PK_ERR_INVALID, "pk_rnnt_greedy_step: args is NULL");
@@ -672,6 +716,10 @@ extern "C" int pk_rnnt_greedy_step(const pk_rnnt_args* a, void* stream) {
     return fail(PK_ERR_INVALID, "pk_rnnt_greedy_step: enc_proj strides must keep 16-byte rows");
   DeviceGuard dg(a->device);
   if (!dg.ok) return fail(PK_ERR_HIP, "pk_rnnt_greedy_step: cannot select device %d", a->device);
+  {  // the static entry point's scratch, looked up on this device's first call (outside capture)
+    void* unused = nullptr;
+    (void)scratch_address(&unused, (hipStream_t)stream, true);
+  }
   switch (a->dtype) {
     case PK_DTYPE_F16:
       return run_step<_Float16>(a, (hipStream_t)stream);
@@ -682,39 +730,6 @@ extern "C" int pk_rnnt_greedy_step(const pk_rnnt_args* a, void* stream) {
   }
 }
 
-// ---------------------------------------------------------------------------
-// Allocation-free decode step: the step's workspace is a static device array,
-// one per GPU, held until the process ends.  Its device address is looked up
-// once per device (with that device current) and passed to the kernels like a
-// caller's workspace; the array's name is never used as an address on the host.
-
-static __device__ __align__(256) uint8_t scratch[PK_RNNT_STATIC_SCRATCH_BYTES];
-
-namespace {
-
-constexpr int kMaxDevices = 64;
-std::mutex g_scratch_mu;
-void* g_scratch_ptr[kMaxDevices] = {};
-
-// This device's scratch address; the device must be current.
-int scratch_address(void** out) {
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
-    return fail(PK_ERR_HIP, "pk_rnnt_greedy_step_static: no usable current device (%d)", dev);
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (!g_scratch_ptr[dev]) {
-    void* ptr = nullptr;
-    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-    if (e != hipSuccess || !ptr)
-      return fail(PK_ERR_HIP, "pk_rnnt_greedy_step_static: hipGetSymbolAddress on device %d: %s", dev,
-                  hipGetErrorString(e));
-    g_scratch_ptr[dev] = ptr;
-  }
-  *out = g_scratch_ptr[dev];
-  return PK_OK;
-}
-
-}  // namespace
 
 extern "C" int pk_rnnt_greedy_step_static(const pk_rnnt_args* a, void* stream) {
   clear_error();
@@ -731,7 +746,7 @@ extern "C" int pk_rnnt_greedy_step_static(const pk_rnnt_args* a, void* stream) {
   DeviceGuard dg(a->device);
   if (!dg.ok) return fail(PK_ERR_HIP, "pk_rnnt_greedy_step_static: cannot select device %d", a->device);
   void* ptr = nullptr;
-  const int rc = scratch_address(&ptr);
+  const int rc = scratch_address(&ptr, (hipStream_t)stream);
   if (rc != PK_OK) return rc;
   pk_rnnt_args b = *a;
   b.workspace = ptr;

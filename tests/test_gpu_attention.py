@@ -161,6 +161,44 @@ def test_whole_chunk_kernel(cuda, left, right, dk, dtype, kind):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("dtype,right,dk", [(torch.float16, 1, 64), (torch.bfloat16, 1, 128),
+                                            (torch.float16, 13, 64), (torch.bfloat16, 13, 128)])
+def test_planted_bias_mistakes_exceed_the_kernel_bar(cuda, dtype, right, dk):
+    """The kernel against oracles that carry a bias mistake, pos_bias_v dropped
+    or pos_bias_u and pos_bias_v swapped, with the biases at the specified
+    N(0, 0.02^2): the difference exceeds the kernel's tolerance, so a mistake in
+    a bias term, too small to show through a whole encoder stack, is caught
+    here (the two-query kernel at 2 frames a step, the whole-chunk one at 14)."""
+    H, left, P, B = 8, 70, 16, 3
+    print(f"\n[attn planted bias] dtype={dtype} right={right} dk={dk}", flush=True)
+    sc = PagedScenario(cuda, dtype, B=B, layers=1, d_model=H * dk, left=left, right=right, page_size=P, seed=31)
+    pos, bu, bv = _relpos(sc, H, 31)
+    T = sc.T
+    proc = np.zeros(B, dtype=np.int64)
+    steps = (left + T) // T + 2  # windows full
+    plants = {"clean": [], "bias_v_dropped": [], "biases_swapped": []}
+    for step in range(steps):
+        sc.open_step()
+        _, mask_np = om.create_streaming_masks(T, np.minimum(proc, left), proc, np.full(B, T), (left, right))
+        _, (q, k, v) = sc.frames()
+        out = ops.paged_relpos_attn(q, k, v, pos, bu, bv, torch.from_numpy(mask_np).to(cuda), num_heads=H, left=left,
+                                    pages=sc.pages, layer=0, append=True)
+        dk_win, dv_win = sc.dense_update(0, k, v)
+        got = to_np64(out)
+        args = (to_np64(q), dk_win, dv_win, to_np64(pos))
+        u64, v64 = to_np64(bu), to_np64(bv)
+        for name, (uu, vv) in {"clean": (u64, v64), "bias_v_dropped": (u64, 0 * v64),
+                               "biases_swapped": (v64, u64)}.items():
+            plants[name].append(float(np.abs(got - oa.relpos_attention(*args, uu, vv, mask_np, H)).max()))
+        proc += T
+    torch.cuda.synchronize()
+    worst = {name: max(e) for name, e in plants.items()}
+    print(f"  {worst} (bar {TOL[dtype]:.0e})", flush=True)
+    assert worst["clean"] <= TOL[dtype]
+    assert worst["bias_v_dropped"] > TOL[dtype] and worst["biases_swapped"] > TOL[dtype], worst
+
+
+@pytest.mark.gpu
 def test_long_window_multi_tile(cuda):
     # left context long enough that the window needs several tiles
     _run(cuda, torch.float16, B=2, H=8, dk=64, left=600, right=1, P=16, steps=6, layers=1)

@@ -8,6 +8,10 @@ ConformerEncoder step (parakeet/modules/encoder.py:11-81,229-267):
   eviction, with and without biases;
 * a closed form: with the feed-forward, attention and conv outputs zeroed, each
   layer is LayerNorm(x), checked against torch's layer_norm;
+* a case computed by hand from encoder.py:50-81 (the numbers are in the test):
+  the feed-forward branches made silu and 3 silu, attention and conv outputs
+  zeroed, so the residual order, the two 0.5 scales and the norm placement
+  fix the output;
 * a planted mistake (a feed-forward branch without its 0.5 scale) is caught.
 """
 
@@ -121,3 +125,39 @@ def test_planted_unscaled_feed_forward_is_caught(monkeypatch):
     monkeypatch.setattr(oe, "feed_forward", lambda x, sd, prefix: 2.0 * real(x, sd, prefix))
     worst, _ = _run_both(enc, B=2, steps=2, seed=10)
     assert worst > 1e-2, worst
+
+
+def test_layer_composition_by_hand():
+    """One layer, d_model 4 (2 heads), unit LayerNorms, computed by hand from
+    ConformerLayer.forward (encoder.py:50-81):
+      FF1(y) = linear2(silu(linear1(y))) with linear1 = [I; 0], linear2 = [I, 0]: silu(y)
+      FF2 the same with linear2 = 3 [I, 0]: 3 silu(y)
+      linear_out = 0 and pointwise_conv2 = 0: the attention and conv branches add 0
+      r1 = x + 0.5 silu(LN(x));  r4 = r1 + 0.5 * 3 silu(LN(r1));  out = LN(r4)
+    For x = [1, -1, 2, -2]: LN(x) = x / sqrt(2.5 + 1e-5) = [0.63245, -0.63245,
+    1.26491, -1.26491]; silu = [0.41302, -0.21943, 0.98646, -0.27846];
+    r1 = [1.20651, -1.10972, 2.49323, -2.13922] (mean 0.11270, variance
+    3.35721); LN(r1) = [0.59697, -0.66716, 1.29923, -1.22904]; 3 silu =
+    [1.15507, -0.67875, 3.06245, -0.83456]; r4 = [1.78405, -1.44910, 4.02444,
+    -2.55651] (mean 0.45073, variance 6.80051); out = [0.51129, -0.72852,
+    1.37041, -1.15318].  The second frame [0.5, 0.25, -1, 3] the same way."""
+    enc = _encoder(D=4, H=2, Ly=1, left=2, right=1, K=3, bias=False, seed=11)
+    layer = enc.layers[0]
+    eye = torch.eye(4, dtype=torch.float64)
+    with torch.no_grad():
+        for mod in layer.modules():
+            if isinstance(mod, torch.nn.LayerNorm):
+                mod.weight.fill_(1.0)
+                mod.bias.zero_()
+        for ff, scale in ((layer.feed_forward1, 1.0), (layer.feed_forward2, 3.0)):
+            ff.linear1.weight.zero_()
+            ff.linear1.weight[:4] = eye
+            ff.linear2.weight.zero_()
+            ff.linear2.weight[:, :4] = scale * eye
+        layer.self_attn.linear_out.weight.zero_()
+        layer.conv.pointwise_conv2.weight.zero_()
+    st = oe.EncoderState(1, 1, 2, 1, 4, 3)
+    x = np.array([[[1.0, -1.0, 2.0, -2.0], [0.5, 0.25, -1.0, 3.0]]])
+    got = oe.encoder_step(x, _state_dict(enc), st, np.full(1, 2), 1, 2, relpos.sinusoid_table(64, 4).astype(np.float64))
+    want = np.array([[0.51129, -0.72852, 1.37041, -1.15318], [-0.28181, -0.41795, -0.97319, 1.67296]])
+    np.testing.assert_allclose(got[0].T, want, atol=2e-5)
