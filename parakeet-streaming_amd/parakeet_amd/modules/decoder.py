@@ -17,6 +17,7 @@ There is no CPU path: without the HIP library the calls raise.
 from __future__ import annotations
 
 import ctypes
+from collections.abc import Sequence
 
 import numpy as np
 import torch
@@ -307,23 +308,79 @@ class GreedyDecoder:
 
     @staticmethod
     def _split(tok: np.ndarray, cnt: np.ndarray, lens: np.ndarray, frame_tokens: bool):
-        """Per-stream token lists from the step's [B, frames * max_symbols] tokens
-        and [B, frames] counts (frames past a stream's length count nothing); the
-        counts and offsets are computed for the whole batch at once."""
+        """Per-stream tokens from the step's [B, frames * max_symbols] tokens and
+        [B, frames] counts (frames past a stream's length count nothing); the
+        counts and offsets are computed for the whole batch at once.  Returns a
+        StreamTokens (each stream's list built when it is read), or with
+        ``frame_tokens`` a list per stream of a list per frame."""
         B = len(lens)
         if B == 0:
-            return []
+            return StreamTokens(np.zeros((0, 0), dtype=np.int32), np.zeros(0, dtype=np.int64)) if not frame_tokens else []
         T = cnt.shape[1]
         n = np.where(np.arange(T)[None, :] < np.asarray(lens)[:, None], cnt, 0).astype(np.int64)
         tot = n.sum(1)
-        # the emitted tokens only, stream after stream, as one list
+        if not frame_tokens:
+            return StreamTokens(tok, tot)
+        # the emitted tokens only, stream after stream
         flat = tok[np.arange(tok.shape[1])[None, :] < tot[:, None]].tolist()
         off = np.concatenate([[0], np.cumsum(tot)])
-        if not frame_tokens:
-            o = off.tolist()
-            return [flat[o[b] : o[b + 1]] for b in range(B)]
         edges = (off[:-1, None] + np.concatenate([np.zeros((B, 1), dtype=np.int64), np.cumsum(n, axis=1)], axis=1)).tolist()
         return [[flat[e[i] : e[i + 1]] for i in range(int(l))] for e, l in zip(edges, lens)]
+
+
+class StreamTokens(Sequence):
+    """The tokens a decode step emitted for each stream of its batch, as the
+    step left them: row b of ``rows`` [B, frames * max_symbols] holds stream b's
+    tokens in its first ``counts()[b]`` entries.  Reads as a sequence of
+    per-stream lists (``tokens[b]`` is stream b's list, built when read), so a
+    caller that touches a few streams, or only the counts, pays nothing for the
+    rest; ``flat()`` packs them stream after stream (the reference returns a
+    list per stream, model_runner.py:347-447)."""
+
+    __slots__ = ("rows", "_counts")
+
+    def __init__(self, rows: np.ndarray, counts: np.ndarray):
+        self.rows = rows
+        self._counts = counts
+
+    def __len__(self) -> int:
+        return len(self._counts)
+
+    def __getitem__(self, b):
+        if isinstance(b, slice):
+            return [self[i] for i in range(*b.indices(len(self)))]
+        n = len(self)
+        b = int(b)
+        if b < 0:
+            b += n
+        if not 0 <= b < n:
+            raise IndexError(f"stream {b} out of range for a batch of {n}")
+        return self.rows[b, : self._counts[b]].tolist()
+
+    def counts(self) -> np.ndarray:
+        """Tokens per stream, [B]."""
+        return self._counts
+
+    def total(self) -> int:
+        return int(self._counts.sum())
+
+    def offsets(self) -> np.ndarray:
+        """[B + 1] offsets of the streams' tokens in ``flat()``."""
+        return np.concatenate([[0], np.cumsum(self._counts)])
+
+    def flat(self) -> np.ndarray:
+        """Every emitted token, stream after stream."""
+        return self.rows[np.arange(self.rows.shape[1])[None, :] < self._counts[:, None]]
+
+    def __eq__(self, other):
+        if isinstance(other, StreamTokens):
+            return np.array_equal(self._counts, other._counts) and np.array_equal(self.flat(), other.flat())
+        if isinstance(other, Sequence) and not isinstance(other, (str, bytes)):
+            return len(self) == len(other) and all(self[b] == list(other[b]) for b in range(len(self)))
+        return NotImplemented
+
+    def __repr__(self) -> str:
+        return f"StreamTokens({[self[b] for b in range(min(len(self), 4))]}{' ...' if len(self) > 4 else ''})"
 
 
 class PendingTokens:
@@ -340,9 +397,11 @@ class PendingTokens:
         if self._out is None:
             self._event.synchronize()
             o = self._buf.numpy()
-            self._out = GreedyDecoder._split(o[:, : self._n_tok], o[:, self._n_tok :], self._lens, self._frame_tokens)
+            # the buffer is reused two calls later: the lazy result keeps its own copy
+            self._out = GreedyDecoder._split(o[:, : self._n_tok].copy(), o[:, self._n_tok :], self._lens,
+                                             self._frame_tokens)
             self._buf = None
         return self._out
 
 
-__all__ = ["Predictor", "Joiner", "GreedyDecoder", "PendingTokens"]
+__all__ = ["Predictor", "Joiner", "GreedyDecoder", "PendingTokens", "StreamTokens"]

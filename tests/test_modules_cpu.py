@@ -149,3 +149,30 @@ def test_encoder_loads_reference_shaped_state_dict_strictly():
     assert not res.missing_keys and not res.unexpected_keys
     for k, v in enc.state_dict().items():
         assert torch.equal(v, sd[k]), k
+
+
+def test_stream_tokens_read_like_per_stream_lists():
+    """The decode step's lazy per-stream result against the per-frame lists of
+    the same step concatenated per stream, including streams whose length cuts
+    frames off (their counts must not show) and empty streams."""
+    import numpy as np
+
+    from parakeet_amd.modules.decoder import GreedyDecoder, StreamTokens
+
+    rng = np.random.default_rng(7)
+    B, T, S = 37, 3, 5
+    cnt = rng.integers(0, S + 1, size=(B, T)).astype(np.int32)
+    tok = np.full((B, T * S), -1, dtype=np.int32)
+    for b in range(B):
+        n = int(cnt[b].sum())
+        tok[b, :n] = rng.integers(0, 1000, size=n)
+    lens = rng.integers(0, T + 1, size=B).astype(np.int32)
+    per_frame = GreedyDecoder._split(tok, cnt, lens, True)
+    want = [sum(frames, []) for frames in per_frame]
+    got = GreedyDecoder._split(tok, cnt, lens, False)
+    assert isinstance(got, StreamTokens) and len(got) == B
+    assert got == want and [got[b] for b in range(B)] == want and got[-1] == want[-1] and got[2:5] == want[2:5]
+    assert got.counts().tolist() == [len(w) for w in want] and got.total() == sum(map(len, want))
+    assert got.flat().tolist() == sum(want, []) and got.offsets()[-1] == got.total()
+    empty = GreedyDecoder._split(tok[:0], cnt[:0], lens[:0], False)
+    assert len(empty) == 0 and empty == []
