@@ -1225,7 +1225,9 @@ __global__ void __launch_bounds__(256, 4) relpos_attn_chunk_kernel(const AttnK<S
   const __amdgpu_buffer_rsrc_t r_kn = rows_rsrc(p.kn + b * p.k_sb, st_k, (uint32_t)p.T);
   const __amdgpu_buffer_rsrc_t r_vn = rows_rsrc(p.vn + b * p.v_sb, st_v, (uint32_t)p.T);
   const __amdgpu_buffer_rsrc_t r_q = rows_rsrc(p.q + b * p.q_sb, st_q, (uint32_t)min(p.T, 14));
-  const __amdgpu_buffer_rsrc_t r_pos = rows_rsrc(p.pos, st_p, (uint32_t)p.pos_rows);
+  // the position rows any score reads: 0 .. window + chunk - 2 (the staging's
+  // rows past them read zeros without a memory request)
+  const __amdgpu_buffer_rsrc_t r_pos = rows_rsrc(p.pos, st_p, (uint32_t)min(p.pos_rows, p.Lk + p.T - 1));
 
   // ---------------- prologue: every load independent of the page table
   // query operand: lane (kg, q16) holds row q16's columns ks*32 + kg*8 .. + 7
