@@ -829,13 +829,19 @@ struct Sub2Geom {
   static constexpr int VEC = 8;                                     // 16-bit elements per 16 bytes
   static constexpr int XR = 8 * NF + 7, XC = 8 * QT + 7;             // input rows / cols of the tile
   static constexpr int XN = (XR * XC + 7) / 8 * 8;
-  static constexpr int R2 = 2 * NF + 1, C2 = 2 * QT + 1, M2 = R2 * C2, T2 = (M2 + 15) / 16;  // after dw 1
+  static constexpr int R2 = 2 * NF + 1, C2 = 2 * QT + 1;  // after dw 1
   static constexpr int JG = (C2 + 3) / 4;   // first depthwise conv: groups of 4 output columns
+  // after dw 1 and conv.3, positions i2 C2P + q2: rows padded to whole 4-column
+  // groups, so every group's 4 stores land in its own row (the padding
+  // columns are never read as taps of the second depthwise conv)
+  static constexpr int C2P = 4 * JG, M2 = R2 * C2P, T2 = (M2 + 15) / 16;
   // after conv.0: rows of C1 columns stored C1P apart, so a row's 4-output group
   // reads 9 columns from one 16-byte aligned chunk and the next dword
   static constexpr int R1 = 4 * NF + 3, C1 = 4 * QT + 3, C1P = 8 * JG + 8;
   static constexpr int M1 = R1 * C1P, T1 = (M1 + 15) / 16;
-  static constexpr int M1S = ((T1 * 2) | 1) * 8;  // a1g channel stride: 8 x odd elements (distinct banks)
+  static constexpr int T1W = (T1 + W - 1) / W;  // conv.0 position tiles a wave (wave + W u)
+  static constexpr int T1P = T1W * W;           // tiles stored: every wave's last tile, zeros past M1
+  static constexpr int M1S = ((T1P * 2) | 1) * 8;  // a1g channel stride: 8 x odd elements (distinct banks)
   static constexpr int M3 = NF * QT, T3 = (M3 + 15) / 16;                                   // after dw 2
   static constexpr int GS = kSub2CG + VEC;  // a2g position stride (padded by 16 bytes)
   static constexpr int NH = W < 16 ? 2 : 1;  // channel parts of the second depthwise conv and conv.6
@@ -844,7 +850,6 @@ struct Sub2Geom {
   static constexpr int NTL = C / 16;        // channel tiles of a pointwise conv
   // conv.6: a wave takes CPW channel tiles (consecutive) and position tiles pg + PG u
   static constexpr int CPW = NTL > W ? NTL / W : 1, NTW = NTL / CPW, PG = W / NTW;
-  static constexpr int T1W = (T1 + W - 1) / W;
   // conv.3: a wave takes channel tiles 2 (w mod NP), 2 (w mod NP) + 1 and
   // position tiles w / NP + P3 u, so each wave reads 1 / P3 of the positions' rows
   static constexpr int NP = C / 32, P3 = W / NP, T2W = (T2 + P3 - 1) / P3;
@@ -888,7 +893,9 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int lr = lane & 15, lg = lane >> 4;
   const int nt = (wave % G::NTW) * G::CPW, pg = wave / G::NTW;  // the wave's first conv.6 channel tile, position group
-  const int np = wave % G::NP, pg3 = wave / G::NP;    // the wave's conv.3 channel tile pair and position group
+  // the wave's conv.3 channel tile pair and position group (0 when one group
+  // takes every position tile, which the compiler then sees)
+  const int np = wave % G::NP, pg3 = G::P3 == 1 ? 0 : wave / G::NP;
   const int F = p.F;
   const int F1 = half_up(F), F2 = half_up(F1), F3 = half_up(F2);
 
@@ -911,25 +918,27 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))
   const int len1 = half_up(s.length), len2 = half_up(len1), len3 = half_up(len2);
 
   // ---- weights, biases and the input tile, every global load issued before
-  //      the first LDS store (one round trip): the 3x3 weights as 16-byte
-  //      chunks of their [C][9] arrays, the input rows >= length and the
-  //      padding as zeros
-  constexpr int kWCh = 9 * C / VEC;                                   // 16-byte chunks of a [C][9] array
-  constexpr int kWPer = (kWCh + NTH - 1) / NTH;
+  //      the first LDS store (one round trip): thread c < C reads channel c's
+  //      9 taps of each 3x3 conv and its biases (as 16-bit words) and stores
+  //      them in the layouts above with dword or wider stores; the input rows
+  //      >= length and the padding as zeros
   constexpr int kXPer = (G::XN + NTH - 1) / NTH;
-  u32x4 w0c[kWPer], w2c[kWPer], w5c[kWPer];
-#pragma unroll
-  for (int u = 0; u < kWPer; ++u) {
-    const int ch = min(tid + u * NTH, kWCh - 1);
-    w0c[u] = ld16(p.w0 + ch * VEC);
-    w2c[u] = ld16(p.w2 + ch * VEC);
-    w5c[u] = ld16(p.w5 + ch * VEC);
-  }
-  float bias[5] = {0.f, 0.f, 0.f, 0.f, 0.f};  // conv.0/2/3/5/6 of channel tid
+  uint16_t k0[9], k2[9], k5[9], b0 = 0;
+  float bias[4] = {0.f, 0.f, 0.f, 0.f};  // conv.2/3/5/6 of channel tid
   if (tid < C) {
-    const ST* bp[5] = {p.b0, p.b2, p.b3, p.b5, p.b6};
+    const uint16_t* const q0 = reinterpret_cast<const uint16_t*>(p.w0) + 9 * tid;
+    const uint16_t* const q2 = reinterpret_cast<const uint16_t*>(p.w2) + 9 * tid;
+    const uint16_t* const q5 = reinterpret_cast<const uint16_t*>(p.w5) + 9 * tid;
 #pragma unroll
-    for (int k = 0; k < 5; ++k)
+    for (int k = 0; k < 9; ++k) {
+      k0[k] = q0[k];
+      k2[k] = q2[k];
+      k5[k] = q5[k];
+    }
+    if (p.b0) b0 = reinterpret_cast<const uint16_t*>(p.b0)[tid];
+    const ST* bp[4] = {p.b2, p.b3, p.b5, p.b6};
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
       if (bp[k]) bias[k] = from_st(bp[k][tid]);
   }
   // the input tile: rows >= length and the padding as zeros
@@ -949,34 +958,22 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))
       xr[u] = ok ? v : 0.f;
     }
   }
-#pragma unroll
-  for (int u = 0; u < kWPer; ++u) {
-    const int ch = tid + u * NTH;
-    if (ch < kWCh) {
-      const Chunk<ST> a = __builtin_bit_cast(Chunk<ST>, w0c[u]);
-      const Chunk<ST> b2 = __builtin_bit_cast(Chunk<ST>, w2c[u]);
-      const Chunk<ST> b5 = __builtin_bit_cast(Chunk<ST>, w5c[u]);
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        const int i = ch * VEC + e, c = i / 9, k = i - c * 9;
-        const int kt = k / 3, kf = k - kt * 3;
-        w0p[w0_index(c, k)] = a.v[e];
-        // tap kf of row kt: half kf & 1 of dword 2 kt + kf / 2 (taps 0, 1 | 2, 0)
-        const int d = 2 * kt + kf / 2;
-        reinterpret_cast<ST*>(&w2p[d >> 2][c][d & 3])[kf & 1] = b2.v[e];
-        reinterpret_cast<ST*>(&w5p[w5_index<C>(k >> 1, c)])[k & 1] = b5.v[e];
-      }
-    }
-  }
   if (tid < C) {
+    auto pk = [](uint32_t lo, uint32_t hi) { return lo | hi << 16; };
+    // conv.0: taps 0..8, the bias at 9 (it rides on a tap that reads 1), zeros
+    *reinterpret_cast<uint2*>(&w0p[w0_index(tid, 0)]) = make_uint2(pk(k0[0], k0[1]), pk(k0[2], k0[3]));
+    *reinterpret_cast<uint2*>(&w0p[w0_index(tid, 4)]) = make_uint2(pk(k0[4], k0[5]), pk(k0[6], k0[7]));
+    *reinterpret_cast<uint2*>(&w0p[w0_index(tid, 8)]) = make_uint2(pk(k0[8], b0), 0u);
+    *reinterpret_cast<uint2*>(&w0p[w0_index(tid, 12)]) = make_uint2(0u, 0u);
+    // first depthwise conv: rows kt as (w0 w1) and (w2 0)
+    *reinterpret_cast<u32x4*>(&w2p[0][tid][0]) = u32x4{pk(k2[0], k2[1]), k2[2], pk(k2[3], k2[4]), k2[5]};
+    *reinterpret_cast<u32x4*>(&w2p[1][tid][0]) = u32x4{pk(k2[6], k2[7]), k2[8], 0u, 0u};
+    // second depthwise conv: tap pairs, tap 9 is 0
 #pragma unroll
-    for (int kt = 0; kt < 3; ++kt) reinterpret_cast<ST*>(&w2p[(2 * kt + 1) >> 2][tid][(2 * kt + 1) & 3])[1] = to_st<ST>(0.f);
-    reinterpret_cast<ST*>(&w5p[w5_index<C>(4, tid)])[1] = to_st<ST>(0.f);
-    w0p[w0_index(tid, 9)] = to_st<ST>(bias[0]);  // the bias rides on a tap that reads 1
+    for (int pp = 0; pp < 4; ++pp) w5p[w5_index<C>(pp, tid)] = pk(k5[2 * pp], k5[2 * pp + 1]);
+    w5p[w5_index<C>(4, tid)] = k5[8];
 #pragma unroll
-    for (int k = 10; k < 16; ++k) w0p[w0_index(tid, k)] = to_st<ST>(0.f);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) bsm[k][tid] = bias[k + 1];
+    for (int k = 0; k < 4; ++k) bsm[k][tid] = bias[k];
   }
   // conv.3's weight rows of the wave's channel tiles: lane holds W3[n][g + 8 lg ..];
   // the first group's k-step loads now, each next one during the group before
@@ -1032,7 +1029,9 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))
   }
 
   // conv.0 for channels g .. g + 31 -> a1 [channel][position]: D rows are
-  // positions, so a lane holds 4 consecutive positions of one channel
+  // positions, so a lane holds 4 consecutive positions of one channel.  Every
+  // wave stores T1W tiles (the tiles past the map are zeros), so the products
+  // carry no branch and the compiler interleaves them with the stores.
   auto conv0 = [&](int g, ST* a1) {
     s16x4_t wop[2];
 #pragma unroll
@@ -1040,34 +1039,49 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))
 #pragma unroll
     for (int u = 0; u < G::T1W; ++u) {
       const int mt = wave + W * u;
-      if (mt < G::T1) {
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-          const f32x4_t d = Mma16<ST>::k16(xop[u], wop[ct], f32x4_t{0.f, 0.f, 0.f, 0.f});
-          *reinterpret_cast<uint2*>(&a1[(ct * 16 + lr) * G::M1S + mt * 16 + 4 * lg]) =
-              make_uint2(relu2(cvt2<ST>(d[0], d[1])), relu2(cvt2<ST>(d[2], d[3])));
-        }
+      for (int ct = 0; ct < 2; ++ct) {
+        const f32x4_t d = Mma16<ST>::k16(xop[u], wop[ct], f32x4_t{0.f, 0.f, 0.f, 0.f});
+        *reinterpret_cast<uint2*>(&a1[(ct * 16 + lr) * G::M1S + mt * 16 + 4 * lg]) =
+            make_uint2(relu2(cvt2<ST>(d[0], d[1])), relu2(cvt2<ST>(d[2], d[3])));
       }
     }
   };
   // first depthwise conv of channels g .. g + 31 -> a2 [position][32]: a
-  // thread takes one channel and 4 adjacent output columns of one output row;
-  // per input row, 9 columns come from a 16-byte chunk and the next one's
-  // first dword (that chunk read whole where registers allow: a 16-byte LDS
-  // read of 16 channels' rows is conflict free, a 4-byte one at this stride
-  // is not), and each tap pair is one fp32-accumulating dot2 (w0 w1 | w2 0)
+  // thread takes one channel (tid mod 32, the same in every group) and 4
+  // adjacent output columns of one output row, at most D1N such items, whose
+  // a1 / a2 offsets are worked out once (d1off: a1 offset | a2 offset << 16,
+  // all ones past the items); per input row, 9 columns come from a 16-byte
+  // chunk and the next one's first dword (that chunk read whole where
+  // registers allow: a 16-byte LDS read of 16 channels' rows is conflict
+  // free, a 4-byte one at this stride is not), and each tap pair is one
+  // fp32-accumulating dot2 (w0 w1 | w2 0)
+  constexpr int kD1Items = kSub2CG * G::R2 * G::JG, D1N = (kD1Items + NTH - 1) / NTH;
+  static_assert(NTH % kSub2CG == 0, "a thread keeps its channel");
+  static_assert(kSub2CG * G::M1S <= 65536 && G::T2 * 16 * G::GS <= 65536, "16-bit offsets");
+  const int dc = tid % kSub2CG;
+  uint32_t d1off[D1N];
+#pragma unroll
+  for (int u = 0; u < D1N; ++u) {
+    const int rest = tid / kSub2CG + u * (NTH / kSub2CG);
+    const int i2 = rest % G::R2, jg = rest / G::R2;
+    d1off[u] = rest < G::R2 * G::JG
+                   ? (uint32_t)(dc * G::M1S + 2 * i2 * G::C1P + 8 * jg) |
+                         ((uint32_t)((i2 * G::C2P + 4 * jg) * G::GS + dc) << 16)
+                   : ~0u;
+  }
   auto dwconv1 = [&](int g, const ST* a1, ST* a2) {
-    for (int it = tid; it < kSub2CG * G::R2 * G::JG; it += NTH) {
-      const int c = it % kSub2CG, rest = it / kSub2CG;
-      const int i2 = rest % G::R2, jg = rest / G::R2;
-      const u32x4 wa = *reinterpret_cast<const u32x4*>(&w2p[0][g + c][0]);
-      const u32x4 wb = *reinterpret_cast<const u32x4*>(&w2p[1][g + c][0]);
-      const uint32_t wr[6] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y};
-      const float bv = bsm[0][g + c];
+    const u32x4 wa = *reinterpret_cast<const u32x4*>(&w2p[0][g + dc][0]);
+    const u32x4 wb = *reinterpret_cast<const u32x4*>(&w2p[1][g + dc][0]);
+    const uint32_t wr[6] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y};
+    const float bv = bsm[0][g + dc];
+#pragma unroll
+    for (int u = 0; u < D1N; ++u) {
+      if (d1off[u] == ~0u) continue;
       float o[4] = {bv, bv, bv, bv};
 #pragma unroll
       for (int kt = 0; kt < 3; ++kt) {
-        const ST* row = &a1[c * G::M1S + (2 * i2 + kt) * G::C1P + 8 * jg];
+        const ST* row = &a1[(d1off[u] & 0xffffu) + kt * G::C1P];
         const u32x4 q = *reinterpret_cast<const u32x4*>(row);
         uint32_t d4;
         if constexpr (G::T2W * 2 <= 8) {
@@ -1083,10 +1097,9 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))
       }
       const uint32_t p01 = cvt2<ST>(o[0], o[1]), p23 = cvt2<ST>(o[2], o[3]);
       const uint16_t h[4] = {(uint16_t)p01, (uint16_t)(p01 >> 16), (uint16_t)p23, (uint16_t)(p23 >> 16)};
-      uint16_t* const dst = reinterpret_cast<uint16_t*>(&a2[(i2 * G::C2 + 4 * jg) * G::GS + c]);
+      uint16_t* const dst = reinterpret_cast<uint16_t*>(&a2[d1off[u] >> 16]);
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj)
-        if (4 * jg + jj < G::C2) dst[jj * G::GS] = h[jj];
+      for (int jj = 0; jj < 4; ++jj) dst[jj * G::GS] = h[jj];
     }
   };
   // conv.3: one k-step over a group's 32 input channels (weights in wk) for
@@ -1127,7 +1140,7 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))
 #pragma unroll
   for (int u = 0; u < G::T2W; ++u) {
     const int m = (pg3 + G::P3 * u) * 16 + lr;
-    const int i2 = m / G::C2, q2 = m - i2 * G::C2;
+    const int i2 = m / G::C2P, q2 = m - i2 * G::C2P;
     const int r2 = 2 * t0 - 2 + i2, c2 = 2 * p0 - 2 + q2;
     const bool ok = m < G::M2 && r2 >= 0 && r2 < len2 && c2 >= 0 && c2 < F2;
 #pragma unroll
@@ -1185,12 +1198,12 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))
         sum[0] = x.x, sum[1] = x.y, sum[2] = x.z, sum[3] = x.w;
         sum[4] = y.x, sum[5] = y.y, sum[6] = y.z, sum[7] = y.w;
       }
-      const ST* const src = &a2o[(2 * f * G::C2 + 2 * q) * G::RS + cc];
+      const ST* const src = &a2o[(2 * f * G::C2P + 2 * q) * G::RS + cc];
 #pragma unroll
       for (int pp = 0; pp < 5; ++pp) {
         const int ta = 2 * pp, tb = 2 * pp + 1;
-        const u32x4 A = ld16(src + ((ta / 3) * G::C2 + ta % 3) * G::RS);
-        const u32x4 B = tb < 9 ? ld16(src + ((tb / 3) * G::C2 + tb % 3) * G::RS) : u32x4{0u, 0u, 0u, 0u};
+        const u32x4 A = ld16(src + ((ta / 3) * G::C2P + ta % 3) * G::RS);
+        const u32x4 B = tb < 9 ? ld16(src + ((tb / 3) * G::C2P + tb % 3) * G::RS) : u32x4{0u, 0u, 0u, 0u};
         const u32x4 W0 = *reinterpret_cast<const u32x4*>(&w5p[w5_index<C>(pp, cw)]);
         const u32x4 W1 = *reinterpret_cast<const u32x4*>(&w5p[w5_index<C>(pp, cw + 4)]);
         const uint32_t a[4] = {A.x, A.y, A.z, A.w}, bb[4] = {B.x, B.y, B.z, B.w};
