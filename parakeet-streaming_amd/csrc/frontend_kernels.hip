@@ -820,6 +820,14 @@ __device__ static inline int w5_index(int pp, int c) {
   return pp * C + ((c >> 2) & 1) * (C / 2) + (c >> 3) * 4 + (c & 3);
 }
 
+// Position (within a wave's 16 T1W conv.0 positions) of row r of the wave's
+// conv.0 tile u: tiles 2v and 2v + 1 map row 4a + e to 32 v + 8 a + 4 (u & 1)
+// + e, so D fragments of the pair in one lane are 8 consecutive positions; a
+// last unpaired tile maps row r to 32 (T1W / 2) + r
+__device__ static inline int sub2_pos(int u, int r, int T1W) {
+  return u < (T1W & ~1) ? 32 * (u >> 1) + 8 * (r >> 2) + 4 * (u & 1) + (r & 3) : 32 * (T1W >> 1) + r;
+}
+
 // W waves a workgroup: 16 (one workgroup a CU), or 8 with the second stage
 // run over channel halves (NH = 2) so that two workgroups share a CU and one's
 // depthwise (VALU) work overlaps the other's pointwise (MFMA) work
@@ -892,7 +900,9 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))
 
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int lr = lane & 15, lg = lane >> 4;
-  const int nt = (wave % G::NTW) * G::CPW, pg = wave / G::NTW;  // the wave's first conv.6 channel tile, position group
+  // the wave's first conv.6 channel tile and its position group (0 when one
+  // group takes every position tile)
+  const int nt = (wave % G::NTW) * G::CPW, pg = G::PG == 1 ? 0 : wave / G::NTW;
   // the wave's conv.3 channel tile pair and position group (0 when one group
   // takes every position tile, which the compiler then sees)
   const int np = wave % G::NP, pg3 = G::P3 == 1 ? 0 : wave / G::NP;
@@ -991,9 +1001,10 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))
   }
   __syncthreads();
 
-  // ---- conv.0 A operands, per wave its position tiles wave + 16 u: lane
-  //      (lr, lg) holds taps 4 lg .. 4 lg + 3 of position 16 mt + lr (tap 9
-  //      reads 1, taps 10.. read 0), all zero for a position outside the map
+  // ---- conv.0 A operands: the wave's T1W tiles cover its 16 T1W positions
+  //      from 16 T1W wave on (sub2_pos); lane (lr, lg) holds taps 4 lg ..
+  //      4 lg + 3 of the position of row lr (tap 9 reads 1, taps 10.. read 0),
+  //      all zero for a position outside the map
   int toff[4];
   short tval[4];
 #pragma unroll
@@ -1005,17 +1016,20 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))
   s16x4_t xop[G::T1W];
 #pragma unroll
   for (int u = 0; u < G::T1W; ++u) {
-    const int m = (wave + W * u) * 16 + lr;
+    const int m = 16 * G::T1W * wave + sub2_pos(u, lr, G::T1W);
     const int mm = min(m, G::M1 - 1);
     const int i1 = mm / G::C1P, qr = mm - i1 * G::C1P, q1 = min(qr, G::C1 - 1);
     const int r1 = 4 * t0 - 6 + i1, c1 = 4 * p0 - 6 + qr;
     const bool ok = m < G::M1 && qr < G::C1 && r1 >= 0 && r1 < len1 && c1 >= 0 && c1 < F1;
-    const ST* const x = &xin[2 * i1 * G::XC + 2 * q1];
+    const ST* const x = &xin[2 * i1 * G::XC + 2 * q1];  // in the tile for every lane
+    // masked with an and rather than a select, so the reads are not moved
+    // under a branch (one LDS round trip for all of them)
+    const short okm = ok ? short(-1) : short(0);
     short v[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const short t = __builtin_bit_cast(short, x[toff[e]]);
-      v[e] = ok ? (4 * lg + e < 9 ? t : tval[e]) : short(0);
+      v[e] = (4 * lg + e < 9 ? t : tval[e]) & okm;
     }
     xop[u] = s16x4_t{v[0], v[1], v[2], v[3]};
   }
@@ -1029,20 +1043,30 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))
   }
 
   // conv.0 for channels g .. g + 31 -> a1 [channel][position]: D rows are
-  // positions, so a lane holds 4 consecutive positions of one channel.  Every
-  // wave stores T1W tiles (the tiles past the map are zeros), so the products
-  // carry no branch and the compiler interleaves them with the stores.
+  // positions, so a lane holds 4 positions of one channel per tile, and 8
+  // consecutive ones over a pair of tiles (sub2_pos): one 16-byte store, which
+  // 16 channels' rows at this stride take without bank conflicts.  Every wave
+  // stores T1W tiles (the tiles past the map are zeros), so the products carry
+  // no branch and the compiler interleaves them with the stores.
   auto conv0 = [&](int g, ST* a1) {
     s16x4_t wop[2];
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) wop[ct] = *reinterpret_cast<const s16x4_t*>(&w0p[w0_index(g + ct * 16 + lr, 4 * lg)]);
+    ST* const a1w = a1 + 16 * G::T1W * wave;
 #pragma unroll
-    for (int u = 0; u < G::T1W; ++u) {
-      const int mt = wave + W * u;
+    for (int ct = 0; ct < 2; ++ct) {
+      ST* const row = a1w + (ct * 16 + lr) * G::M1S;
 #pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        const f32x4_t d = Mma16<ST>::k16(xop[u], wop[ct], f32x4_t{0.f, 0.f, 0.f, 0.f});
-        *reinterpret_cast<uint2*>(&a1[(ct * 16 + lr) * G::M1S + mt * 16 + 4 * lg]) =
+      for (int v = 0; v < G::T1W / 2; ++v) {
+        const f32x4_t d0 = Mma16<ST>::k16(xop[2 * v], wop[ct], f32x4_t{0.f, 0.f, 0.f, 0.f});
+        const f32x4_t d1 = Mma16<ST>::k16(xop[2 * v + 1], wop[ct], f32x4_t{0.f, 0.f, 0.f, 0.f});
+        *reinterpret_cast<u32x4*>(&row[32 * v + 8 * lg]) =
+            u32x4{relu2(cvt2<ST>(d0[0], d0[1])), relu2(cvt2<ST>(d0[2], d0[3])), relu2(cvt2<ST>(d1[0], d1[1])),
+                  relu2(cvt2<ST>(d1[2], d1[3]))};
+      }
+      if constexpr (G::T1W % 2) {
+        const f32x4_t d = Mma16<ST>::k16(xop[G::T1W - 1], wop[ct], f32x4_t{0.f, 0.f, 0.f, 0.f});
+        *reinterpret_cast<uint2*>(&row[32 * (G::T1W / 2) + 4 * lg]) =
             make_uint2(relu2(cvt2<ST>(d[0], d[1])), relu2(cvt2<ST>(d[2], d[3])));
       }
     }
@@ -1052,10 +1076,10 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))
   // adjacent output columns of one output row, at most D1N such items, whose
   // a1 / a2 offsets are worked out once (d1off: a1 offset | a2 offset << 16,
   // all ones past the items); per input row, 9 columns come from a 16-byte
-  // chunk and the next one's first dword (that chunk read whole where
-  // registers allow: a 16-byte LDS read of 16 channels' rows is conflict
-  // free, a 4-byte one at this stride is not), and each tap pair is one
-  // fp32-accumulating dot2 (w0 w1 | w2 0)
+  // chunk and the next one's first dword (that chunk read whole: a 16-byte
+  // LDS read of 16 channels' rows is conflict free, a 4-byte one at this
+  // stride is not), and each tap pair is one fp32-accumulating dot2
+  // (w0 w1 | w2 0)
   constexpr int kD1Items = kSub2CG * G::R2 * G::JG, D1N = (kD1Items + NTH - 1) / NTH;
   static_assert(NTH % kSub2CG == 0, "a thread keeps its channel");
   static_assert(kSub2CG * G::M1S <= 65536 && G::T2 * 16 * G::GS <= 65536, "16-bit offsets");
@@ -1083,14 +1107,9 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))
       for (int kt = 0; kt < 3; ++kt) {
         const ST* row = &a1[(d1off[u] & 0xffffu) + kt * G::C1P];
         const u32x4 q = *reinterpret_cast<const u32x4*>(row);
-        uint32_t d4;
-        if constexpr (G::T2W * 2 <= 8) {
-          const u32x4 q2 = *reinterpret_cast<const u32x4*>(row + 8);
-          asm volatile("" ::"v"(q2.y), "v"(q2.z), "v"(q2.w));  // keep the read 16 bytes wide
-          d4 = q2.x;
-        } else {  // no registers to spare beside the conv.3 accumulators
-          d4 = *reinterpret_cast<const uint32_t*>(row + 8);
-        }
+        const u32x4 q2 = *reinterpret_cast<const u32x4*>(row + 8);
+        asm volatile("" ::"v"(q2.y), "v"(q2.z), "v"(q2.w));  // keep the read 16 bytes wide
+        const uint32_t d4 = q2.x;
         const uint32_t d[5] = {q.x, q.y, q.z, q.w, d4};
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) o[jj] = dot2<ST>(d[jj + 1], wr[2 * kt + 1], dot2<ST>(d[jj], wr[2 * kt], o[jj]));
@@ -1115,9 +1134,13 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))
       }
     }
   };
+  // Two barriers a group: conv.0 (a1g) | the depthwise conv (a1g -> a2g) |
+  // conv.3 (a2g) with the next group's conv.0 (a1g, whose last reader is
+  // behind the second barrier); the next depthwise conv rewrites a2g only
+  // after the next first barrier, which every wave reaches after its conv.3.
+  conv0(0, a1g);
 #pragma unroll 1
   for (int g = 0; g < C; g += kSub2CG) {
-    conv0(g, a1g);
     __syncthreads();
     dwconv1(g, a1g, a2g);
     __syncthreads();
@@ -1125,9 +1148,10 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))
     if (g + kSub2CG < C) {  // the next group's k-step loads during its conv.0 and depthwise conv
 #pragma unroll
       for (int h = 0; h < 2; ++h) wk[h] = ld16(w3row[h] + g + kSub2CG);
+      conv0(g + kSub2CG, a1g);
     }
-    __syncthreads();  // the next group rewrites a1g / a2g
   }
+  __syncthreads();  // the second stage rewrites the group buffers
 
   // ---- second stage, NH channel parts of CH channels one after the other:
   //      conv.3's mask and ReLU -> a2out [position][CH] (over the group
@@ -1170,9 +1194,8 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))
         }
       }
     }
-    // conv.6's weights for the wave's channel tiles and this part's k-steps:
-    // with one workgroup a CU they load while the second depthwise conv runs;
-    // with two (fewer registers a wave) after it, while the other workgroup runs
+    // conv.6's weights for the wave's channel tiles and this part's k-steps
+    // load while the second depthwise conv runs
     u32x4 w6q[G::CPW][G::KSH];
     auto load_w6 = [&]() {
 #pragma unroll
@@ -1181,7 +1204,7 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))
         for (int kk = 0; kk < G::KSH; ++kk)
           w6q[i][kk] = ld16(p.w6 + (int64_t)((nt + i) * 16 + lr) * C + VEC * lg + (hh * G::KSH + kk) * 32);
     };
-    if constexpr (G::NH == 1) load_w6();
+    load_w6();
     __syncthreads();
 
     // second depthwise conv, masked: a thread takes 8 channels of one
@@ -1219,7 +1242,6 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))
                        cvt2<ST>(sum[6], sum[7])};
       *reinterpret_cast<u32x4*>(&a3[m3 * G::RS + cc]) = ok ? o : u32x4{0u, 0u, 0u, 0u};
     }
-    if constexpr (G::NH > 1) load_w6();
     __syncthreads();
 
     // conv.6 k-steps over the part's channels
