@@ -17,8 +17,10 @@ The default run then adds, each under its own key with its roofline and CPU
 baseline: the large model's own 14-frame chunk (``large_t14``), the small shape
 at 64 streams (``small_64streams``), the fragmentation stress at 1024 streams
 (``frag_1024streams``) and the end-to-end pcm16 -> tokens step at 128 streams
-(``e2e_pcm16_128streams``); and, under ``concurrent_streams.measured_max``, a
-timed run at the largest batch the GPU holds at the headline shape.
+of the small model (``e2e_pcm16_128streams``) and of the large one (128 mels,
+24 layers, 14 frames a step, 2-layer predictor: ``e2e_pcm16_large_128streams``);
+and, under ``concurrent_streams.measured_max``, a timed run at the largest batch
+the GPU holds at the headline shape.
 
 Prints one JSON line on stdout; progress goes to stderr.
 """
@@ -190,6 +192,18 @@ def cpu_baseline(shape, streams: int, budget_s: float, seed: int) -> dict:
 
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16
 
+# pcm16 -> tokens models (config.py:5-31): mels, d_model, heads, layers, conv
+# kernel, left / right context, subsampling channels, dtype, vocabulary,
+# predictor layers; the first and the next pcm chunks (samples, model_runner.py:53-56)
+# and the per-slot sample and mel rings that hold them; the bias added to the
+# random-init joint's blank logit, so that frames end on blank or on tokens
+E2E_MODELS = {
+    "small": dict(n_mels=80, D=512, H=8, layers=17, K=9, left=70, right=1, C=256, dtype="fp16", vocab=1026,
+                  pred_layers=1, first=1440, chunk=2560, ring=8192, mel_rows=64, blank_bias=3.0),
+    "large": dict(n_mels=128, D=1024, H=8, layers=24, K=9, left=70, right=13, C=256, dtype="bf16", vocab=1024,
+                  pred_layers=2, first=16800, chunk=17920, ring=32768, mel_rows=256, blank_bias=4.0),
+}
+
 
 def synth_pcm(streams: int, n: int, seed: int):
     """int16 pcm per stream: 3 sinusoids of random frequency (100-4000 Hz),
@@ -234,54 +248,59 @@ def _graph_time_us(fn, device, reps: int = 20, inner: int = 10) -> float:
     return 1000.0 * a.elapsed_time(b) / (reps * inner)
 
 
-def front_end_cpu_baseline(sub_sd: dict, budget_s: float, seed: int) -> dict:
+def front_end_cpu_baseline(sub_sd: dict, budget_s: float, seed: int, n_mels: int = 80, first: int = 1440,
+                           chunk: int = 2560) -> dict:
     """The oracle's per-stream pre-encode (FeatureExtractor.push + ConvSubsampling
     on the [cache ; new] window + drop, model_runner.py:181-252) on one host core,
-    on 160 ms chunks of one stream, for about ``budget_s`` seconds."""
+    on ``chunk``-sample chunks of one stream after a ``first``-sample one, for
+    about ``budget_s`` seconds (at least two chunks)."""
     import numpy as np
 
     from oracle import frontend as ofe
 
     from threadpoolctl import threadpool_limits
 
-    p = ofe.FeParams(n_mels=80)
+    p = ofe.FeParams(n_mels=n_mels)
     st = ofe.PreEncodeState(ofe.FeState(p, noise_id=1, seed=1), sub_sd, store_dtype=None)
-    pcm = synth_pcm(1, 1440 + 2560 * 400, seed)[0].astype(np.float32) / 32768.0
+    n_chunks = max(2, min(400, int(400 * 2560 / chunk)))
+    pcm = synth_pcm(1, first + chunk * n_chunks, seed)[0].astype(np.float32) / 32768.0
     with threadpool_limits(limits=1):  # one core, BLAS included
-        st.push(pcm[:1440])
-        pos, chunks, t0 = 1440, 0, time.perf_counter()
-        while time.perf_counter() - t0 < budget_s and pos + 2560 <= len(pcm):
-            st.push(pcm[pos : pos + 2560])
-            pos += 2560
+        st.push(pcm[:first])
+        pos, chunks, t0 = first, 0, time.perf_counter()
+        while (time.perf_counter() - t0 < budget_s or chunks < 2) and pos + chunk <= len(pcm):
+            st.push(pcm[pos : pos + chunk])
+            pos += chunk
             chunks += 1
         el = time.perf_counter() - t0
     return {"chunks_per_s": chunks / el, "chunks": chunks, "seconds": el}
 
 
-def decode_cpu_baseline(pred, joint, vocab: int, budget_s: float, streams: int) -> dict:
+def decode_cpu_baseline(pred, joint, vocab: int, budget_s: float, streams: int, frames: int = 2,
+                        layers: int = 1) -> dict:
     """The oracle's greedy decoding (float64 numpy, one host core) of one stream
-    on 2-frame steps, for about ``budget_s`` seconds, scaled to ``streams`` streams."""
+    on ``frames``-frame steps, for about ``budget_s`` seconds, scaled to
+    ``streams`` streams."""
     import numpy as np
     import torch
 
     from oracle import rnnt
     from threadpoolctl import threadpool_limits
 
-    P = rnnt.RnntParams(pred.state_dict(), joint.state_dict(), 1)
+    P = rnnt.RnntParams(pred.state_dict(), joint.state_dict(), layers)
     sd = rnnt.StreamDecoder(P, vocab)
     g = np.random.default_rng(13)
     n, toks, t0 = 0, 0, time.perf_counter()
     with threadpool_limits(limits=1):
         while time.perf_counter() - t0 < budget_s:
-            toks += len(sd.decode(g.standard_normal((2, P.w_enc.shape[1]))))
+            toks += len(sd.decode(g.standard_normal((frames, P.w_enc.shape[1]))))
             n += 1
     el = time.perf_counter() - t0
     return {
         "value": round(n / el / streams, 4),
-        "unit": f"decode steps/s ({streams} streams x 2 frames)",
+        "unit": f"decode steps/s ({streams} streams x {frames} frames)",
         "cores": 1,
         "kind": "port",
-        "sample": f"{n} two-frame steps of one stream through the oracle's greedy loop (float64 numpy), "
+        "sample": f"{n} {frames}-frame steps of one stream through the oracle's greedy loop (float64 numpy), "
         f"{toks} tokens, in {el:.1f} s, scaled to {streams} streams per step",
     }
 
@@ -312,20 +331,24 @@ def encoder_cpu_baseline(enc, budget_s: float, layers: int, heads: int, left: in
 
 
 def encoder_bench(args, device) -> dict:
-    """``--config e2e``: one streaming step of a random-init small FastConformer
-    from pcm16 to tokens -- 128 streams, each fed a 160 ms chunk (2560 samples)
-    per step: the batched front end (pk_fe_step: sample ring, dither,
+    """``--config e2e``: one streaming step of a random-init FastConformer from
+    pcm16 to tokens, ``--streams`` streams all live (E2E_MODELS; ``--model``):
+    * small: 80 mels, 17 layers, d_model 512, fp16, each stream fed a 160 ms
+      chunk (2560 samples) per step, 2 encoder frames per step;
+    * large: 128 mels, 24 layers, d_model 1024, bf16, 1.12 s chunks (17920
+      samples), 14 encoder frames per step (att_context (70, 13)), a 2-layer
+      predictor.
+    The step: the batched front end (pk_fe_step: sample ring, dither,
     pre-emphasis, FFT, Slaney mel, log; pk_subsample: the 8x convolution stack
-    over each stream's [9 cached + 16 new] mel window; the ``out`` GEMM;
-    model_runner.py:181-252), the encoder (17 layers, d_model 512, 8 heads,
-    feed-forward x4, depthwise conv kernel 9, left context 70, 2 frames per step:
-    torch projections and feed-forward GEMMs, pk_paged_relpos_attn, pk_conv_step,
-    pk_streaming_mask; encoder.py:229-267), then greedy RNNT decoding
-    (pk_rnnt_greedy_step: up to 5 symbols a frame, predictor state per slot on
-    the device; model_runner.py:306-447) with one token copy per step; fp16.
-    Input: int16 pcm of 3 random sinusoids (100-4000 Hz) plus noise at 20 dB
-    SNR, resident on the GPU.  Also times the front-end kernels, the decode step
-    and the conv step alone."""
+    over each stream's [cached ; new] mel window; the ``out`` GEMM;
+    model_runner.py:181-252), the encoder (8 heads, feed-forward x4, depthwise
+    conv kernel 9, left context 70: torch projections and feed-forward GEMMs,
+    pk_paged_relpos_attn, pk_conv_step, pk_streaming_mask; encoder.py:229-267),
+    then greedy RNNT decoding (pk_rnnt_greedy_step: up to 5 symbols a frame,
+    predictor state per slot on the device; model_runner.py:306-447) with one
+    token copy per step.  Input: int16 pcm of 3 random sinusoids (100-4000 Hz)
+    plus noise at 20 dB SNR, resident on the GPU.  Also times the front-end
+    kernels, the decode step and the conv step alone."""
     import numpy as np
     import torch
 
@@ -334,12 +357,14 @@ def encoder_bench(args, device) -> dict:
     from parakeet_amd.modules.encoder import ConformerEncoder, EncoderStepGraph
     from parakeet_amd.modules.frontend import ConvSubsampling, FeatureExtractor, PreEncoder
 
-    B, D, H, Ly, K, left, right = args.streams, 512, 8, 17, 9, 70, 1
-    vocab, out_scale, blank_bias = 1026, 4.0, 3.0
-    n_mels, C = 80, 256
+    model = getattr(args, "model", "small")
+    m = E2E_MODELS[model]
+    B, D, H, Ly, K, left, right = args.streams, m["D"], m["H"], m["layers"], m["K"], m["left"], m["right"]
+    vocab, out_scale, blank_bias = m["vocab"], 4.0, m["blank_bias"]
+    n_mels, C = m["n_mels"], m["C"]
     T = right + 1
-    hop, chunk = 160, 2560
-    dt = torch.float16
+    hop, first_chunk, chunk = 160, m["first"], m["chunk"]
+    dt = {"fp16": torch.float16, "bf16": torch.bfloat16}[m["dtype"]]
     torch.manual_seed(4)
     enc = ConformerEncoder(
         feat_in=n_mels, hidden_size=D, ff_expansion_factor=4, num_layers=Ly, num_heads=H, subsampling_factor=8,
@@ -357,7 +382,7 @@ def encoder_bench(args, device) -> dict:
     # predictor and joiner (config.py:19-22), default init with the output layer
     # scaled and the blank logit biased so frames end on blank or on tokens
     # (the token rate is reported below)
-    pred = Predictor(640, 640, 1, vocab)
+    pred = Predictor(640, 640, m["pred_layers"], vocab)
     joint = Joiner(D, 640, 640, num_classes=vocab)
     with torch.no_grad():
         joint.joint_net[2].weight.mul_(out_scale)
@@ -369,13 +394,13 @@ def encoder_bench(args, device) -> dict:
     dec = GreedyDecoder(pred, joint, blank_id=vocab, num_slots=B)
     dec.reset_slot(np.arange(B))
     fx = FeatureExtractor(n_mels=n_mels, seed=6, device=device)
-    pre = PreEncoder(fx, sub, num_slots=B, device=device)
+    pre = PreEncoder(fx, sub, num_slots=B, device=device, ring_size=m["ring"], mel_rows=m["mel_rows"])
     slots = np.arange(B)
     for s in slots:
         pre.reset_slot(s)
     state = enc.init_streaming_state(batch_size=B, device=device, dtype=dt)
-    pre_steps = 36 + args.warmup
-    n_total = 1440 + chunk * (pre_steps + args.steps)
+    pre_steps = -(-left // T) + 1 + args.warmup  # past the 70-frame window
+    n_total = first_chunk + chunk * (pre_steps + args.steps)
     log(f"synthesising {B} x {n_total} pcm16 samples")
     # at most 256 distinct signals, repeated over larger batches (each stream's
     # dither still differs)
@@ -399,7 +424,7 @@ def encoder_bench(args, device) -> dict:
 
     def step():
         nonlocal pos, n_tokens, n_frames, pending, last_enc
-        n = 1440 if pos == 0 else chunk
+        n = first_chunk if pos == 0 else chunk
         rows, counts, first = pre.step(slots, pcm[:, pos : pos + n], n, False)
         pos += n
         if not (counts == T).all():
@@ -455,7 +480,7 @@ def encoder_bench(args, device) -> dict:
 
         # the front-end kernels alone on the last step's records (re-running a
         # step's records recomputes the same frames into the same ring rows)
-        fe_args = dict(dither=fx.dither, seed=fx.seed, max_new=chunk, max_frames=16)
+        fe_args = dict(dither=fx.dither, seed=fx.seed, max_new=chunk, max_frames=chunk // hop)
         samples = pcm[:, pos - chunk : pos]
         flat = torch.empty((B * T, C * sub.final_freq_dim), dtype=dt, device=device)
         w = sub.conv_weights()
@@ -512,12 +537,17 @@ def encoder_bench(args, device) -> dict:
         log("timed the attention kernel on the step's pages")
     s = 2
     conv_bytes = B * s * (T * 2 * D + 2 * (K - 1) * D + T * D) + s * D * (K + 2)
-    # front-end algorithmic work per step (steady state: 16 new frames, window of 25)
-    F1, F2, F3 = 41, 21, 11
-    fe_bytes = B * (chunk * 2 + chunk * 4 + 16 * n_mels * 4)  # pcm in, ring write, mel rows out
-    # the MACs the 2 kept output frames of each stream depend on: conv.0 rows 2..12,
-    # first depthwise + pointwise rows 2..6, second depthwise + pointwise rows 2..3
-    sub_macs = B * (11 * F1 * C * 9 + 5 * F2 * C * 9 + 5 * F2 * C * C + 2 * F3 * C * 9 + 2 * F3 * C * C)
+    # front-end algorithmic work per step (steady state: chunk / hop new mel frames)
+    F1 = n_mels // 2 + 1
+    F2 = F1 // 2 + 1
+    F3 = F2 // 2 + 1
+    fe_bytes = B * (chunk * 2 + chunk * 4 + (chunk // hop) * n_mels * 4)  # pcm in, ring write, mel rows out
+    # the MACs the T kept output frames of each stream depend on: 4 T + 3 rows
+    # of conv.0, 2 T + 1 of the first depthwise conv and conv.3, T of the second
+    # depthwise conv and conv.6 (T = 2: conv.0 rows 2..12, first depthwise +
+    # pointwise rows 2..6, second depthwise + pointwise rows 2..3)
+    sub_macs = B * ((4 * T + 3) * F1 * C * 9 + (2 * T + 1) * F2 * C * 9 + (2 * T + 1) * F2 * C * C
+                    + T * F3 * C * 9 + T * F3 * C * C)
     sub_tflops = 2 * sub_macs / (sub_us * 1e-6) / 1e12
     # attention: algorithmic bytes per launch (K/V window read, K/V append write,
     # query read and output write, block-table row, mask bytes) plus the shared
@@ -530,18 +560,20 @@ def encoder_bench(args, device) -> dict:
         from parakeet_amd import synth
 
         part_s = min(args.cpu_baseline_seconds, 10.0)
-        att_cpu = cpu_baseline(synth.SMALL_FP16, B, args.cpu_baseline_seconds, seed=5)
+        att_cpu = cpu_baseline(synth.SMALL_FP16 if model == "small" else synth.LARGE_BF16_T14, B,
+                               args.cpu_baseline_seconds, seed=5)
         att_cpu["sample"] = ("the reference's dense encoder-attention path only (not the whole pcm16 -> tokens step): "
                              + att_cpu["sample"])
-        dec_cpu = decode_cpu_baseline(pred, joint, vocab, part_s, B)
+        dec_cpu = decode_cpu_baseline(pred, joint, vocab, part_s, B, frames=T, layers=m["pred_layers"])
         sd = {k: v.detach().double().cpu().numpy() for k, v in sub.state_dict().items()}
-        cb = front_end_cpu_baseline(sd, part_s, seed=8)
+        cb = front_end_cpu_baseline(sd, part_s, seed=8, n_mels=n_mels, first=first_chunk, chunk=chunk)
+        chunk_ms = 1000.0 * chunk / 16000.0
         cpu = {
             "value": round(cb["chunks_per_s"] / B, 4),
-            "unit": f"front-end steps/s ({B} streams x 160 ms)",
+            "unit": f"front-end steps/s ({B} streams x {chunk_ms:g} ms)",
             "cores": 1,
             "kind": "port",
-            "sample": f"{cb['chunks']} chunks of 160 ms of one stream through the oracle's FeatureExtractor.push + "
+            "sample": f"{cb['chunks']} chunks of {chunk_ms:g} ms of one stream through the oracle's FeatureExtractor.push + "
             f"ConvSubsampling (float64 numpy) in {cb['seconds']:.1f} s, scaled to {B} streams per step",
         }
         ec = encoder_cpu_baseline(enc, part_s, Ly, H, left, right, K, D)
@@ -554,12 +586,12 @@ def encoder_bench(args, device) -> dict:
             "cores": 1,
             "kind": "port",
             "sample": f"one stream's pcm16 -> tokens step on one core, the sum of the oracle's front end "
-            f"({1000.0 / cb['chunks_per_s']:.2f} ms a 160 ms chunk), encoder step ({Ly} layers, float64 numpy, "
+            f"({1000.0 / cb['chunks_per_s']:.2f} ms a {chunk_ms:g} ms chunk), encoder step ({Ly} layers, float64 numpy, "
             f"{1000.0 * ec['seconds_per_step']:.2f} ms over {ec['steps']} steps) and greedy decode "
-            f"({1000.0 / (dec_cpu['value'] * B):.2f} ms a 2-frame step), scaled to {B} streams per step",
+            f"({1000.0 / (dec_cpu['value'] * B):.2f} ms a {T}-frame step), scaled to {B} streams per step",
         }
     result = {
-        "metric": "streaming steps/sec from pcm16 to tokens (small FastConformer: front end + 17 layers + greedy RNNT) at 1 GPU",
+        "metric": f"streaming steps/sec from pcm16 to tokens ({model} FastConformer: front end + {Ly} layers + greedy RNNT) at 1 GPU",
         "value": round(1000.0 / ms, 2),
         "unit": "steps/s",
         "n_gpus": 1,
@@ -569,13 +601,14 @@ def encoder_bench(args, device) -> dict:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp16",
+        "dtype": m["dtype"],
         "data": "synthetic pcm16 (3 random sinusoids 100-4000 Hz + noise at 20 dB SNR), random-init weights, pos biases N(0,0.02), joint output x4 with blank logit bias +3",
         "config": {
-            "workload": "small FastConformer step from pcm16: 160 ms per stream -> log-mel (80) -> 8x conv "
-            "subsampling -> 17 layers x (FF/2, paged rel-pos MHA, conv module with per-stream cache, FF/2, LN) "
-            "-> greedy RNNT (LSTM 640, joint 640, 1027 classes, up to 5 symbols a frame), "
-            f"{B} streams all live, 2 encoder frames per step",
+            "workload": f"{model} FastConformer step from pcm16: {1000.0 * chunk / 16000.0:g} ms per stream -> "
+            f"log-mel ({n_mels}) -> 8x conv subsampling -> {Ly} layers x (FF/2, paged rel-pos MHA, conv module "
+            f"with per-stream cache, FF/2, LN) -> greedy RNNT ({m['pred_layers']}-layer LSTM 640, joint 640, "
+            f"{vocab + 1} classes, up to 5 symbols a frame), {B} streams all live, {T} encoder frames per step",
+            "model": model,
             "layers": Ly,
             "d_model": D,
             "heads": H,
@@ -614,7 +647,9 @@ def encoder_bench(args, device) -> dict:
             "unit": "GB/s",
             "frac": round(att_gbs / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "kernel": "relpos_attn_mfma_kernel (fused append + paged rel-pos attention, mask tensor)",
+            "kernel": ("relpos_attn_chunk_kernel (fused append + paged rel-pos attention over one read of the "
+                       "window for all of the chunk's queries, mask tensor)" if T >= 3 else
+                       "relpos_attn_mfma_kernel (fused append + paged rel-pos attention, mask tensor)"),
             "avg_kernel_us": round(att_us, 3),
             "bytes_per_launch": att_bytes,
             "launches_timed": len(att_ev),
@@ -919,6 +954,7 @@ def main() -> int:
     ap.add_argument("--kernel-event-steps", type=int, default=50, help="eager steps timed per kernel for the roofline")
     ap.add_argument("--graph", action="store_true", help="replay every step's launches from one HIP graph (grid sized for all slots)")
     ap.add_argument("--streams", type=int, default=128, help="e2e: streams in the batch (all live)")
+    ap.add_argument("--model", choices=sorted(E2E_MODELS), default="small", help="e2e: the FastConformer size")
     ap.add_argument("--eager-encoder", action="store_true", help="e2e: issue the encoder's ops from Python instead of replaying a recorded step")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB", help="only run a device copy of MIB MiB (counter calibration)")
     ap.add_argument("--cpu-baseline-seconds", type=float, default=15.0)
@@ -993,18 +1029,23 @@ def main() -> int:
             "headline_batch": result["config"]["avg_active_streams"],
             "reference_claim": "around 80 (small) / 60 (large) concurrent streams on an A100 (README.md:26-27)",
         }
-        torch.cuda.reset_peak_memory_stats(device)
-        try:
-            e2e_args = argparse.Namespace(**vars(args))
-            e2e_args.steps, e2e_args.warmup = 20, 5
-            e2e_args.cpu_baseline_seconds = extra_s
-            e2e_args.streams = 128
-            e2e = encoder_bench(e2e_args, device)
-            for k in ("metric", "n_gpus", "higher_is_better", "scaling", "vs_baseline"):
-                e2e.pop(k, None)
-            result["e2e_pcm16_128streams"] = e2e
-        except Exception as e:
-            result["e2e_pcm16_128streams"] = {"error": repr(e)}
+        # pcm16 -> tokens, both model sizes at 128 streams
+        for key, model, steps, warmup in (("e2e_pcm16_128streams", "small", 20, 5),
+                                           ("e2e_pcm16_large_128streams", "large", 10, 3)):
+            _release(device)
+            torch.cuda.reset_peak_memory_stats(device)
+            try:
+                e2e_args = argparse.Namespace(**vars(args))
+                e2e_args.steps, e2e_args.warmup = steps, warmup
+                e2e_args.cpu_baseline_seconds = extra_s
+                e2e_args.streams = 128
+                e2e_args.model = model
+                e2e = encoder_bench(e2e_args, device)
+                for k in ("n_gpus", "higher_is_better", "scaling", "vs_baseline"):
+                    e2e.pop(k, None)
+                result[key] = e2e
+            except Exception as e:
+                result[key] = {"error": repr(e)}
     print(json.dumps(result), flush=True)
     return 0
 
