@@ -201,7 +201,7 @@ E2E_MODELS = {
     "small": dict(n_mels=80, D=512, H=8, layers=17, K=9, left=70, right=1, C=256, dtype="fp16", vocab=1026,
                   pred_layers=1, first=1440, chunk=2560, ring=8192, mel_rows=64, blank_bias=3.0),
     "large": dict(n_mels=128, D=1024, H=8, layers=24, K=9, left=70, right=13, C=256, dtype="bf16", vocab=1024,
-                  pred_layers=2, first=16800, chunk=17920, ring=32768, mel_rows=256, blank_bias=4.0),
+                  pred_layers=2, first=16800, chunk=17920, ring=32768, mel_rows=256, blank_bias=3.5),
 }
 
 
