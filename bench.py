@@ -674,7 +674,9 @@ def encoder_bench(args, device) -> dict:
             "cpu_baseline": dec_cpu,
         },
         "conv_step": {
-            "kernel": "conv_step_kernel (GLU, pad mask, causal depthwise conv with cache, LayerNorm, SiLU)",
+            "kernel": ("conv_chunk_kernel (GLU, pad mask, causal depthwise conv with cache, LayerNorm, SiLU; "
+                       "the chunk's frames in parallel)" if T >= 3 and B * (-(-D // 512)) < 6 * 256 else
+                       "conv_step_kernel (GLU, pad mask, causal depthwise conv with cache, LayerNorm, SiLU)"),
             "avg_kernel_us": round(conv_us, 3),
             "bytes_per_launch": conv_bytes,
             "gbs": round(conv_bytes / (conv_us * 1e-6) / 1e9, 1),

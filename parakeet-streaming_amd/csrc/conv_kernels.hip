@@ -5,8 +5,10 @@
 //   conv_step_kernel  GLU -> padded frames zeroed -> causal depthwise conv over
 //                     [cache ; frames] -> LayerNorm over channels -> SiLU; the
 //                     next cache is written back in place
+//   conv_chunk_kernel the same step with a chunk's frames in parallel (chunks of
+//                     3 or more frames at small batches); same bits
 //
-// One workgroup per stream.  Lane l of the workgroup owns the channels
+// conv_step_kernel: one workgroup per stream.  Lane l of the workgroup owns the channels
 // [l*VEC, (l+1)*VEC) -- one 16-byte chunk, 8 fp16/bf16 or 4 fp32 channels -- so
 // every frame row (cache, GLU input, output) is read and written as whole
 // 16-byte lanes.  A lane keeps a window of `kernel` frames of its channels in
@@ -18,6 +20,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 
 #include "pk_common.h"
@@ -67,6 +70,9 @@ constexpr int kConvMaxWaves = 8;
 // step's other kernels reuse
 template <typename ST, int K, bool STREAM>
 __global__ void __launch_bounds__(64 * kConvMaxWaves) conv_step_kernel(const ConvK<ST> p) {
+  // every product and sum rounds as written (fused only where fmaf says so),
+  // so both forms of the step give the same bits
+#pragma clang fp contract(off)
   constexpr int VEC = Tr<ST>::VEC;
   constexpr int R = K - 1;  // cache rows
   __shared__ float red[kConvMaxWaves];
@@ -152,7 +158,7 @@ __global__ void __launch_bounds__(64 * kConvMaxWaves) conv_step_kernel(const Con
     const float rstd = rsqrtf(var + p.eps);
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
-      const float z = (y[e] - mean) * rstd * lw[e] + lb[e];
+      const float z = fmaf((y[e] - mean) * rstd, lw[e], lb[e]);
       y[e] = z / (1.f + __expf(-z));  // SiLU (convolution.py:157)
     }
     if (own) st16(ob + t * p.o_st, Tr<ST>::pack(y));
@@ -175,11 +181,165 @@ __global__ void __launch_bounds__(64 * kConvMaxWaves) conv_step_kernel(const Con
   }
 }
 
+// The same step with the chunk's frames in parallel, for chunks of several
+// frames (the frames of a chunk depend on each other only through the window,
+// not through any recurrence).  One workgroup per stream of FG groups of nw
+// waves (a group's lanes own the channels as above):
+//   1. every thread: the window [cache ; GLU(frames)] into LDS as the storage
+//      type ([R + T][D]; every global load of the stream issued at once), then
+//      its last R rows back to the cache (every read of the old cache is
+//      behind the barrier);
+//   2. group g takes frames g, g + FG, ...: the depthwise conv over its window
+//      rows in LDS, LayerNorm summed over the group's waves, SiLU.
+// Every sum is the sequential kernel's, in the same order (a lane's channels,
+// then the wave, then the group's waves in order), so the two give the same
+// bits.  The reductions are workgroup barriers, so every group runs the same
+// number of frame iterations (a group past the chunk's end sums zeros).
+template <typename ST, int K, bool STREAM>
+__global__ void __launch_bounds__(64 * kConvMaxWaves) conv_chunk_kernel(const ConvK<ST> p, int FG) {
+#pragma clang fp contract(off)
+  constexpr int VEC = Tr<ST>::VEC;
+  constexpr int R = K - 1;
+  extern __shared__ __align__(16) unsigned char conv_smem[];
+
+  const int b = blockIdx.x;
+  const int nchunk = p.D / VEC;
+  const int nw = (nchunk + 63) >> 6;  // waves of a group
+  const int fg = threadIdx.x / (64 * nw), gt = threadIdx.x - fg * 64 * nw;
+  const int gwave = gt >> 6;
+  const bool own = gt < nchunk;
+  const int c0 = min(gt, nchunk - 1) * VEC;
+  const int slot = p.slots ? p.slots[b] : b;
+  if (slot < 0 || slot >= p.num_slots) return;  // workgroup-uniform
+  const int rows = R + p.T;
+  ST* const win = reinterpret_cast<ST*>(conv_smem);                               // [rows][D]
+  float* const red = reinterpret_cast<float*>(conv_smem + (size_t)rows * p.D * sizeof(ST)) + fg * nw;  // [FG][nw]
+  ST* const crow0 = p.cache + ((int64_t)slot * p.num_layers + p.layer) * R * p.D;
+  const uint8_t* padb = p.pad ? p.pad + (int64_t)b * p.T : nullptr;
+  const int64_t len = p.lengths ? p.lengths[b] : p.len_scalar;
+
+  // 1. the window: cache rows, then each frame's GLU output (convolution.py:152-155)
+  //    rounded to the storage type, zero where padded
+  for (int i = threadIdx.x; i < rows * nchunk; i += blockDim.x) {
+    const int r = i / nchunk, c = (i - r * nchunk) * VEC;
+    u32x4 v;
+    if (r < R) {
+      const ST* q = crow0 + (int64_t)r * p.D + c;
+      v = STREAM ? ld16_stream(q) : ld16(q);
+    } else {
+      const int t = r - R;
+      const ST* q = p.h + b * p.h_sb + t * p.h_st + c;
+      float a[VEC], g[VEC], o[VEC];
+      Tr<ST>::unpack(STREAM ? ld16_stream(q) : ld16(q), a);
+      Tr<ST>::unpack(STREAM ? ld16_stream(q + p.D) : ld16(q + p.D), g);
+      const bool valid = padb ? padb[t] == 0 : (int64_t)t < len;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) o[e] = valid ? a[e] / (1.f + __expf(-g[e])) : 0.f;
+      v = Tr<ST>::pack(o);
+    }
+    *reinterpret_cast<u32x4*>(win + (size_t)r * p.D + c) = v;
+  }
+  __syncthreads();
+  // the next cache: the window's last R rows (convolution.py:46)
+  for (int i = threadIdx.x; i < R * nchunk; i += blockDim.x) {
+    const int r = i / nchunk, c = (i - r * nchunk) * VEC;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(win + (size_t)(p.T + r) * p.D + c);
+    if constexpr (STREAM)
+      st16_stream(crow0 + (int64_t)r * p.D + c, v);
+    else
+      st16(crow0 + (int64_t)r * p.D + c, v);
+  }
+
+  // 2. the lane's taps, bias and LayerNorm parameters
+  float w[VEC][K];
+  {
+    const ST* wp = p.w + (int64_t)c0 * K;
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      float f[VEC];
+      Tr<ST>::unpack(ld16(wp + i * VEC), f);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) w[(i * VEC + e) / K][(i * VEC + e) % K] = f[e];
+    }
+  }
+  float bias[VEC], lw[VEC], lb[VEC];
+  if (p.bias) {
+    Tr<ST>::unpack(ld16(p.bias + c0), bias);
+  } else {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) bias[e] = 0.f;
+  }
+  Tr<ST>::unpack(ld16(p.lnw + c0), lw);
+  Tr<ST>::unpack(ld16(p.lnb + c0), lb);
+  const float inv_d = 1.f / (float)p.D;
+  // the group's sum of a value over its waves, in wave order, in every lane
+  auto gsum = [&](float v) {
+    v = group_sum<64>(v);
+    if (nw == 1) return v;
+    if ((gt & 63) == 0) red[gwave] = v;
+    __syncthreads();
+    float s = 0.f;
+    for (int i = 0; i < nw; ++i) s += red[i];
+    __syncthreads();  // `red` is rewritten by the next call
+    return s;
+  };
+
+  const int iters = (p.T + FG - 1) / FG;
+  for (int it = 0; it < iters; ++it) {
+    const int t = fg + it * FG;
+    const bool act = t < p.T && own;
+    // causal depthwise conv: output t sees window rows t .. t + R
+    float y[VEC];
+    float s = 0.f;
+    if (act) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) y[e] = bias[e];
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        float x[VEC];
+        Tr<ST>::unpack(*reinterpret_cast<const u32x4*>(win + (size_t)(t + k) * p.D + c0), x);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) y[e] = fmaf(w[e][k], x[e], y[e]);
+      }
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) s += y[e];
+    }
+    // LayerNorm over d_model (convolution.py:156), two-pass mean / variance
+    const float mean = gsum(act ? s : 0.f) * inv_d;
+    float q = 0.f;
+    if (act) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float d = y[e] - mean;
+        q = fmaf(d, d, q);
+      }
+    }
+    const float var = gsum(act ? q : 0.f) * inv_d;
+    const float rstd = rsqrtf(var + p.eps);
+    if (act) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float z = fmaf((y[e] - mean) * rstd, lw[e], lb[e]);
+        y[e] = z / (1.f + __expf(-z));  // SiLU (convolution.py:157)
+      }
+      st16(p.out + b * p.o_sb + t * p.o_st + c0, Tr<ST>::pack(y));
+    }
+  }
+}
+
 namespace {
 
 // a step's conv caches (every layer's rows of the batch) above this share of
 // the 256 MB last-level cache take the streaming policy
 constexpr int64_t kConvStreamingBytes = 192ll << 20;
+// chunks of at least this many frames take the frames-in-parallel kernel when
+// the stream's window fits its LDS budget and the frame-by-frame kernel would
+// have fewer than kConvChunkWavesPerCu waves a CU (measured crossover at 14
+// frames: about 700 streams at d_model 1024 bf16, 1,500 at 512 fp16; past it
+// the frame-by-frame kernel's many streams hide its per-frame latency better)
+constexpr int kConvChunkMinT = 3;
+constexpr size_t kConvChunkLds = 64 * 1024;
+constexpr int kConvChunkWavesPerCu = 6;
 
 template <typename ST, int K>
 int launch_conv(const ConvK<ST>& k, int batch, hipStream_t s) {
@@ -187,6 +347,19 @@ int launch_conv(const ConvK<ST>& k, int batch, hipStream_t s) {
   const int nchunk = k.D / VEC;
   const int nw = (nchunk + 63) / 64;
   const int64_t cache_bytes = (int64_t)batch * k.num_layers * (K - 1) * k.D * (int64_t)sizeof(ST);
+  const size_t win_bytes = (size_t)(K - 1 + k.T) * k.D * sizeof(ST);
+  if (k.T >= kConvChunkMinT && win_bytes + kConvMaxWaves * sizeof(float) <= kConvChunkLds &&
+      (int64_t)batch * nw < (int64_t)kConvChunkWavesPerCu * cu_count()) {
+    // as many groups of nw waves as the frames and the workgroup's waves allow
+    const int fgroups = std::min(k.T, kConvMaxWaves / nw);
+    const size_t lds = win_bytes + (size_t)fgroups * nw * sizeof(float);
+    const dim3 grid((unsigned)batch), block(64u * nw * fgroups);
+    if (cache_bytes > kConvStreamingBytes)
+      hipLaunchKernelGGL((conv_chunk_kernel<ST, K, true>), grid, block, lds, s, k, fgroups);
+    else
+      hipLaunchKernelGGL((conv_chunk_kernel<ST, K, false>), grid, block, lds, s, k, fgroups);
+    return check_launch("pk_conv_step");
+  }
   if (cache_bytes > kConvStreamingBytes)
     hipLaunchKernelGGL((conv_step_kernel<ST, K, true>), dim3((unsigned)batch), dim3(64u * nw), 0, s, k);
   else

@@ -192,14 +192,16 @@ def test_module_in_place_and_tensor_state_agree(cuda, dt):
     assert tuple(a.conv.shape) == (N, Ly, D, K - 1)
 
 
-def test_streaming_policy_is_bit_exact(cuda):
+@pytest.mark.parametrize("B,L,D,T,dt,blk", [(2048, 13, 512, 2, torch.float16, 256), (600, 24, 1024, 14, torch.bfloat16, 64)],
+                         ids=["frame-by-frame", "frames-in-parallel"])
+def test_streaming_policy_is_bit_exact(cuda, B, L, D, T, dt, blk):
     """A batch whose conv caches over all layers pass the host's 192 MiB
     streaming threshold (2048 streams x 13 layers x 8 rows x 512 x 2 bytes =
-    218 MB) runs with the streaming cache policy; the same streams in blocks
-    of 256 (27 MB) run with the cached one.  Outputs and updated caches must
-    agree bit for bit."""
-    B, L, D, K, T, layer = 2048, 13, 512, 9, 2, 5
-    dt = torch.float16
+    218 MB at 2 frames; 600 x 24 x 8 x 1024 x 2 = 236 MB at 14 frames, where
+    both batches take the frames-in-parallel kernel) runs with the streaming
+    cache policy; the same streams in blocks (27 MB, 25 MB) run with the
+    cached one.  Outputs and updated caches must agree bit for bit."""
+    K, layer = 9, 5
     w, _, lw, lb = _params(D, K, dt, 11, False)
     wd, lwd, lbd = w.to(cuda), lw.to(cuda), lb.to(cuda)
     g = torch.Generator().manual_seed(12)
@@ -208,9 +210,49 @@ def test_streaming_policy_is_bit_exact(cuda):
     c2 = c1.clone()
     y1 = ops.conv_step(h, c1, wd, lwd, lbd, layer=layer)
     y2 = torch.empty_like(y1)
-    for b0 in range(0, B, 256):
-        slots = torch.arange(b0, b0 + 256, dtype=torch.int32, device=cuda)
-        y2[b0 : b0 + 256] = ops.conv_step(h[b0 : b0 + 256], c2, wd, lwd, lbd, layer=layer, slots=slots)
+    for b0 in range(0, B, blk):
+        b1 = min(B, b0 + blk)
+        slots = torch.arange(b0, b1, dtype=torch.int32, device=cuda)
+        y2[b0:b1] = ops.conv_step(h[b0:b1], c2, wd, lwd, lbd, layer=layer, slots=slots)
     torch.cuda.synchronize()
     assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
     assert torch.equal(c1.view(torch.int16), c2.view(torch.int16))
+
+
+def _bits(t):
+    return t.view(torch.int32) if t.element_size() == 4 else t.view(torch.int16)
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("D,T,K", [(1024, 14, 9), (520, 7, 9), (136, 5, 5), (24, 3, 9), (512, 14, 3)])
+def test_chunk_form_equals_two_frame_steps(cuda, dt, D, T, K):
+    """A chunk of 3 or more frames goes to the frames-in-parallel kernel (the
+    window staged in LDS, groups of waves over the frames) at batches under
+    about six of the other kernel's waves a CU; chunks of 1-2 frames to the
+    frame-by-frame one.  The same frames fed as one T-frame step
+    and as steps of 2 (and a last 1) through the cache give the same outputs
+    and the same final cache, bit for bit: every sum is the same in the same
+    order, for d_model a power of two or not (where 1/d_model is inexact and a
+    fused and an unfused rounding of the LayerNorm statistics would differ)."""
+    if dt == torch.float32 and D % 4 or dt != torch.float32 and D % 8:
+        pytest.skip("d_model not a whole number of 16-byte chunks")
+    print(f"\n[conv chunk form] {dt} D={D} T={T} K={K}", flush=True)
+    S, Ly, B, layer = 9, 2, 7, 1
+    rng = np.random.default_rng(D + T + K)
+    slots = torch.from_numpy(rng.permutation(S)[:B].astype(np.int32)).to(cuda)
+    w, b, lw, lb = (None if x is None else x.to(cuda) for x in _params(D, K, dt, seed=D * 3 + K, bias=True))
+    g = torch.Generator().manual_seed(T * 5 + K)
+    c1 = torch.randn(S, Ly, K - 1, D, generator=g).to(dt).to(cuda)
+    c2 = c1.clone()
+    h = torch.randn(B, T, 2 * D, generator=g).to(dt).to(cuda)
+    pad = torch.from_numpy(rng.random((B, T)) < 0.25).to(cuda)
+    y1 = ops.conv_step(h, c1, w, lw, lb, layer=layer, slots=slots, pad_mask=pad, dw_bias=b)
+    parts = []
+    for t0 in range(0, T, 2):
+        t1 = min(T, t0 + 2)
+        parts.append(ops.conv_step(h[:, t0:t1].contiguous(), c2, w, lw, lb, layer=layer, slots=slots,
+                                   pad_mask=pad[:, t0:t1].contiguous(), dw_bias=b))
+    torch.cuda.synchronize()
+    y2 = torch.cat(parts, dim=1)
+    assert torch.equal(_bits(y1), _bits(y2)), f"outputs differ at {int((_bits(y1) != _bits(y2)).sum())} values"
+    assert torch.equal(_bits(c1), _bits(c2)), "caches differ"
