@@ -675,7 +675,8 @@ def encoder_bench(args, device) -> dict:
         },
         "conv_step": {
             "kernel": ("conv_chunk_kernel (GLU, pad mask, causal depthwise conv with cache, LayerNorm, SiLU; "
-                       "the chunk's frames in parallel)" if T >= 3 and B * (-(-D // 512)) < 6 * 256 else
+                       "the chunk's frames in parallel)" if T >= 3 and B * (-(-D // 512)) <
+                       6 * torch.cuda.get_device_properties(device).multi_processor_count else
                        "conv_step_kernel (GLU, pad mask, causal depthwise conv with cache, LayerNorm, SiLU)"),
             "avg_kernel_us": round(conv_us, 3),
             "bytes_per_launch": conv_bytes,
