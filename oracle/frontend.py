@@ -119,17 +119,22 @@ def philox4x32_10(ctr, key):
 
 
 def dither_normal(seed: int, noise_id: int, idx) -> np.ndarray:
-    """N(0, 1) for global sample indices ``idx`` of one stream: Philox counter
-    (idx lo, idx hi, noise_id, 0), key (seed lo, seed hi); Box-Muller on the
-    first two words, u1 = (r0 + 1) 2^-32 in (0, 1], u2 = r1 2^-32."""
+    """N(0, 1) for global sample indices ``idx`` of one stream.  Samples 4j ..
+    4j + 3 share one Philox draw: counter (j lo, j hi, noise_id, 0), key (seed
+    lo, seed hi).  Box-Muller on the word pairs (r0, r1) for samples 4j (cos)
+    and 4j + 1 (sin) and (r2, r3) for 4j + 2 (cos) and 4j + 3 (sin), with
+    u1 = (ra + 1) 2^-32 in (0, 1] and u2 = rb 2^-32."""
     idx = np.asarray(idx, dtype=np.int64)
-    r0, r1, _, _ = philox4x32_10(
-        (idx & _U32, idx >> 32, np.full_like(idx, noise_id & _U32), np.zeros_like(idx)),
+    j, q = idx >> 2, idx & 3
+    r0, r1, r2, r3 = philox4x32_10(
+        (j & _U32, j >> 32, np.full_like(j, noise_id & _U32), np.zeros_like(j)),
         (seed & _U32, (seed >> 32) & _U32),
     )
-    u1 = (r0.astype(np.float64) + 1.0) * 2.0**-32
-    u2 = r1.astype(np.float64) * 2.0**-32
-    return np.sqrt(-2.0 * np.log(u1)) * np.cos(2.0 * np.pi * u2)
+    ra = np.where(q < 2, r0, r2).astype(np.float64)
+    rb = np.where(q < 2, r1, r3).astype(np.float64)
+    radius = np.sqrt(-2.0 * np.log((ra + 1.0) * 2.0**-32))
+    angle = 2.0 * np.pi * rb * 2.0**-32
+    return radius * np.where(q % 2 == 0, np.cos(angle), np.sin(angle))
 
 
 # ---------------------------------------------------------------------------

@@ -75,14 +75,20 @@ __device__ static inline void philox4x32_10(uint32_t& c0, uint32_t& c1, uint32_t
   }
 }
 
-// Standard normal for global sample i of one stream: Box-Muller on the first two
-// Philox words, u1 = (r0 + 1) 2^-32, u2 = r1 2^-32.  v_cos_f32 takes revolutions.
-__device__ static inline float dither_normal(int64_t i, uint32_t noise_id, uint32_t k0, uint32_t k1) {
-  uint32_t c0 = (uint32_t)i, c1 = (uint32_t)((uint64_t)i >> 32), c2 = noise_id, c3 = 0u;
+// Standard normals for global samples 4j .. 4j + 3 of one stream, from one
+// Philox draw (counter j): Box-Muller on the word pairs (r0, r1) -> cos, sin
+// for 4j, 4j + 1 and (r2, r3) -> cos, sin for 4j + 2, 4j + 3, with
+// u1 = (ra + 1) 2^-32 and u2 = rb 2^-32.  v_cos_f32 / v_sin_f32 take revolutions.
+__device__ static inline void dither_normal4(int64_t j, uint32_t noise_id, uint32_t k0, uint32_t k1, float* z) {
+  uint32_t c0 = (uint32_t)j, c1 = (uint32_t)((uint64_t)j >> 32), c2 = noise_id, c3 = 0u;
   philox4x32_10(c0, c1, c2, c3, k0, k1);
-  const float u1 = ((float)c0 + 1.0f) * 2.3283064365386963e-10f;
-  const float u2 = (float)c1 * 2.3283064365386963e-10f;
-  return sqrtf(-2.0f * __logf(u1)) * __builtin_amdgcn_cosf(u2);
+  const float ra = sqrtf(-2.0f * __logf(((float)c0 + 1.0f) * 2.3283064365386963e-10f));
+  const float rb = sqrtf(-2.0f * __logf(((float)c2 + 1.0f) * 2.3283064365386963e-10f));
+  const float va = (float)c1 * 2.3283064365386963e-10f, vb = (float)c3 * 2.3283064365386963e-10f;
+  z[0] = ra * __builtin_amdgcn_cosf(va);
+  z[1] = ra * __builtin_amdgcn_sinf(va);
+  z[2] = rb * __builtin_amdgcn_cosf(vb);
+  z[3] = rb * __builtin_amdgcn_sinf(vb);
 }
 
 __device__ static inline float2 cmul(float2 a, float2 b) {
@@ -169,26 +175,33 @@ __global__ void __launch_bounds__(64 * kFeWaves) fe_kernel(const FeK p) {
   // staging, one global round trip per phase: every load of a phase is issued
   // into registers before any of them is stored
   __shared__ int2 rng_s[kMaxMels];
-  constexpr int kXsPer = (kSpanMax + 64 * kFeWaves - 1) / (64 * kFeWaves);
+  // the span in groups of 4 consecutive global samples (one dither draw a
+  // group): group q holds samples 4 (g0 + q) .. + 3, g0 = floor(span0 / 4)
+  constexpr int kGroups = (kSpanMax + 3) / 4 + 1;
+  constexpr int kXsPer = (kGroups + 64 * kFeWaves - 1) / (64 * kFeWaves);
   constexpr int kFbPer = kMaxMels * kBand / (64 * kFeWaves);
   constexpr int kWinPer = kMaxWin / (64 * kFeWaves);
-  float xr[kXsPer], wr[kWinPer];
+  float xr[kXsPer][4], wr[kWinPer];
   const int mc = min(tid, p.n_mels - 1);
   const int2 rr = make_int2(p.fb_range[2 * mc], p.fb_range[2 * mc + 1]);
 #pragma unroll
   for (int u = 0; u < kWinPer; ++u) wr[u] = p.window[min(tid + u * 64 * kFeWaves, p.win - 1)];
-  // raw sample i from this call's input or the ring (0 outside [0, total)):
+  // raw samples from this call's input or the ring (0 outside [0, total)):
   // unconditional loads from clamped addresses
+  const int64_t g0 = span0 >> 2;  // floor, span0 may be negative
 #pragma unroll
   for (int u = 0; u < kXsPer; ++u) {
-    const int i = tid + u * 64 * kFeWaves;
-    const int64_t g = span0 + i;
-    const bool ok = i < span && g >= 0 && g < total;
-    const bool fresh = g >= s.sample_base;
-    const float xn = sample_in(ok && fresh ? g - s.sample_base : 0);
-    const float xo = ring[ok && !fresh ? (g & rmask) : 0];
-    const float x = fresh ? xn : xo;
-    xr[u] = ok ? x : 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t g = 4 * (g0 + tid + u * 64 * kFeWaves) + e;
+      const int64_t i = g - span0;
+      const bool ok = i >= 0 && i < span && g >= 0 && g < total;
+      const bool fresh = g >= s.sample_base;
+      const float xn = sample_in(ok && fresh ? g - s.sample_base : 0);
+      const float xo = ring[ok && !fresh ? (g & rmask) : 0];
+      const float x = fresh ? xn : xo;
+      xr[u][e] = ok ? x : 0.f;
+    }
   }
   if (tid < p.n_mels) rng_s[tid] = make_int2(max(rr.x, 0), min(rr.y, kBins));
 #pragma unroll
@@ -198,12 +211,17 @@ __global__ void __launch_bounds__(64 * kFeWaves) fe_kernel(const FeK p) {
   }
 #pragma unroll
   for (int u = 0; u < kXsPer; ++u) {
-    const int i = tid + u * 64 * kFeWaves;
-    const int64_t g = span0 + i;
-    if (i < span) {  // the span is the frames' reach, usually well under the staging's size
-      float x = xr[u];
-      if (p.dither != 0.f && g >= 0 && g < total) x += p.dither * dither_normal(g, s.noise_id, p.seed_lo, p.seed_hi);
-      xs[i] = x;
+    const int64_t j = g0 + tid + u * 64 * kFeWaves;
+    const int64_t i0 = 4 * j - span0;  // xs index of the group's first sample
+    // the span is the frames' reach, usually well under the staging's size
+    if (i0 + 3 >= 0 && i0 < span) {
+      float z[4] = {0.f, 0.f, 0.f, 0.f};
+      if (p.dither != 0.f && 4 * j + 3 >= 0 && 4 * j < total) dither_normal4(j, s.noise_id, p.seed_lo, p.seed_hi, z);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t i = i0 + e, g = 4 * j + e;
+        if (i >= 0 && i < span) xs[i] = g >= 0 && g < total ? xr[u][e] + p.dither * z[e] : xr[u][e];
+      }
     }
   }
   __syncthreads();

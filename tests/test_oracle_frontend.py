@@ -43,6 +43,18 @@ def test_dither_is_standard_normal_and_keyed():
     assert np.array_equal(fe.dither_normal(7, 3, [5, 100_000]), z[[5, 100_000]])
     assert not np.allclose(fe.dither_normal(7, 4, np.arange(16)), z[:16])
     assert not np.allclose(fe.dither_normal(8, 3, np.arange(16)), z[:16])
+    # Box-Muller pairs: samples 4j, 4j+1 (and 4j+2, 4j+3) are the cos and sin of
+    # one angle on one radius, the radius from the Philox draw of counter j
+    # (pinned by the known answers above), so their squares sum to -2 ln u1;
+    # within and across pairs the samples are uncorrelated
+    j = np.arange(50_000)
+    r0, _, r2, _ = fe.philox4x32_10((j, np.zeros_like(j), np.full_like(j, 3), np.zeros_like(j)), (7, 0))
+    zz = z.reshape(-1, 4)
+    for k, r in ((0, r0), (2, r2)):
+        rad2 = -2.0 * np.log((r.astype(np.float64) + 1.0) * 2.0**-32)
+        np.testing.assert_allclose(zz[:, k] ** 2 + zz[:, k + 1] ** 2, rad2, rtol=1e-12, atol=1e-12)
+    for a, b in ((0, 1), (1, 2), (2, 3), (0, 2)):
+        assert abs(np.corrcoef(zz[:, a], zz[:, b])[0, 1]) < 0.02
 
 
 @pytest.mark.parametrize("n_mels,fmax", [(80, None), (128, None), (64, 6000.0)])
