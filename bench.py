@@ -16,7 +16,8 @@ tensors resident in HBM before timing.
 The default run then adds, each under its own key with its roofline and CPU
 baseline: the large model's own 14-frame chunk (``large_t14``), the small shape
 at 64 streams (``small_64streams``), the fragmentation stress at 1024 streams
-(``frag_1024streams``) and the end-to-end pcm16 -> tokens step at 128 streams
+(``frag_1024streams``), the fp32 plumbing case of 4 streams and one layer
+(``plumbing_4streams``) and the end-to-end pcm16 -> tokens step at 128 streams
 of the small model (``e2e_pcm16_128streams``) and of the large one (128 mels,
 24 layers, 14 frames a step, 2-layer predictor: ``e2e_pcm16_large_128streams``);
 and, under ``concurrent_streams.measured_max``, a timed run at the largest batch
@@ -1016,6 +1017,7 @@ def main() -> int:
             ("large_t14", lambda: paged_bench("large-t14", device, args, 100, 10, 30, extra_s)),
             ("small_64streams", lambda: paged_bench("small", device, args, 100, 10, 30, extra_s)),
             ("frag_1024streams", lambda: paged_bench("frag", device, args, 100, 10, 30, extra_s)),
+            ("plumbing_4streams", lambda: paged_bench("plumbing", device, args, 100, 10, 30, min(extra_s, 4.0))),
         ]
         for key, fn in extras:
             torch.cuda.reset_peak_memory_stats(device)
