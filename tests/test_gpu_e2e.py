@@ -14,8 +14,8 @@ Workloads:
   layers, conv kernel 9, left context 70, 2 frames a step, fp16, 45 steps (the
   window fills after 35, pages are evicted from then on);
 * large FastConformer shape at its own chunking: 128 mels, d_model 1024,
-  8 heads x 128, 6 layers, chunk of 14 encoder frames (att_context (70, 13)),
-  bf16, 4 streams, 9 steps (eviction from step 6).
+  8 heads x 128, all 24 layers, chunk of 14 encoder frames (att_context
+  (70, 13)), bf16, 4 streams, 9 steps (eviction from step 6).
 
 Bar (stated per dtype in TOL): max |got - ref| over every output element, step
 and stream, and the RMS of the error over a step.  The outputs leave the final
@@ -25,12 +25,13 @@ or bf16 (2^-8) between operations.  Through the front end, the residual adds,
 the five LayerNorms, the 2 feed-forward blocks and the attention and conv
 branches of each layer, the roundings add up to 15-17 u at the worst element
 and 2-4 u in RMS: measured fp16 (17 layers) max 8.35e-3 (17 u), RMS 1.84e-3;
-bf16 (6 layers) max 5.65e-2 (14 u), RMS 6.6e-3.  The bars leave about a factor
-of two: fp16 max 1.6e-2 and RMS 3.5e-3, bf16 max 1e-1 and RMS 1.5e-2.  The GPU
-run compared with an oracle carrying a plausible mistake in the composition
-(relative positions reversed: max 0.42 / 0.32; conv taps shifted by one frame:
-1.14 / 0.48; a feed-forward branch without its 0.5: 0.26 / 0.23, fp16 / bf16)
-exceeds them by far, so they catch those.  A mistake in a bias term (pos_bias_v
+bf16 (24 layers) max 4.57e-2 (12 u), RMS 8.5e-3 (at 6 layers 5.65e-2 and
+6.6e-3).  The bars leave about a factor of two: fp16 max 1.6e-2 and RMS
+3.5e-3, bf16 max 1e-1 and RMS 1.5e-2.  The GPU run compared with an oracle
+carrying a plausible mistake in the composition (relative positions reversed:
+max 0.42 / 0.47; conv taps shifted by one frame: 1.14 / 0.39; a feed-forward
+branch without its 0.5: 0.26 / 0.24, fp16 / bf16) exceeds them by far, so they
+catch those.  A mistake in a bias term (pos_bias_v
 dropped) moves the stack's outputs by less than the dtype's rounding (fp16 max
 1.04e-2 against 8.35e-3 clean; bf16 unchanged): the kernel-level bars catch it.
 """
@@ -52,7 +53,7 @@ pytestmark = pytest.mark.gpu
 CASES = {
     # D, H, layers, K, left, right, n_mels, C, dtype, streams, steps, first chunk, next chunks, ring, mel rows
     "small_fp16": (512, 8, 17, 9, 70, 1, 80, 256, torch.float16, 4, 45, 1440, 2560, 8192, 64),
-    "large_bf16_t14": (1024, 8, 6, 9, 70, 13, 128, 256, torch.bfloat16, 4, 9, 16800, 17920, 32768, 256),
+    "large_bf16_t14": (1024, 8, 24, 9, 70, 13, 128, 256, torch.bfloat16, 4, 9, 16800, 17920, 32768, 256),
 }
 TOL = {torch.float16: (1.6e-2, 3.5e-3), torch.bfloat16: (1e-1, 1.5e-2)}  # (max abs, rms)
 
