@@ -529,7 +529,7 @@ int pk_rnnt_greedy_step(const pk_rnnt_args* args, void* stream);
  * serving loops that forbid hipMalloc).  args->workspace must be NULL; every
  * other argument is pk_rnnt_greedy_step's.  A step whose
  * pk_rnnt_workspace_bytes(...) exceeds the array is rejected with
- * PK_ERR_UNSUPPORTED (at fp16 with one 640-unit LSTM layer, about 6,000
+ * PK_ERR_UNSUPPORTED (at fp16 with one 640-unit LSTM layer, about 5,800
  * streams).  The kernels initialise every scratch word they read, so nothing
  * needs clearing between calls.  Every call on one GPU shares that GPU's
  * array: calls that overlap on one GPU (different streams, different threads)

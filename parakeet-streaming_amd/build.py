@@ -19,6 +19,7 @@ REPO = HERE.parent
 CSRC = HERE / "csrc"
 INCLUDE = REPO / "include"
 BUILD_DIR = HERE / "_build"
+CHECKS = REPO / "tests" / "native"
 LIB_PATH = HERE / "parakeet_amd" / "libparakeet_paged.so"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -78,7 +79,20 @@ def build(verbose: bool = False) -> Path:
     tmp = LIB_PATH.with_suffix(".so.tmp")
     _run([HIPCC, "-shared", f"--offload-arch={ARCH}", "-fPIC", *map(str, objs), "-o", str(tmp)], verbose)
     os.replace(tmp, LIB_PATH)
+    build_checks(verbose)
     return LIB_PATH
+
+
+def build_checks(verbose: bool = False) -> list[Path]:
+    """The stand-alone GPU check programs of tests/native (run by the GPU tests)."""
+    out_dir = CHECKS / "_build"
+    out_dir.mkdir(parents=True, exist_ok=True)
+    built = []
+    for src in sorted(CHECKS.glob("*.hip")):
+        exe = out_dir / src.stem
+        _run([HIPCC, *HIP_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-x", "hip", str(src), "-o", str(exe)], verbose)
+        built.append(exe)
+    return built
 
 
 def clean() -> None:

@@ -6,7 +6,7 @@
 // s < max_symbols, 2 + layers launches with no host synchronisation:
 //   joint_kernel     hid = relu(enc_proj[b, t] + pred_proj[slot]) (rounded to the
 //                    storage type), logits = W_out hid + b_out (rounded), and the
-//                    first maximum over a tile of 128 vocabulary rows: MFMA with
+//                    first maximum over a tile of 64 vocabulary rows: MFMA with
 //                    the weight rows as A and the 16 streams as B columns.
 //                    Workgroups whose streams are all done for the frame return
 //                    at once -- the reference's "every decision blank" break.
@@ -20,8 +20,9 @@
 //                    Every workgroup reads all of a stream's h, so h' goes to a
 //                    per-batch scratch; c is owned by one thread per element.
 //   pred_kernel      pred_proj[slot] = W_pred h'_top + b_pred for the updated
-//                    streams, and h' copied from the scratch into the slot state
-//                    (this launch runs after every read of the old h).
+//                    streams, and h' copied from the scratch into the slot state,
+//                    a share by every workgroup (this launch runs after every
+//                    read of the old h).
 // In compact mode (large batches) a select_kernel launch after the joint takes
 // every stream's decision, records it and lists the streams that emitted a
 // token; the LSTM and pred launches, and the next symbol's joint, then tile over
@@ -66,7 +67,12 @@ struct MmaR<float> {
   }
 };
 
-constexpr int kVT = 128;      // vocabulary rows per joint workgroup
+// Workgroup sizes of the joint and pred launches: more, smaller workgroups
+// than one per 128 rows, so that a launch spreads its weight reads over more
+// CUs (at 128 streams the joint then takes 136 workgroups, the pred 160).
+constexpr int kVT = 64;                // vocabulary rows per joint workgroup
+constexpr int kJointWaves = kVT / 16;  // a wave per 16 rows
+constexpr int kPredWaves = 2;          // pred_proj columns per workgroup: 16 a wave
 constexpr int kCompactMinBatch = 1024;  // compact mode by default from this batch
 constexpr int kMaxDim = 1024;  // hidden / joint sizes held in LDS
 // per-stream words of the step workspace: flag, token, emitted count, pad
@@ -109,11 +115,6 @@ __device__ static inline bool stream_ok(const DecK& p, int b) {
   return b < p.batch && (uint32_t)p.slots[b] < (uint32_t)p.num_slots;
 }
 
-// A stream decides at (t, s) while t is one of its frames and it has not yet
-// decided blank in frame t (word 0 of its workspace: 1 = blank seen).
-__device__ static inline bool active_at(const DecK& p, int b, const int32_t* w) {
-  return stream_ok(p, b) && p.t < p.lengths[b] && (p.s == 0 || w[0] == 0);
-}
 
 // Entry e of a launch's stream set: the batch itself (list < 0), or list
 // `list` of the streams that emitted a token; -1 past the set.
@@ -125,11 +126,12 @@ __device__ static inline int listed_stream(const DecK& p, int list, int e) {
   return (uint32_t)b < (uint32_t)p.batch ? b : -1;
 }
 
-// Weight chunks loaded ahead of their MFMAs: 20 k-steps of a 16-bit row (10 of
-// fp32) per round trip, within the registers a decode wave has to spare.
+// Weight chunks loaded ahead of their MFMAs: 10 k-steps per round trip.  A
+// workgroup of 4-8 waves then has 40-80 KB of weights in flight; with twice
+// that in flight a round trip took about four times as long.
 template <typename ST>
 struct KChunk {
-  static constexpr int CH = sizeof(ST) == 4 ? 10 : 20;
+  static constexpr int CH = 10;
 };
 
 // The wave's 16 weight rows (A, from global memory) against 16 columns held in
@@ -177,84 +179,123 @@ __device__ static inline f32x4_t mma_rows(const u32x4 (&w0)[KChunk<ST>::CH], con
   return d;
 }
 
-// ---------------------------------------------------------------------------
+// The same with the first two chunks already loaded (w1: k-steps CH .. 2 CH).
 template <typename ST>
-__global__ void __launch_bounds__(512) joint_kernel(const DecK p) {
-  constexpr int VEC = 16 / sizeof(ST);
+__device__ static inline f32x4_t mma_rows2(const u32x4 (&w0)[KChunk<ST>::CH], const u32x4 (&w1)[KChunk<ST>::CH],
+                                           const ST* wa, const ST* wb, int ka, int nk, const ST* col, int lg,
+                                           f32x4_t d) {
+  constexpr int CH = KChunk<ST>::CH;
+  d = mma_chunk<ST>(w0, col, 0, nk, lg, d);
+  d = mma_chunk<ST>(w1, col, CH, nk, lg, d);
+  for (int k0 = 2 * CH; k0 < nk; k0 += CH) {
+    u32x4 w[CH];
+    load_chunk<ST>(w, wa, wb, ka, nk, k0, lg);
+    __builtin_amdgcn_sched_barrier(0);
+    d = mma_chunk<ST>(w, col, k0, nk, lg, d);
+  }
+  return d;
+}
+
+// ---------------------------------------------------------------------------
+// The words a stream's activity test reads, loaded in one round (b < batch).
+struct StreamWords {
+  int32_t slot, len, blank_seen;
+};
+__device__ static inline StreamWords stream_words(const DecK& p, int b) {
+  return StreamWords{p.slots[b], p.lengths[b], ws_of(p, b)[0]};
+}
+// A stream decides at (t, s) while its slot is valid, t is one of its frames
+// and it has not yet decided blank in frame t (word 0 of its workspace: 1 =
+// blank seen).
+__device__ static inline bool active_from(const DecK& p, const StreamWords& w) {
+  return (uint32_t)w.slot < (uint32_t)p.num_slots && p.t < w.len && (p.s == 0 || w.blank_seen == 0);
+}
+
+template <typename ST>
+__global__ void __launch_bounds__(kJointWaves * 64) joint_kernel(const DecK p) {
+  constexpr int VEC = 16 / sizeof(ST), W = kJointWaves;
+  constexpr int CPT = kMaxDim / VEC / 16;  // a thread's 16-byte chunks of a hid row, at most
+  static_assert(W * 64 == 16 * 16, "hid staging: 16 threads a stream");
   __shared__ __align__(16) ST hid[16][kMaxDim + 8];
-  __shared__ float bv[8][16];
-  __shared__ int bi[8][16];
-  __shared__ int32_t act_s[16], slot_s[16], bid_s[16];
+  __shared__ float bv[W][16];
+  __shared__ int bi[W][16];
+  __shared__ int32_t bid_s[16];
   const int vt = blockIdx.x, b0 = blockIdx.y * 16;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
   // this iteration's list starts empty (its other half, read below, is the
   // previous iteration's)
   if (p.compact && vt == 0 && blockIdx.y == 0 && tid == 0) p.acount[p.it & 1] = 0;
   // the tile's streams: the batch, or after a frame's first symbol (compact
-  // mode) the streams that emitted a token in the previous iteration
+  // mode) the streams that emitted a token in the previous iteration; a
+  // workgroup past that list loads nothing
   const int list = p.compact && p.s > 0 ? (p.it - 1) & 1 : -1;
-  if (tid < 16) {
-    const int b = listed_stream(p, list, b0 + tid);
-    const bool a = b >= 0 && active_at(p, b, ws_of(p, b));
-    act_s[tid] = a;
-    slot_s[tid] = a ? p.slots[b] : 0;
-    bid_s[tid] = b;
-  }
-  __syncthreads();
-  bool any = false;
-  for (int k = 0; k < 16; ++k) any |= act_s[k] != 0;
-  if (!any) return;  // uniform: every stream of the tile is done for this frame
-  // the weight rows' first chunk and the biases of the lane's 4 rows: loads
-  // that depend on nothing, issued ahead of the staging loads
+  if (list >= 0 && b0 >= min(p.acount[list], p.batch)) return;
+  // lane c of every 16-lane group reads entry c's stream words, so each wave
+  // holds the activity of all 16 entries: a tile with none deciding returns
+  // before any weight or row load, with no barrier (every wave sees the same
+  // words).  Thread -> (stream entry k, chunks c + 16 j of its hid row); entry
+  // k's words come from lane k of the thread's group.
+  const int k = tid >> 4, c = tid & 15;
+  const int bc = listed_stream(p, list, b0 + c);
+  StreamWords swc{0, 0, 1};
+  if (bc >= 0) swc = stream_words(p, bc);
+  const bool ac = bc >= 0 && active_from(p, swc);
+  if (__ballot(ac) == 0) return;
+  const int src = (lane & 48) | k;
+  const int b = __shfl(bc, src);
+  const bool act = __shfl((int)ac, src) != 0;
+  const int sk = __shfl(swc.slot, src);  // every lane takes part in the shuffles
+  const int slot = act ? sk : 0;
+  // the weight rows' first chunk and the biases of the lane's 4 rows, then the
+  // hid row of the entry (zero for a stream not deciding: every load from an
+  // address valid for any entry, then masked), the second weight chunk behind
   const int J = p.J, nch = J / VEC, ks = J / (4 * VEC);
-  const int r = vt * kVT + wave * 16 + lr;
-  const ST* wrow = (const ST*)p.w_out + (int64_t)min(r, p.V1 - 1) * J;
-  u32x4 w0[KChunk<ST>::CH];
+  const int r0 = vt * kVT + wave * 16;
+  const ST* wrow = (const ST*)p.w_out + (int64_t)min(r0 + lr, p.V1 - 1) * J;
+  u32x4 w0[KChunk<ST>::CH], w1[KChunk<ST>::CH];
   load_chunk<ST>(w0, wrow, wrow, ks, ks, 0, lg);
   float bias[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) bias[i] = from_st(((const ST*)p.b_out)[min(vt * kVT + wave * 16 + 4 * lg + i, p.V1 - 1)]);
-  __builtin_amdgcn_sched_barrier(0);
-  // hid for the 16 streams (zero for streams not deciding): every load is issued
-  // first, from an address that is valid for any stream, then masked
-  constexpr int IT = (16 * kMaxDim / VEC + 511) / 512;
-  u32x4 er[IT], qr[IT];
+  for (int i = 0; i < 4; ++i) bias[i] = from_st(((const ST*)p.b_out)[min(r0 + 4 * lg + i, p.V1 - 1)]);
+  const ST* er_src = (const ST*)p.enc + max(b, 0) * p.enc_sb + (int64_t)p.t * p.enc_st;
+  const ST* qr_src = (const ST*)p.pred_proj + (int64_t)slot * J;
+  u32x4 er[CPT], qr[CPT];
 #pragma unroll
-  for (int it = 0; it < IT; ++it) {
-    const int i = min(tid + it * 512, 16 * nch - 1);
-    const int k = i / nch, cc = (i - k * nch) * VEC;
-    const int b = max(bid_s[k], 0);
-    er[it] = ld16((const ST*)p.enc + b * p.enc_sb + (int64_t)p.t * p.enc_st + cc);
-    qr[it] = ld16((const ST*)p.pred_proj + (int64_t)slot_s[k] * J + cc);
+  for (int j = 0; j < CPT; ++j) {
+    if (16 * j < nch) {  // uniform
+      const int cc = min(c + 16 * j, nch - 1) * VEC;
+      er[j] = ld16(er_src + cc);
+      qr[j] = ld16(qr_src + cc);
+    }
   }
+  load_chunk<ST>(w1, wrow, wrow, ks, ks, KChunk<ST>::CH, lg);
+  if (c == 0) bid_s[k] = b;
 #pragma unroll
-  for (int it = 0; it < IT; ++it) {
-    const int i = tid + it * 512;
-    if (i < 16 * nch) {
-      const int k = i / nch, cc = (i - k * nch) * VEC;
+  for (int j = 0; j < CPT; ++j) {
+    if (c + 16 * j < nch) {
       float out[VEC];
-      if (act_s[k]) {
+      if (act) {
         float e[VEC], q[VEC];
-        Tr<ST>::unpack(er[it], e);
-        Tr<ST>::unpack(qr[it], q);
+        Tr<ST>::unpack(er[j], e);
+        Tr<ST>::unpack(qr[j], q);
 #pragma unroll
         for (int u = 0; u < VEC; ++u) out[u] = fmaxf(round_to<ST>(e[u] + q[u]), 0.f);
       } else {
 #pragma unroll
         for (int u = 0; u < VEC; ++u) out[u] = 0.f;
       }
-      *reinterpret_cast<u32x4*>(&hid[k][cc]) = Tr<ST>::pack(out);
+      *reinterpret_cast<u32x4*>(&hid[k][(c + 16 * j) * VEC]) = Tr<ST>::pack(out);
     }
   }
   __syncthreads();
-  // logits of rows vt*128 + 16*wave .. for the 16 streams
-  const f32x4_t d = mma_rows<ST>(w0, wrow, wrow, ks, ks, &hid[lr][0], lg, f32x4_t{0.f, 0.f, 0.f, 0.f});
+  // logits of rows r0 .. r0 + 15 for the 16 streams
+  const f32x4_t d = mma_rows2<ST>(w0, w1, wrow, wrow, ks, ks, &hid[lr][0], lg, f32x4_t{0.f, 0.f, 0.f, 0.f});
   // lane holds rows 4*lg + i (of the wave's 16) for stream lr
   float best = -INFINITY;
   int bidx = 0x7fffffff;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int row = vt * kVT + wave * 16 + 4 * lg + i;
+    const int row = r0 + 4 * lg + i;
     if (row < p.V1) {
       const float v = round_to<ST>(d[i] + bias[i]);
       if (v > best) {  // rows ascend: the first maximum wins ties
@@ -272,6 +313,14 @@ __global__ void __launch_bounds__(512) joint_kernel(const DecK p) {
       bidx = oi;
     }
   }
+  if (W == 1) {
+    if (lg == 0 && bid_s[lr] >= 0) {
+      int32_t* ws = ws_of(p, bid_s[lr]);
+      ws[kWsHead + 2 * vt] = __float_as_int(best);
+      ws[kWsHead + 2 * vt + 1] = bidx;
+    }
+    return;
+  }
   if (lg == 0) {
     bv[wave][lr] = best;
     bi[wave][lr] = bidx;
@@ -280,7 +329,7 @@ __global__ void __launch_bounds__(512) joint_kernel(const DecK p) {
   if (tid < 16 && bid_s[tid] >= 0) {
     float v = bv[0][tid];
     int ix = bi[0][tid];
-    for (int w = 1; w < 8; ++w)
+    for (int w = 1; w < W; ++w)
       if (bv[w][tid] > v || (bv[w][tid] == v && bi[w][tid] < ix)) {
         v = bv[w][tid];
         ix = bi[w][tid];
@@ -293,32 +342,47 @@ __global__ void __launch_bounds__(512) joint_kernel(const DecK p) {
 
 // ---------------------------------------------------------------------------
 // Stream b's decision at (t, s): the first maximum over the vocabulary tiles'
-// partial maxima; -1 when the stream is not deciding or decides blank.
+// partial maxima; -1 when the stream is not deciding or decides blank.  Taken
+// by the 16 lanes c = 0 .. 15 of an aligned lane group, every lane with the
+// same b (every lane gets the result): lane c reads tiles c, c + 16, ... and
+// the lanes combine.  The (value, index) pairs are ordered by value, then by
+// the lower index, a total order over the pairs the joint writes (never NaN),
+// so any combining order gives the sequential scan's first maximum.  The
+// stream words and the first 64 tiles are loaded in one round.
 // Workspace words: 0 = blank seen in the current frame, 1 = token that updates
 // the predictor this iteration (-1: none), 2 = tokens emitted this step.
-__device__ static inline int decide(const DecK& p, int b, bool* act_out) {
+__device__ static inline int decide16(const DecK& p, int b, int c, bool* act_out) {
   const int32_t* ws = ws_of(p, b);
-  const bool act = active_at(p, b, ws);
-  *act_out = act;
-  if (!act) return -1;
-  // tiles in ascending order; the (max, index) pairs of 8 tiles are loaded
-  // together ahead of their compares
-  float v = 0.f;
-  int ix = -1;
-  for (int k0 = 0; k0 < p.vtiles; k0 += 8) {
-    int2 m[8];
+  const StreamWords sw = stream_words(p, b);
+  float v = -INFINITY;
+  int ix = 0x7fffffff;
+  for (int k0 = 0; k0 < p.vtiles; k0 += 64) {
+    int2 m[4];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) m[u] = *reinterpret_cast<const int2*>(ws + kWsHead + 2 * min(k0 + u, p.vtiles - 1));
+    for (int u = 0; u < 4; ++u)
+      m[u] = *reinterpret_cast<const int2*>(ws + kWsHead + 2 * min(k0 + c + 16 * u, p.vtiles - 1));
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < 4; ++u) {
       const float ov = __int_as_float(m[u].x);
       const int oi = m[u].y;
-      if (k0 + u < p.vtiles && (k0 + u == 0 || ov > v || (ov == v && oi < ix))) {
+      if (k0 + c + 16 * u < p.vtiles && (ov > v || (ov == v && oi < ix))) {
         v = ov;
         ix = oi;
       }
     }
   }
+#pragma unroll
+  for (int m = 1; m < 16; m <<= 1) {
+    const float ov = __shfl_xor(v, m);
+    const int oi = __shfl_xor(ix, m);
+    if (ov > v || (ov == v && oi < ix)) {
+      v = ov;
+      ix = oi;
+    }
+  }
+  const bool act = active_from(p, sw);
+  *act_out = act;
+  if (!act) return -1;
   return (ix == p.blank || ix < 0 || ix >= p.V1) ? -1 : ix;
 }
 
@@ -350,10 +414,11 @@ __device__ static inline void record(const DecK& p, int b, bool act, int tok) {
 // the order of the atomic appends; every later launch treats each stream on
 // its own, so the order does not change any result).
 __global__ void __launch_bounds__(256) select_kernel(const DecK p) {
-  const int b = blockIdx.x * 256 + threadIdx.x;
-  if (b >= p.batch) return;
+  const int c = threadIdx.x & 15, b = blockIdx.x * 16 + (threadIdx.x >> 4);  // 16 lanes a stream
+  if (b >= p.batch) return;  // uniform per lane group
   bool act;
-  const int tk = decide(p, b, &act);
+  const int tk = decide16(p, b, c, &act);
+  if (c != 0) return;
   record(p, b, act, tk);
   if (tk >= 0) {
     const int cur = p.it & 1;
@@ -365,196 +430,229 @@ __global__ void __launch_bounds__(256) select_kernel(const DecK p) {
 // ---------------------------------------------------------------------------
 template <typename ST>
 struct LstmCfg {
-  static constexpr int SPW = 16;  // streams per workgroup
-  static constexpr int WAVES = 4 * (SPW / 16);           // 4 gates x stream tiles
-  static constexpr int KMAX = 2 * kMaxDim;
+  static constexpr int SPW = 16;   // streams per workgroup
+  static constexpr int WAVES = 8;  // 4 gates x {input part, recurrent part}
 };
 
+// Waves 0-3 (the input part) take gate gi's W_ih x, waves 4-7 (the recurrent
+// part) W_hh h.  Nothing the recurrent part loads (its weight rows, the slots'
+// h and c, the biases) depends on this iteration's decision, so it is all in
+// flight from the launch's first instructions, beside the decision and the
+// embedding rows of the input part.  The recurrent part continues each gate's
+// MFMA chain from the input part's sums, so the k-steps run in the order of
+// one chain over K = [x ; h].
 template <typename ST>
 __global__ void __launch_bounds__(LstmCfg<ST>::WAVES * 64) lstm_kernel(const DecK p) {
+#pragma clang fp contract(off)
   typedef LstmCfg<ST> Cfg;
   constexpr int VEC = 16 / sizeof(ST), SPW = Cfg::SPW;
-  constexpr int RS = 2 * 640 + VEC;  // [x ; h] row of one stream (hidden 640 in LDS)
-  __shared__ __align__(16) ST inp[SPW][RS];
+  constexpr int H = 640;                 // the hidden size the host accepts
+  constexpr int RS = H + VEC;            // x or h row of one stream in LDS
+  constexpr int NCH = H / VEC, CPT = NCH / 16;  // 16-byte chunks of a row; a thread's share
+  static_assert(SPW * 16 == 256 && NCH % 16 == 0, "a part's 256 threads: 16 a stream");
+  __shared__ __align__(16) ST xs[SPW][RS];
+  __shared__ __align__(16) ST hs[SPW][RS];
   __shared__ float gsm[4][SPW][17];
-  __shared__ int32_t tok_s[SPW], slot_s[SPW], bid_s[SPW];
-  constexpr int H = 640;  // the hidden size the host accepts
+  __shared__ int32_t tok_s[SPW];
   const int L = p.layers, layer = p.layer;
   const int u0 = blockIdx.x * 16, b0 = blockIdx.y * SPW;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
-  // which streams update: layer 0 decides (prime: every stream, token blank),
-  // the layers above read layer 0's record
-  if (tid < SPW) {
-    int b = b0 + tid;
-    int tk = -1;
-    if (p.compact && !p.prime) {  // the select launch decided and recorded
-      b = listed_stream(p, p.it & 1, b0 + tid);
-      tk = b >= 0 ? ws_of(p, b)[1] : -1;
-    } else if (b < p.batch) {
-      if (p.prime) {
-        tk = stream_ok(p, b) ? p.blank : -1;
-      } else if (layer == 0) {  // a stream with a bad slot is never active: no token, zero counts
-        bool act;
-        tk = decide(p, b, &act);
-        if (blockIdx.x == 0) record(p, b, act, tk);
-      } else {
-        tk = ws_of(p, b)[1];
-      }
+  const int part = wave >> 2, gi = wave & 3;
+  // compact mode: a workgroup past the list's entries loads nothing
+  const bool listed = p.compact && !p.prime;
+  if (listed && b0 >= min(p.acount[p.it & 1], p.batch)) return;
+  // thread -> (stream entry k, chunks c + 16 j of its row); the 16 threads of an
+  // entry are lanes of one wave.  Layer 0 decides (prime: every stream, token
+  // blank); the layers above and compact mode read the recorded token.  Every
+  // thread of an entry takes the decision; lane c == 0 of column 0 records it.
+  const int pt = tid & 255, k = pt >> 4, c = pt & 15;
+  const bool deciding = layer == 0 && !p.compact && !p.prime;
+  int tk = -1;
+  bool act = false;
+  if (deciding && part == 0 && b0 + k < p.batch) tk = decide16(p, b0 + k, c, &act);
+  // lane c of every 16-lane group reads whether entry c may update (deciding:
+  // it is active), so each wave holds all 16 entries: a tile with none returns
+  // before any weight or row load, with no barrier (every wave sees the same
+  // words); entry k's stream comes from lane k of the thread's group
+  const int bq = listed ? listed_stream(p, p.it & 1, b0 + (lane & 15)) : (b0 + (lane & 15) < p.batch ? b0 + (lane & 15) : -1);
+  int tq = -1, sq = 0;  // entry (lane & 15)'s token (deciding: 0 if active) and slot
+  if (bq >= 0) {
+    const StreamWords w = stream_words(p, bq);
+    sq = (uint32_t)w.slot < (uint32_t)p.num_slots ? w.slot : 0;
+    if (deciding) tq = active_from(p, w) ? 0 : -1;
+    else if (p.prime) tq = (uint32_t)w.slot < (uint32_t)p.num_slots ? p.blank : -1;
+    else tq = ws_of(p, bq)[1];
+  }
+  const int kl = (lane & 48) | k;  // the lane holding entry k; every lane takes part in the shuffles
+  const int b = __shfl(bq, kl), tkq = __shfl(tq, kl), slot_k = __shfl(sq, kl);
+  if (__ballot(tq >= 0) == 0) {
+    // no stream of the tile is active: column 0 still records every decision
+    // (no token, and the frame's counters at its first symbol)
+    if (deciding && part == 0 && blockIdx.x == 0 && c == 0 && b >= 0) record(p, b, act, tk);
+    return;
+  }
+  if (!deciding) tk = tkq;
+  // the wave's weight rows: gate gi, units u0 .. u0 + 15, first chunk
+  const int64_t row = (int64_t)layer * 4 * H + gi * H + u0 + lr;
+  constexpr int ks = H / (4 * VEC);
+  const ST* wrow = (const ST*)(part ? p.w_hh : p.w_ih) + row * H;
+  u32x4 w0[KChunk<ST>::CH];
+  load_chunk<ST>(w0, wrow, wrow, ks, ks, 0, lg);
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4 v[CPT];
+  u32x4 w1[KChunk<ST>::CH];  // the second weight chunk
+  float cb[9];   // recurrent part: c and the 8 biases of (entry k, unit c)
+  int slot = 0;  // recurrent part: the entry's slot
+  if (part == 0) {
+    const bool rec = deciding && blockIdx.x == 0 && c == 0 && b >= 0;
+    if (c == 0) tok_s[k] = tk;
+    // the second weight chunk, then x: the embedding row of the token (layer 0)
+    // or the layer below's new h; loads from addresses valid for any entry,
+    // then masked
+    load_chunk<ST>(w1, wrow, wrow, ks, ks, KChunk<ST>::CH, lg);
+    const ST* src = layer == 0 ? (const ST*)p.embed + (int64_t)max(tk, 0) * H
+                               : (const ST*)p.hn + ((int64_t)max(b, 0) * L + layer - 1) * H;
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) v[j] = ld16(src + (c + 16 * j) * VEC);
+    if (rec) record(p, b, act, tk);  // its reads queue behind the row loads
+#pragma unroll
+    for (int j = 0; j < CPT; ++j)
+      *reinterpret_cast<u32x4*>(&xs[k][(c + 16 * j) * VEC]) = tk >= 0 ? v[j] : u32x4{0u, 0u, 0u, 0u};
+  } else {
+    // h of the entry's slot (zero on a stream's first step), and for the cell
+    // update of unit u0 + c: its c and biases.  An entry that does not update
+    // reads slot 0's finite values; its MFMA column and cell are never used.
+    slot = slot_k;
+    const ST* src = (const ST*)p.h + ((int64_t)slot * L + layer) * H;
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) v[j] = ld16(src + (c + 16 * j) * VEC);
+    const int64_t bo = (int64_t)layer * 4 * H + u0 + c;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      cb[q] = from_st(((const ST*)p.b_ih)[bo + q * H]);
+      cb[4 + q] = from_st(((const ST*)p.b_hh)[bo + q * H]);
     }
-    tok_s[tid] = tk;
-    slot_s[tid] = tk >= 0 ? p.slots[b] : 0;  // a stream that updates has a valid slot
-    bid_s[tid] = tk >= 0 ? b : 0;
+    cb[8] = from_st(((const ST*)p.c)[((int64_t)slot * L + layer) * H + u0 + c]);
+#pragma unroll
+    for (int j = 0; j < CPT; ++j)
+      *reinterpret_cast<u32x4*>(&hs[k][(c + 16 * j) * VEC]) = p.prime ? u32x4{0u, 0u, 0u, 0u} : v[j];
   }
   __syncthreads();
   bool any = false;
-  for (int k = 0; k < SPW; ++k) any |= tok_s[k] >= 0;
-  constexpr int nch = H / VEC;
+  for (int e = 0; e < SPW; ++e) any |= tok_s[e] >= 0;
   if (!any) return;  // uniform: no stream of the tile updates
-  // gate gi rows gi*H + u0 .. +16 for stream tile sb: K = [x ; h] against
-  // [W_ih | W_hh]; the first weight chunk is issued ahead of the staging loads
-  const int gi = wave & 3, sb = wave >> 2;
-  const int64_t row = (int64_t)layer * 4 * H + gi * H + u0 + lr;
-  constexpr int ks = H / (4 * VEC);
-  const ST* wi = (const ST*)p.w_ih + row * H;
-  const ST* wh = (const ST*)p.w_hh + row * H;
-  u32x4 w0[KChunk<ST>::CH];
-  load_chunk<ST>(w0, wi, wh, ks, 2 * ks, 0, lg);
-  __builtin_amdgcn_sched_barrier(0);
-  // [x ; h] of each stream: x = embedding row of the token (layer 0) or the new
-  // h of the layer below; h = this layer's current h (zero on a stream's first
-  // step).  Every load is issued first, from an address valid for any stream,
-  // then masked.
-  constexpr int NTH = Cfg::WAVES * 64, IT = (SPW * 2 * nch + NTH - 1) / NTH;
-  u32x4 xr[IT];
+  // gate gi rows for the 16 streams: the input part's k-steps, then the
+  // recurrent part's from those sums (its second chunk loading meanwhile);
+  // lane: units u0 + 4 lg + i, stream lr
+  if (part == 1) load_chunk<ST>(w1, wrow, wrow, ks, ks, KChunk<ST>::CH, lg);
+  if (part == 0) {
+    const f32x4_t d = mma_rows2<ST>(w0, w1, wrow, wrow, ks, ks, &xs[lr][0], lg, f32x4_t{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-  for (int it = 0; it < IT; ++it) {
-    const int i = min(tid + it * NTH, SPW * 2 * nch - 1);
-    const int k = i / (2 * nch), cc = (i - k * 2 * nch) * VEC;
-    const int b = bid_s[k];
-    const ST* src;
-    if (cc < H)
-      src = layer == 0 ? (const ST*)p.embed + (int64_t)max(tok_s[k], 0) * H + cc
-                       : (const ST*)p.hn + ((int64_t)b * L + layer - 1) * H + cc;
-    else
-      src = (const ST*)p.h + ((int64_t)slot_s[k] * L + layer) * H + cc - H;
-    xr[it] = ld16(src);
-  }
-#pragma unroll
-  for (int it = 0; it < IT; ++it) {
-    const int i = tid + it * NTH;
-    if (i < SPW * 2 * nch) {
-      const int k = i / (2 * nch), cc = (i - k * 2 * nch) * VEC;
-      const bool keep = tok_s[k] >= 0 && (cc < H || !p.prime);
-      *reinterpret_cast<u32x4*>(&inp[k][cc]) = keep ? xr[it] : u32x4{0u, 0u, 0u, 0u};
-    }
+    for (int i = 0; i < 4; ++i) gsm[gi][lr][4 * lg + i] = d[i];
   }
   __syncthreads();
-  const f32x4_t d = mma_rows<ST>(w0, wi, wh, ks, 2 * ks, &inp[sb * 16 + lr][0], lg, f32x4_t{0.f, 0.f, 0.f, 0.f});
-  // lane: units u0 + 4*lg + i of gate gi, stream sb*16 + lr
+  if (part == 1) {
+    f32x4_t d;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) gsm[gi][sb * 16 + lr][4 * lg + i] = d[i];
+    for (int i = 0; i < 4; ++i) d[i] = gsm[gi][lr][4 * lg + i];
+    d = mma_rows2<ST>(w0, w1, wrow, wrow, ks, ks, &hs[lr][0], lg, d);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) gsm[gi][lr][4 * lg + i] = d[i];
+  }
   __syncthreads();
-  // cell update: thread -> (stream, unit)
-  for (int i = tid; i < SPW * 16; i += Cfg::WAVES * 64) {
-    const int k = i / 16, u = i % 16, b = bid_s[k];
-    if (tok_s[k] < 0) continue;
-    const int64_t so = ((int64_t)slot_s[k] * L + layer) * H + u0 + u;
-    const int64_t bo = (int64_t)layer * 4 * H + u0 + u;
+  // cell update: recurrent-part thread -> (stream entry k, unit u0 + c)
+  if (part == 1 && tok_s[k] >= 0) {  // a stream that updates has a valid slot
     float g4[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      g4[q] = gsm[q][k][u] + from_st(((const ST*)p.b_ih)[bo + q * H]) + from_st(((const ST*)p.b_hh)[bo + q * H]);
+    for (int q = 0; q < 4; ++q) g4[q] = gsm[q][k][c] + cb[q] + cb[4 + q];
     const float ig = 1.f / (1.f + __expf(-g4[0])), fg = 1.f / (1.f + __expf(-g4[1]));
     const float gg = tanhf(g4[2]), og = 1.f / (1.f + __expf(-g4[3]));
-    const float c0 = p.prime ? 0.f : from_st(((const ST*)p.c)[so]);
-    const float c1 = fg * c0 + ig * gg;
-    ((ST*)p.c)[so] = to_st<ST>(c1);
-    ((ST*)p.hn)[((int64_t)b * L + layer) * H + u0 + u] = to_st<ST>(og * tanhf(c1));
+    const float c0 = p.prime ? 0.f : cb[8];
+    // one rounding order whatever the surrounding code: the input gate's
+    // product fused, the forget gate's rounded first
+    const float c1 = fmaf(ig, gg, fg * c0);
+    ((ST*)p.c)[((int64_t)slot * L + layer) * H + u0 + c] = to_st<ST>(c1);
+    ((ST*)p.hn)[((int64_t)b * L + layer) * H + u0 + c] = to_st<ST>(og * tanhf(c1));
   }
 }
 
 // ---------------------------------------------------------------------------
 template <typename ST>
-__global__ void __launch_bounds__(256) pred_kernel(const DecK p) {
-  constexpr int VEC = 16 / sizeof(ST);
-  __shared__ __align__(16) ST hs[16][kMaxDim + 8];
-  __shared__ int32_t tok_s[16], slot_s[16], bid_s[16];
-  constexpr int H = 640;  // the hidden size the host accepts
+__global__ void __launch_bounds__(kPredWaves * 64) pred_kernel(const DecK p) {
+  constexpr int VEC = 16 / sizeof(ST), W = kPredWaves, NTH = W * 64, TPS = NTH / 16;
+  constexpr int H = 640;                        // the hidden size the host accepts
+  constexpr int NCH = H / VEC, CPT = NCH / TPS;  // 16-byte chunks of an h row; a thread's share
+  static_assert(NCH % TPS == 0, "h row chunks over a stream's threads");
+  __shared__ __align__(16) ST hs[16][H + VEC];
+  __shared__ int32_t tok_s[16], slot_s[16];
   const int J = p.J, L = p.layers;
-  const int j0 = blockIdx.x * 64, b0 = blockIdx.y * 16;
+  const int j0 = blockIdx.x * (16 * W), b0 = blockIdx.y * 16;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
-  if (tid < 16) {
-    const int b = listed_stream(p, p.compact && !p.prime ? p.it & 1 : -1, b0 + tid);
-    const int tk = b >= 0 && stream_ok(p, b) ? (p.prime ? 0 : ws_of(p, b)[1]) : -1;
-    tok_s[tid] = tk;
-    slot_s[tid] = tk >= 0 ? p.slots[b] : 0;
-    bid_s[tid] = tk >= 0 ? b : 0;
+  // the streams that updated: the batch's (prime: every stream's), or in compact
+  // mode the list of this iteration's token emitters; a workgroup past that
+  // list loads nothing
+  const int list = p.compact && !p.prime ? p.it & 1 : -1;
+  if (list >= 0 && b0 >= min(p.acount[list], p.batch)) return;
+  // lane c of every 16-lane group reads entry c's token and slot, so each wave
+  // holds all 16: a tile with no update returns before any weight or row
+  // load, with no barrier (every wave sees the same words).  Thread ->
+  // (stream entry k, chunks c + TPS j of a row); entry k's words come from
+  // lane k of the thread's group.
+  const int k = tid / TPS, c = tid % TPS;
+  const int bq = listed_stream(p, list, b0 + (lane & 15));
+  int sq = 0, tq = -1;
+  if (bq >= 0) {
+    sq = p.slots[bq];
+    if ((uint32_t)sq < (uint32_t)p.num_slots) tq = p.prime ? 0 : ws_of(p, bq)[1];
   }
-  __syncthreads();
-  bool any = false;
-  for (int k = 0; k < 16; ++k) any |= tok_s[k] >= 0;
-  if (!any) return;
-  // this wave's weight rows (their first chunk issued ahead of the staging
-  // loads); a wave past the joint size keeps its lanes but loads row J - 1
+  if (__ballot(tq >= 0) == 0) return;
+  const int src = (lane & 48) | k;
+  const int b = __shfl(bq, src), tk = __shfl(tq, src);
+  const int sk = __shfl(sq, src);  // every lane takes part in the shuffles
+  const int slot = tk >= 0 ? sk : 0;
+  // this wave's weight rows (first chunk) and its lanes' biases; a wave past
+  // the joint size keeps its lanes but reads row J - 1
   constexpr int ks = H / (4 * VEC);
-  const bool wave_live = j0 + wave * 16 < J;  // uniform per wave
-  const ST* wrow = (const ST*)p.w_pred + (int64_t)min(j0 + wave * 16 + lr, J - 1) * H;
-  u32x4 w0[KChunk<ST>::CH];
+  const int jw = j0 + wave * 16;
+  const bool wave_live = jw < J;  // uniform per wave
+  const ST* wrow = (const ST*)p.w_pred + (int64_t)min(jw + lr, J - 1) * H;
+  u32x4 w0[KChunk<ST>::CH], w1[KChunk<ST>::CH];
   load_chunk<ST>(w0, wrow, wrow, ks, ks, 0, lg);
-  __builtin_amdgcn_sched_barrier(0);
-  // the top layer's new h of the 16 streams: loads first (valid addresses for
-  // any stream), then masked into LDS
-  constexpr int nch = H / VEC, IT = (16 * nch + 255) / 256;
-  u32x4 hr[IT];
+  float bias[4];
 #pragma unroll
-  for (int it = 0; it < IT; ++it) {
-    const int i = min(tid + it * 256, 16 * nch - 1);
-    const int k = i / nch, cc = (i - k * nch) * VEC, b = bid_s[k];
-    hr[it] = ld16((const ST*)p.hn + ((int64_t)b * L + L - 1) * H + cc);
+  for (int i = 0; i < 4; ++i) bias[i] = from_st(((const ST*)p.b_pred)[min(jw + 4 * lg + i, J - 1)]);
+  // the top layer's new h of the entry, loads first (valid addresses for any
+  // entry), then masked into LDS
+  const ST* top = (const ST*)p.hn + ((int64_t)max(b, 0) * L + L - 1) * H;
+  u32x4 hr[CPT];
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) hr[j] = ld16(top + (c + TPS * j) * VEC);
+  // the new h of every layer into the slot state: this workgroup's share,
+  // chunks q = blockIdx.x + gridDim.x (c + TPS m) of the entry's L rows
+  const int nq = L * NCH, qs = gridDim.x * TPS;
+  const ST* hn_b = (const ST*)p.hn + (int64_t)max(b, 0) * L * H;
+  ST* h_s = (ST*)p.h + (int64_t)slot * L * H;
+  load_chunk<ST>(w1, wrow, wrow, ks, ks, KChunk<ST>::CH, lg);
+  if (c == 0) {
+    tok_s[k] = tk;
+    slot_s[k] = slot;
   }
 #pragma unroll
-  for (int it = 0; it < IT; ++it) {
-    const int i = tid + it * 256;
-    if (i < 16 * nch) {
-      const int k = i / nch, cc = (i - k * nch) * VEC;
-      *reinterpret_cast<u32x4*>(&hs[k][cc]) = tok_s[k] >= 0 ? hr[it] : u32x4{0u, 0u, 0u, 0u};
-    }
-  }
-  // the new h of every layer into the slot state (one column of workgroups),
-  // IT chunks per thread at a time: loads, then stores
-  if (blockIdx.x == 0) {
-    for (int i0 = 0; i0 < 16 * L * nch; i0 += 256 * IT) {
-      u32x4 v[IT];
-#pragma unroll
-      for (int it = 0; it < IT; ++it) {
-        const int i = min(i0 + tid + it * 256, 16 * L * nch - 1);
-        const int k = i / (L * nch), r = i - k * L * nch, b = bid_s[k];
-        const int l = r / nch, cc = (r - l * nch) * VEC;
-        v[it] = ld16((const ST*)p.hn + ((int64_t)b * L + l) * H + cc);
-      }
-#pragma unroll
-      for (int it = 0; it < IT; ++it) {
-        const int i = i0 + tid + it * 256;
-        if (i < 16 * L * nch) {
-          const int k = i / (L * nch), r = i - k * L * nch;
-          if (tok_s[k] >= 0) {
-            const int l = r / nch, cc = (r - l * nch) * VEC;
-            st16((ST*)p.h + ((int64_t)slot_s[k] * L + l) * H + cc, v[it]);
-          }
-        }
-      }
-    }
+  for (int j = 0; j < CPT; ++j)
+    *reinterpret_cast<u32x4*>(&hs[k][(c + TPS * j) * VEC]) = tk >= 0 ? hr[j] : u32x4{0u, 0u, 0u, 0u};
+  for (int q = blockIdx.x + gridDim.x * c; q < nq; q += qs) {
+    const u32x4 v = ld16(hn_b + (q / NCH) * H + (q % NCH) * VEC);
+    if (tk >= 0) st16(h_s + (q / NCH) * H + (q % NCH) * VEC, v);
   }
   __syncthreads();
   if (!wave_live) return;  // uniform per wave; no barrier below
-  const f32x4_t d = mma_rows<ST>(w0, wrow, wrow, ks, ks, &hs[lr][0], lg, f32x4_t{0.f, 0.f, 0.f, 0.f});
-  // lane: outputs j0 + 16 wave + 4 lg + i for stream lr
+  const f32x4_t d = mma_rows2<ST>(w0, w1, wrow, wrow, ks, ks, &hs[lr][0], lg, f32x4_t{0.f, 0.f, 0.f, 0.f});
+  // lane: outputs jw + 4 lg + i for stream lr
   if (tok_s[lr] >= 0) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int jj = j0 + wave * 16 + 4 * lg + i;
-      ((ST*)p.pred_proj)[(int64_t)slot_s[lr] * J + jj] =
-          to_st<ST>(d[i] + from_st(((const ST*)p.b_pred)[jj]));
+      const int jj = jw + 4 * lg + i;
+      ((ST*)p.pred_proj)[(int64_t)slot_s[lr] * J + jj] = to_st<ST>(d[i] + bias[i]);
     }
   }
 }
@@ -608,14 +706,14 @@ static int run_step(const pk_rnnt_args* a, hipStream_t st) {
   k.prime = a->prime;
   const dim3 gj(k.vtiles, (a->batch + 15) / 16);
   const dim3 gl(a->hidden / 16, (a->batch + LstmCfg<ST>::SPW - 1) / LstmCfg<ST>::SPW);
-  const dim3 gp((a->joint + 63) / 64, (a->batch + 15) / 16);
+  const dim3 gp((a->joint + 16 * kPredWaves - 1) / (16 * kPredWaves), (a->batch + 15) / 16);
   auto lstm = [&]() {
     for (int l = 0; l < a->layers; ++l) {
       k.layer = l;
       hipLaunchKernelGGL(lstm_kernel<ST>, gl, dim3(LstmCfg<ST>::WAVES * 64), 0, st, k);
     }
   };
-  auto pred = [&]() { hipLaunchKernelGGL(pred_kernel<ST>, gp, dim3(256), 0, st, k); };
+  auto pred = [&]() { hipLaunchKernelGGL(pred_kernel<ST>, gp, dim3(kPredWaves * 64), 0, st, k); };
   k.t = k.s = 0;
   if (!a->prime) {
     for (int t = 0; t < a->max_frames; ++t)
@@ -623,8 +721,8 @@ static int run_step(const pk_rnnt_args* a, hipStream_t st) {
         k.t = t;
         k.s = s;
         k.it = t * a->max_symbols + s;
-        hipLaunchKernelGGL(joint_kernel<ST>, gj, dim3(512), 0, st, k);
-        if (k.compact) hipLaunchKernelGGL(select_kernel, dim3((a->batch + 255) / 256), dim3(256), 0, st, k);
+        hipLaunchKernelGGL(joint_kernel<ST>, gj, dim3(kJointWaves * 64), 0, st, k);
+        if (k.compact) hipLaunchKernelGGL(select_kernel, dim3((a->batch + 15) / 16), dim3(256), 0, st, k);
         lstm();
         pred();
       }

@@ -70,17 +70,26 @@ struct Tr<_Float16> {
   }
 };
 
-// bfloat16 is carried as raw 16-bit patterns; fp32 -> bf16 rounds to nearest even.
+// bfloat16 is carried as raw 16-bit patterns; fp32 -> bf16 rounds to nearest
+// even with gfx950's v_cvt_pk_bf16_f32, two values an instruction.  For every
+// fp32 input it gives the bits of the integer rounding (u + 0x7fff + ((u >> 16)
+// & 1)) >> 16, and for a NaN (u >> 16) | 0x40 (sign and high payload kept,
+// quieted): tests/native/bf16_rounding_check.hip runs all 2^32 inputs.
 struct bf16_t {
   uint16_t bits;
 };
 
-__device__ static inline uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;  // quiet NaN
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// lo in bits 0-15, hi in bits 16-31
+__device__ static inline uint32_t bf16_pair_bits(float lo, float hi) {
+  bf16x2_t v;
+  v.x = (__bf16)lo;
+  v.y = (__bf16)hi;
+  return __builtin_bit_cast(uint32_t, v);
 }
+
+__device__ static inline uint32_t f32_to_bf16_bits(float f) { return bf16_pair_bits(f, 0.f) & 0xffffu; }
 
 template <>
 struct Tr<bf16_t> {
@@ -97,10 +106,10 @@ struct Tr<bf16_t> {
   }
   __device__ static inline u32x4 pack(const float* f) {
     u32x4 v;
-    v.x = f32_to_bf16_bits(f[0]) | (f32_to_bf16_bits(f[1]) << 16);
-    v.y = f32_to_bf16_bits(f[2]) | (f32_to_bf16_bits(f[3]) << 16);
-    v.z = f32_to_bf16_bits(f[4]) | (f32_to_bf16_bits(f[5]) << 16);
-    v.w = f32_to_bf16_bits(f[6]) | (f32_to_bf16_bits(f[7]) << 16);
+    v.x = bf16_pair_bits(f[0], f[1]);
+    v.y = bf16_pair_bits(f[2], f[3]);
+    v.z = bf16_pair_bits(f[4], f[5]);
+    v.w = bf16_pair_bits(f[6], f[7]);
     return v;
   }
 };

@@ -167,10 +167,10 @@ def test_rnnt_args_validated_before_launch():
     assert L.pk_rnnt_greedy_step(ctypes.byref(a), None) == _lib.PK_ERR_INVALID
     a.blank, a.joint = 1026, 600  # joint not a multiple of 64
     assert L.pk_rnnt_greedy_step(ctypes.byref(a), None) == _lib.PK_ERR_UNSUPPORTED
-    # workspace: per-stream words (4 + 2 x 9 vocabulary tiles) rounded to 256 B, then h'
-    # per-stream words 128 x (4 + 2 x 9 tiles), two stream lists and their counts,
-    # rounded to 256 bytes; then the new h of every stream and layer
-    assert L.pk_rnnt_workspace_bytes(_lib.DTYPE_F16, 128, 1027, 1, 640) == 12544 + 128 * 640 * 2
+    # workspace: per-stream words 128 x (4 + 2 x 17 tiles of 64 vocabulary rows), two
+    # stream lists and their counts, rounded to 256 bytes; then the new h of every
+    # stream and layer
+    assert L.pk_rnnt_workspace_bytes(_lib.DTYPE_F16, 128, 1027, 1, 640) == 20736 + 128 * 640 * 2
     assert L.pk_rnnt_workspace_bytes(_lib.DTYPE_F32, 1, 1025, 2, 640) == 256 + 2 * 640 * 4
 
 
