@@ -141,10 +141,9 @@ struct KChunk {
 // loads are all issued before the chunk's first MFMA (the index clamped, so
 // every load is valid): a wave waits for one L2 round trip per CH k-steps rather
 // than one per k-step.  The k-steps accumulate in order, as a plain loop would.
-template <typename ST>
-__device__ static inline void load_chunk(u32x4 (&w)[KChunk<ST>::CH], const ST* wa, const ST* wb, int ka, int nk,
-                                         int k0, int lg) {
-  constexpr int VEC = 16 / sizeof(ST), CH = KChunk<ST>::CH;
+template <typename ST, int CH>
+__device__ static inline void load_chunk(u32x4 (&w)[CH], const ST* wa, const ST* wb, int ka, int nk, int k0, int lg) {
+  constexpr int VEC = 16 / sizeof(ST);
 #pragma unroll
   for (int u = 0; u < CH; ++u) {
     const int kk = min(k0 + u, nk - 1);
@@ -153,10 +152,9 @@ __device__ static inline void load_chunk(u32x4 (&w)[KChunk<ST>::CH], const ST* w
   }
 }
 
-template <typename ST>
-__device__ static inline f32x4_t mma_chunk(const u32x4 (&w)[KChunk<ST>::CH], const ST* col, int k0, int nk, int lg,
-                                           f32x4_t d) {
-  constexpr int VEC = 16 / sizeof(ST), CH = KChunk<ST>::CH;
+template <typename ST, int CH>
+__device__ static inline f32x4_t mma_chunk(const u32x4 (&w)[CH], const ST* col, int k0, int nk, int lg, f32x4_t d) {
+  constexpr int VEC = 16 / sizeof(ST);
 #pragma unroll
   for (int u = 0; u < CH; ++u)
     if (k0 + u < nk) d = MmaR<ST>::step(w[u], *reinterpret_cast<const u32x4*>(col + (k0 + u) * 4 * VEC + VEC * lg), d);
@@ -165,10 +163,9 @@ __device__ static inline f32x4_t mma_chunk(const u32x4 (&w)[KChunk<ST>::CH], con
 
 // d += the product, with the first chunk's weights already loaded into w0 (its
 // loads issued early, so their round trip overlaps the caller's other loads).
-template <typename ST>
-__device__ static inline f32x4_t mma_rows(const u32x4 (&w0)[KChunk<ST>::CH], const ST* wa, const ST* wb, int ka,
-                                          int nk, const ST* col, int lg, f32x4_t d) {
-  constexpr int CH = KChunk<ST>::CH;
+template <typename ST, int CH>
+__device__ static inline f32x4_t mma_rows(const u32x4 (&w0)[CH], const ST* wa, const ST* wb, int ka, int nk,
+                                          const ST* col, int lg, f32x4_t d) {
   d = mma_chunk<ST>(w0, col, 0, nk, lg, d);
   for (int k0 = CH; k0 < nk; k0 += CH) {
     u32x4 w[CH];
@@ -180,11 +177,9 @@ __device__ static inline f32x4_t mma_rows(const u32x4 (&w0)[KChunk<ST>::CH], con
 }
 
 // The same with the first two chunks already loaded (w1: k-steps CH .. 2 CH).
-template <typename ST>
-__device__ static inline f32x4_t mma_rows2(const u32x4 (&w0)[KChunk<ST>::CH], const u32x4 (&w1)[KChunk<ST>::CH],
-                                           const ST* wa, const ST* wb, int ka, int nk, const ST* col, int lg,
-                                           f32x4_t d) {
-  constexpr int CH = KChunk<ST>::CH;
+template <typename ST, int CH>
+__device__ static inline f32x4_t mma_rows2(const u32x4 (&w0)[CH], const u32x4 (&w1)[CH], const ST* wa,
+                                           const ST* wb, int ka, int nk, const ST* col, int lg, f32x4_t d) {
   d = mma_chunk<ST>(w0, col, 0, nk, lg, d);
   d = mma_chunk<ST>(w1, col, CH, nk, lg, d);
   for (int k0 = 2 * CH; k0 < nk; k0 += CH) {
@@ -351,39 +346,49 @@ __global__ void __launch_bounds__(kJointWaves * 64) joint_kernel(const DecK p) {
 // stream words and the first 64 tiles are loaded in one round.
 // Workspace words: 0 = blank seen in the current frame, 1 = token that updates
 // the predictor this iteration (-1: none), 2 = tokens emitted this step.
-__device__ static inline int decide16(const DecK& p, int b, int c, bool* act_out) {
+// The loads of a decision: the stream words and the lane's first 4 tiles (the
+// first 64 tiles of the group), issued together.
+struct DecideLoads {
+  StreamWords sw;
+  int2 m[4];
+};
+__device__ static inline DecideLoads decide_load(const DecK& p, int b, int c) {
   const int32_t* ws = ws_of(p, b);
-  const StreamWords sw = stream_words(p, b);
+  DecideLoads d;
+  d.sw = stream_words(p, b);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) d.m[u] = *reinterpret_cast<const int2*>(ws + kWsHead + 2 * min(c + 16 * u, p.vtiles - 1));
+  return d;
+}
+__device__ static inline void decide_take(float ov, int oi, float& v, int& ix) {
+  if (ov > v || (ov == v && oi < ix)) {
+    v = ov;
+    ix = oi;
+  }
+}
+__device__ static inline int decide_finish(const DecK& p, int b, int c, const DecideLoads& d, bool* act_out) {
   float v = -INFINITY;
   int ix = 0x7fffffff;
-  for (int k0 = 0; k0 < p.vtiles; k0 += 64) {
-    int2 m[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-      m[u] = *reinterpret_cast<const int2*>(ws + kWsHead + 2 * min(k0 + c + 16 * u, p.vtiles - 1));
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const float ov = __int_as_float(m[u].x);
-      const int oi = m[u].y;
-      if (k0 + c + 16 * u < p.vtiles && (ov > v || (ov == v && oi < ix))) {
-        v = ov;
-        ix = oi;
-      }
+  for (int u = 0; u < 4; ++u)
+    if (c + 16 * u < p.vtiles) decide_take(__int_as_float(d.m[u].x), d.m[u].y, v, ix);
+  const int32_t* ws = ws_of(p, b);
+  for (int k0 = 64; k0 < p.vtiles; k0 += 16) {  // tiles past the first 64 (vocabularies past 4,096 rows)
+    const int t = k0 + c;
+    if (t < p.vtiles) {
+      const int2 m = *reinterpret_cast<const int2*>(ws + kWsHead + 2 * t);
+      decide_take(__int_as_float(m.x), m.y, v, ix);
     }
   }
 #pragma unroll
-  for (int m = 1; m < 16; m <<= 1) {
-    const float ov = __shfl_xor(v, m);
-    const int oi = __shfl_xor(ix, m);
-    if (ov > v || (ov == v && oi < ix)) {
-      v = ov;
-      ix = oi;
-    }
-  }
-  const bool act = active_from(p, sw);
+  for (int m = 1; m < 16; m <<= 1) decide_take(__shfl_xor(v, m), __shfl_xor(ix, m), v, ix);
+  const bool act = active_from(p, d.sw);
   *act_out = act;
   if (!act) return -1;
   return (ix == p.blank || ix < 0 || ix >= p.V1) ? -1 : ix;
+}
+__device__ static inline int decide16(const DecK& p, int b, int c, bool* act_out) {
+  return decide_finish(p, b, c, decide_load(p, b, c), act_out);
 }
 
 // The record of stream b's decision (one writer per stream).  Other
@@ -428,28 +433,30 @@ __global__ void __launch_bounds__(256) select_kernel(const DecK p) {
 }
 
 // ---------------------------------------------------------------------------
-template <typename ST>
+// SPW streams per workgroup (16 or 32; the host takes 32 when that keeps every
+// workgroup on a CU of its own), 8 waves: 4 gates x {input part, recurrent part}.
+template <typename ST, int SPW>
 struct LstmCfg {
-  static constexpr int SPW = 16;   // streams per workgroup
-  static constexpr int WAVES = 8;  // 4 gates x {input part, recurrent part}
+  static constexpr int WAVES = 8;
+  static constexpr int NE = SPW / 16;  // stream entries a thread: k + 16 e
+  static constexpr int CH = 10;        // k-steps of a weight chunk
 };
 
 // Waves 0-3 (the input part) take gate gi's W_ih x, waves 4-7 (the recurrent
-// part) W_hh h.  Nothing the recurrent part loads (its weight rows, the slots'
-// h and c, the biases) depends on this iteration's decision, so it is all in
-// flight from the launch's first instructions, beside the decision and the
-// embedding rows of the input part.  The recurrent part continues each gate's
-// MFMA chain from the input part's sums, so the k-steps run in the order of
-// one chain over K = [x ; h].
-template <typename ST>
-__global__ void __launch_bounds__(LstmCfg<ST>::WAVES * 64) lstm_kernel(const DecK p) {
+// part) W_hh h.  The recurrent part's loads (its weight rows, the slots' h and
+// c, the biases) do not depend on this iteration's decision, so they are in
+// flight beside the decision and the embedding rows of the input part.  The
+// recurrent part continues each gate's MFMA chain from the input part's sums,
+// so the k-steps run in the order of one chain over K = [x ; h].
+template <typename ST, int SPW>
+__global__ void __launch_bounds__(512) lstm_kernel(const DecK p) {  // LstmCfg::WAVES x 64
 #pragma clang fp contract(off)
-  typedef LstmCfg<ST> Cfg;
-  constexpr int VEC = 16 / sizeof(ST), SPW = Cfg::SPW;
+  typedef LstmCfg<ST, SPW> Cfg;
+  constexpr int VEC = 16 / sizeof(ST), NE = Cfg::NE, CH = Cfg::CH;
   constexpr int H = 640;                 // the hidden size the host accepts
   constexpr int RS = H + VEC;            // x or h row of one stream in LDS
   constexpr int NCH = H / VEC, CPT = NCH / 16;  // 16-byte chunks of a row; a thread's share
-  static_assert(SPW * 16 == 256 && NCH % 16 == 0, "a part's 256 threads: 16 a stream");
+  static_assert(NCH % 16 == 0 && (NE == 1 || NE == 2) && Cfg::WAVES * 64 == 512, "a part's 256 threads: 16 a stream entry");
   __shared__ __align__(16) ST xs[SPW][RS];
   __shared__ __align__(16) ST hs[SPW][RS];
   __shared__ float gsm[4][SPW][17];
@@ -461,118 +468,179 @@ __global__ void __launch_bounds__(LstmCfg<ST>::WAVES * 64) lstm_kernel(const Dec
   // compact mode: a workgroup past the list's entries loads nothing
   const bool listed = p.compact && !p.prime;
   if (listed && b0 >= min(p.acount[p.it & 1], p.batch)) return;
-  // thread -> (stream entry k, chunks c + 16 j of its row); the 16 threads of an
-  // entry are lanes of one wave.  Layer 0 decides (prime: every stream, token
-  // blank); the layers above and compact mode read the recorded token.  Every
-  // thread of an entry takes the decision; lane c == 0 of column 0 records it.
+  // thread -> stream entries k + 16 e and chunks c + 16 j of their rows; the 16
+  // threads of an entry are lanes of one wave.  Layer 0 decides (prime: every
+  // stream, token blank); the layers above and compact mode read the recorded
+  // token.  Every thread of an entry takes the decision; lane c == 0 of column
+  // 0 records it.
   const int pt = tid & 255, k = pt >> 4, c = pt & 15;
   const bool deciding = layer == 0 && !p.compact && !p.prime;
-  int tk = -1;
-  bool act = false;
-  if (deciding && part == 0 && b0 + k < p.batch) tk = decide16(p, b0 + k, c, &act);
-  // lane c of every 16-lane group reads whether entry c may update (deciding:
-  // it is active), so each wave holds all 16 entries: a tile with none returns
-  // before any weight or row load, with no barrier (every wave sees the same
-  // words); entry k's stream comes from lane k of the thread's group
-  const int bq = listed ? listed_stream(p, p.it & 1, b0 + (lane & 15)) : (b0 + (lane & 15) < p.batch ? b0 + (lane & 15) : -1);
-  int tq = -1, sq = 0;  // entry (lane & 15)'s token (deciding: 0 if active) and slot
-  if (bq >= 0) {
-    const StreamWords w = stream_words(p, bq);
-    sq = (uint32_t)w.slot < (uint32_t)p.num_slots ? w.slot : 0;
-    if (deciding) tq = active_from(p, w) ? 0 : -1;
-    else if (p.prime) tq = (uint32_t)w.slot < (uint32_t)p.num_slots ? p.blank : -1;
-    else tq = ws_of(p, bq)[1];
+  int tk[NE];
+  bool act[NE];
+  DecideLoads dl[NE];
+#pragma unroll
+  for (int e = 0; e < NE; ++e) {
+    tk[e] = -1;
+    act[e] = false;
+    if (deciding && part == 0) dl[e] = decide_load(p, min(b0 + k + 16 * e, p.batch - 1), c);
+  }
+  // lane c of every 16-lane group reads whether entries c + 16 e may update
+  // (deciding: they are active), so each wave holds all entries: a tile with
+  // none returns before any weight or row load, with no barrier (every wave
+  // sees the same words); entry k + 16 e's stream, token and slot come from
+  // lane k of the thread's group
+  int bq[NE], tq[NE], sq[NE];
+  bool may = false;
+#pragma unroll
+  for (int e = 0; e < NE; ++e) {
+    const int q = b0 + (lane & 15) + 16 * e;
+    bq[e] = listed ? listed_stream(p, p.it & 1, q) : (q < p.batch ? q : -1);
+    tq[e] = -1;  // deciding: 0 if active
+    sq[e] = 0;
+    if (bq[e] >= 0) {
+      const StreamWords w = stream_words(p, bq[e]);
+      const bool sok = (uint32_t)w.slot < (uint32_t)p.num_slots;
+      sq[e] = sok ? w.slot : 0;
+      if (deciding) tq[e] = active_from(p, w) ? 0 : -1;
+      else if (p.prime) tq[e] = sok ? p.blank : -1;
+      else tq[e] = ws_of(p, bq[e])[1];
+    }
+    may |= tq[e] >= 0;
   }
   const int kl = (lane & 48) | k;  // the lane holding entry k; every lane takes part in the shuffles
-  const int b = __shfl(bq, kl), tkq = __shfl(tq, kl), slot_k = __shfl(sq, kl);
-  if (__ballot(tq >= 0) == 0) {
+  int b[NE], slot[NE];
+#pragma unroll
+  for (int e = 0; e < NE; ++e) {
+    b[e] = __shfl(bq[e], kl);
+    slot[e] = __shfl(sq[e], kl);
+    const int t = __shfl(tq[e], kl);
+    if (!deciding) tk[e] = t;
+  }
+  if (deciding && part == 0) {
+#pragma unroll
+    for (int e = 0; e < NE; ++e)
+      if (b[e] >= 0) tk[e] = decide_finish(p, b[e], c, dl[e], &act[e]);
+  }
+  const bool rec = deciding && part == 0 && blockIdx.x == 0 && c == 0;
+  if (__ballot(may) == 0) {
     // no stream of the tile is active: column 0 still records every decision
     // (no token, and the frame's counters at its first symbol)
-    if (deciding && part == 0 && blockIdx.x == 0 && c == 0 && b >= 0) record(p, b, act, tk);
+    if (rec) {
+#pragma unroll
+      for (int e = 0; e < NE; ++e)
+        if (b[e] >= 0) record(p, b[e], act[e], tk[e]);
+    }
     return;
   }
-  if (!deciding) tk = tkq;
   // the wave's weight rows: gate gi, units u0 .. u0 + 15, first chunk
   const int64_t row = (int64_t)layer * 4 * H + gi * H + u0 + lr;
   constexpr int ks = H / (4 * VEC);
   const ST* wrow = (const ST*)(part ? p.w_hh : p.w_ih) + row * H;
-  u32x4 w0[KChunk<ST>::CH];
+  u32x4 w0[CH];
   load_chunk<ST>(w0, wrow, wrow, ks, ks, 0, lg);
   __builtin_amdgcn_sched_barrier(0);
-  u32x4 v[CPT];
-  u32x4 w1[KChunk<ST>::CH];  // the second weight chunk
-  float cb[9];   // recurrent part: c and the 8 biases of (entry k, unit c)
-  int slot = 0;  // recurrent part: the entry's slot
+  u32x4 v[NE][CPT];
+  u32x4 w1[CH];   // the second weight chunk
+  float cb[8];    // recurrent part: the 8 biases of unit u0 + c
+  float c0[NE];   // recurrent part: c of (entry k + 16 e, unit u0 + c)
   if (part == 0) {
-    const bool rec = deciding && blockIdx.x == 0 && c == 0 && b >= 0;
-    if (c == 0) tok_s[k] = tk;
+    if (c == 0) {
+#pragma unroll
+      for (int e = 0; e < NE; ++e) tok_s[k + 16 * e] = tk[e];
+    }
     // the second weight chunk, then x: the embedding row of the token (layer 0)
     // or the layer below's new h; loads from addresses valid for any entry,
     // then masked
-    load_chunk<ST>(w1, wrow, wrow, ks, ks, KChunk<ST>::CH, lg);
-    const ST* src = layer == 0 ? (const ST*)p.embed + (int64_t)max(tk, 0) * H
-                               : (const ST*)p.hn + ((int64_t)max(b, 0) * L + layer - 1) * H;
+    load_chunk<ST>(w1, wrow, wrow, ks, ks, CH, lg);
 #pragma unroll
-    for (int j = 0; j < CPT; ++j) v[j] = ld16(src + (c + 16 * j) * VEC);
-    if (rec) record(p, b, act, tk);  // its reads queue behind the row loads
+    for (int e = 0; e < NE; ++e) {
+      const ST* src = layer == 0 ? (const ST*)p.embed + (int64_t)max(tk[e], 0) * H
+                                 : (const ST*)p.hn + ((int64_t)max(b[e], 0) * L + layer - 1) * H;
 #pragma unroll
-    for (int j = 0; j < CPT; ++j)
-      *reinterpret_cast<u32x4*>(&xs[k][(c + 16 * j) * VEC]) = tk >= 0 ? v[j] : u32x4{0u, 0u, 0u, 0u};
+      for (int j = 0; j < CPT; ++j) v[e][j] = ld16(src + (c + 16 * j) * VEC);
+    }
+    if (rec) {  // its reads queue behind the row loads
+#pragma unroll
+      for (int e = 0; e < NE; ++e)
+        if (b[e] >= 0) record(p, b[e], act[e], tk[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < NE; ++e)
+#pragma unroll
+      for (int j = 0; j < CPT; ++j)
+        *reinterpret_cast<u32x4*>(&xs[k + 16 * e][(c + 16 * j) * VEC]) = tk[e] >= 0 ? v[e][j] : u32x4{0u, 0u, 0u, 0u};
   } else {
-    // h of the entry's slot (zero on a stream's first step), and for the cell
+    // h of the entries' slots (zero on a stream's first step), and for the cell
     // update of unit u0 + c: its c and biases.  An entry that does not update
     // reads slot 0's finite values; its MFMA column and cell are never used.
-    slot = slot_k;
-    const ST* src = (const ST*)p.h + ((int64_t)slot * L + layer) * H;
 #pragma unroll
-    for (int j = 0; j < CPT; ++j) v[j] = ld16(src + (c + 16 * j) * VEC);
+    for (int e = 0; e < NE; ++e) {
+      const ST* src = (const ST*)p.h + ((int64_t)slot[e] * L + layer) * H;
+#pragma unroll
+      for (int j = 0; j < CPT; ++j) v[e][j] = ld16(src + (c + 16 * j) * VEC);
+    }
     const int64_t bo = (int64_t)layer * 4 * H + u0 + c;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       cb[q] = from_st(((const ST*)p.b_ih)[bo + q * H]);
       cb[4 + q] = from_st(((const ST*)p.b_hh)[bo + q * H]);
     }
-    cb[8] = from_st(((const ST*)p.c)[((int64_t)slot * L + layer) * H + u0 + c]);
 #pragma unroll
-    for (int j = 0; j < CPT; ++j)
-      *reinterpret_cast<u32x4*>(&hs[k][(c + 16 * j) * VEC]) = p.prime ? u32x4{0u, 0u, 0u, 0u} : v[j];
+    for (int e = 0; e < NE; ++e) c0[e] = from_st(((const ST*)p.c)[((int64_t)slot[e] * L + layer) * H + u0 + c]);
+#pragma unroll
+    for (int e = 0; e < NE; ++e)
+#pragma unroll
+      for (int j = 0; j < CPT; ++j)
+        *reinterpret_cast<u32x4*>(&hs[k + 16 * e][(c + 16 * j) * VEC]) = p.prime ? u32x4{0u, 0u, 0u, 0u} : v[e][j];
   }
   __syncthreads();
   bool any = false;
   for (int e = 0; e < SPW; ++e) any |= tok_s[e] >= 0;
   if (!any) return;  // uniform: no stream of the tile updates
-  // gate gi rows for the 16 streams: the input part's k-steps, then the
-  // recurrent part's from those sums (its second chunk loading meanwhile);
-  // lane: units u0 + 4 lg + i, stream lr
-  if (part == 1) load_chunk<ST>(w1, wrow, wrow, ks, ks, KChunk<ST>::CH, lg);
+  // gate gi rows for the streams, 16 a column tile: the input part's k-steps,
+  // then the recurrent part's from those sums (its second chunk loading
+  // meanwhile); lane: units u0 + 4 lg + i, stream 16 ct + lr
+  if (part == 1) load_chunk<ST>(w1, wrow, wrow, ks, ks, CH, lg);
   if (part == 0) {
-    const f32x4_t d = mma_rows2<ST>(w0, w1, wrow, wrow, ks, ks, &xs[lr][0], lg, f32x4_t{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-    for (int i = 0; i < 4; ++i) gsm[gi][lr][4 * lg + i] = d[i];
+    for (int ct = 0; ct < NE; ++ct) {
+      const f32x4_t d =
+          mma_rows2<ST>(w0, w1, wrow, wrow, ks, ks, &xs[16 * ct + lr][0], lg, f32x4_t{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+      for (int i = 0; i < 4; ++i) gsm[gi][16 * ct + lr][4 * lg + i] = d[i];
+    }
   }
   __syncthreads();
   if (part == 1) {
-    f32x4_t d;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) d[i] = gsm[gi][lr][4 * lg + i];
-    d = mma_rows2<ST>(w0, w1, wrow, wrow, ks, ks, &hs[lr][0], lg, d);
+    for (int ct = 0; ct < NE; ++ct) {
+      f32x4_t d;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) gsm[gi][lr][4 * lg + i] = d[i];
+      for (int i = 0; i < 4; ++i) d[i] = gsm[gi][16 * ct + lr][4 * lg + i];
+      d = mma_rows2<ST>(w0, w1, wrow, wrow, ks, ks, &hs[16 * ct + lr][0], lg, d);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) gsm[gi][16 * ct + lr][4 * lg + i] = d[i];
+    }
   }
   __syncthreads();
-  // cell update: recurrent-part thread -> (stream entry k, unit u0 + c)
-  if (part == 1 && tok_s[k] >= 0) {  // a stream that updates has a valid slot
-    float g4[4];
+  // cell update: recurrent-part thread -> (stream entries k + 16 e, unit u0 + c)
+  if (part == 1) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) g4[q] = gsm[q][k][c] + cb[q] + cb[4 + q];
-    const float ig = 1.f / (1.f + __expf(-g4[0])), fg = 1.f / (1.f + __expf(-g4[1]));
-    const float gg = tanhf(g4[2]), og = 1.f / (1.f + __expf(-g4[3]));
-    const float c0 = p.prime ? 0.f : cb[8];
-    // one rounding order whatever the surrounding code: the input gate's
-    // product fused, the forget gate's rounded first
-    const float c1 = fmaf(ig, gg, fg * c0);
-    ((ST*)p.c)[((int64_t)slot * L + layer) * H + u0 + c] = to_st<ST>(c1);
-    ((ST*)p.hn)[((int64_t)b * L + layer) * H + u0 + c] = to_st<ST>(og * tanhf(c1));
+    for (int e = 0; e < NE; ++e) {
+      const int ke = k + 16 * e;
+      if (tok_s[ke] < 0) continue;  // a stream that updates has a valid slot
+      float g4[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) g4[q] = gsm[q][ke][c] + cb[q] + cb[4 + q];
+      const float ig = 1.f / (1.f + __expf(-g4[0])), fg = 1.f / (1.f + __expf(-g4[1]));
+      const float gg = tanhf(g4[2]), og = 1.f / (1.f + __expf(-g4[3]));
+      const float cp = p.prime ? 0.f : c0[e];
+      // one rounding order whatever the surrounding code: the input gate's
+      // product fused, the forget gate's rounded first
+      const float c1 = fmaf(ig, gg, fg * cp);
+      ((ST*)p.c)[((int64_t)slot[e] * L + layer) * H + u0 + c] = to_st<ST>(c1);
+      ((ST*)p.hn)[((int64_t)b[e] * L + layer) * H + u0 + c] = to_st<ST>(og * tanhf(c1));
+    }
   }
 }
 
@@ -705,12 +773,26 @@ static int run_step(const pk_rnnt_args* a, hipStream_t st) {
   k.h = a->h;
   k.prime = a->prime;
   const dim3 gj(k.vtiles, (a->batch + 15) / 16);
-  const dim3 gl(a->hidden / 16, (a->batch + LstmCfg<ST>::SPW - 1) / LstmCfg<ST>::SPW);
+  // 32 streams a LSTM workgroup when every stream may update (a frame's first
+  // symbol, or priming) and that leaves no CU with two workgroups, else 16: at
+  // later symbols the smaller tiles more often have no update and return early
+  // (16-bit types only: the fp32 rows of 32 streams do not fit in LDS)
+  const int cus = cu_count();
+  const bool wide_fits = sizeof(ST) == 2 && !k.compact &&
+                         (int64_t)(a->hidden / 16) * ((a->batch + 15) / 16) > cus &&
+                         (int64_t)(a->hidden / 16) * ((a->batch + 31) / 32) <= cus;
+  const dim3 gl16(a->hidden / 16, (a->batch + 15) / 16), gl32(a->hidden / 16, (a->batch + 31) / 32);
   const dim3 gp((a->joint + 16 * kPredWaves - 1) / (16 * kPredWaves), (a->batch + 15) / 16);
   auto lstm = [&]() {
     for (int l = 0; l < a->layers; ++l) {
       k.layer = l;
-      hipLaunchKernelGGL(lstm_kernel<ST>, gl, dim3(LstmCfg<ST>::WAVES * 64), 0, st, k);
+      if constexpr (sizeof(ST) == 2) {
+        if (wide_fits && (k.prime || k.s == 0)) {
+          hipLaunchKernelGGL((lstm_kernel<ST, 32>), gl32, dim3(LstmCfg<ST, 32>::WAVES * 64), 0, st, k);
+          continue;
+        }
+      }
+      hipLaunchKernelGGL((lstm_kernel<ST, 16>), gl16, dim3(LstmCfg<ST, 16>::WAVES * 64), 0, st, k);
     }
   };
   auto pred = [&]() { hipLaunchKernelGGL(pred_kernel<ST>, gp, dim3(kPredWaves * 64), 0, st, k); };
