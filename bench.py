@@ -95,6 +95,8 @@ def churn_step(runner, churn, events=None, graph=False) -> int:
 TRAFFIC_SUMMARY = {
     "large": os.path.join(HERE, "profiles", "relpos_attn_large_bf16_230streams_hbm_counters.md"),
     "large-t14": os.path.join(HERE, "profiles", "relpos_attn_chunk_large_bf16_t14_230streams.md"),
+    "small": os.path.join(HERE, "profiles", "relpos_attn_small_fp16_64streams.md"),
+    "frag": os.path.join(HERE, "profiles", "relpos_attn_frag_fp16_1024streams.md"),
 }
 
 
@@ -840,7 +842,7 @@ def paged_bench(config_name: str, device, args, steps: int, warmup: int, event_s
         },
         "wall_s": round(wall, 3),
     }
-    achieved = total_bytes / (kern_ms * 1e-3) / 1e9
+    achieved = total_bytes / (kern_ms * 1e-3) / 1e9 if kern_ms > 0 else 0.0  # 0: no launch was event-timed
     traffic = measured_traffic(config_name, ev_B) if args.rows_per_lane == 0 else None
     roof = {
         "bound": "hbm",
@@ -856,7 +858,7 @@ def paged_bench(config_name: str, device, args, steps: int, warmup: int, event_s
         "bytes_shared_per_launch": shared,
         "bytes_per_launch": int(round(total_bytes / n_launch)),
     }
-    if traffic:
+    if traffic and avg_us > 0:
         # the same launch time over the bytes the HBM counters read
         roof["frac_counter_bytes"] = round(traffic / (avg_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
     if probes and not args.no_copy_ceiling:
