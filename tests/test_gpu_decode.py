@@ -123,29 +123,30 @@ def test_streams_are_independent_of_the_batch(cuda):
         assert torch.equal(b.h[[2, 4, 6]], before)
 
 
-@pytest.mark.parametrize("dt,layers", [(torch.float16, 1), (torch.bfloat16, 2)])
-def test_wide_lstm_tiles_match_narrow(cuda, dt, layers):
-    """128 streams in one batch take the LSTM launches of 32 streams a workgroup at a
-    frame's first symbol (their 16-stream tiles would leave CUs with two
-    workgroups); the same streams as two batches of 64 take 16-stream workgroups
-    throughout.  Tokens and state agree bit for bit.  The joint's encoder
-    projection is the identity, so the enc GEMM gives the same bits whatever
-    kernel each batch size picks."""
+@pytest.mark.parametrize("dt,layers,n", [(torch.float16, 1, 128), (torch.bfloat16, 2, 128), (torch.bfloat16, 2, 150)])
+def test_wide_lstm_tiles_match_narrow(cuda, dt, layers, n):
+    """n streams in one batch (128; 150, whose last 32-stream tile is partial) take
+    the LSTM launches of 32 streams a workgroup at a frame's first symbol (their
+    16-stream tiles would leave CUs with two workgroups); the same streams as two
+    half batches take 16-stream workgroups throughout.  Tokens and state agree bit
+    for bit.  The joint's encoder projection is the identity, so the enc GEMM
+    gives the same bits whatever kernel each batch size picks."""
     pred, joint, _ = _model(1024, 640, layers, dt, cuda, seed=11, blank_bias=2.5)
     with torch.no_grad():
         joint.enc.weight.copy_(torch.eye(640, dtype=dt))
         joint.enc.bias.zero_()
-    a = GreedyDecoder(pred, joint, blank_id=1024, num_slots=128)
-    b = GreedyDecoder(pred, joint, blank_id=1024, num_slots=128)
-    a.reset_slot(range(128))
-    b.reset_slot(range(128))
+    a = GreedyDecoder(pred, joint, blank_id=1024, num_slots=n)
+    b = GreedyDecoder(pred, joint, blank_id=1024, num_slots=n)
+    a.reset_slot(range(n))
+    b.reset_slot(range(n))
     g = torch.Generator().manual_seed(13)
+    h = n // 2
     n_tok = 0
     for step in range(3):
-        enc = (0.5 * torch.randn(128, 4, 640, generator=g)).to(dt).to(cuda)
-        lengths = np.array([4 - (i % 3 == 0) for i in range(128)])
-        ta = a.decode(np.arange(128), enc, lengths)
-        tb = list(b.decode(np.arange(64), enc[:64], lengths[:64])) + list(b.decode(np.arange(64, 128), enc[64:], lengths[64:]))
+        enc = (0.5 * torch.randn(n, 4, 640, generator=g)).to(dt).to(cuda)
+        lengths = np.array([4 - (i % 3 == 0) for i in range(n)])
+        ta = a.decode(np.arange(n), enc, lengths)
+        tb = list(b.decode(np.arange(h), enc[:h], lengths[:h])) + list(b.decode(np.arange(h, n), enc[h:], lengths[h:]))
         assert [list(x) for x in ta] == [list(x) for x in tb], f"step {step}"
         assert torch.equal(a.h, b.h) and torch.equal(a.c, b.c) and torch.equal(a.pred_proj, b.pred_proj)
         n_tok += sum(len(x) for x in ta)
