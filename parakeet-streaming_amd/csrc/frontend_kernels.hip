@@ -306,10 +306,29 @@ __global__ void __launch_bounds__(64 * kFeWaves) fe_kernel(const FeK p) {
     wave_lds_sync();
     float* mrow = p.mel + ((int64_t)s.slot * p.mel_rows + (f & (p.mel_rows - 1))) * p.n_mels;
     for (int m = lane; m < p.n_mels; m += 64) {
-      const int lo = rng_s[m].x, hi = rng_s[m].y;
+      const int lo = rng_s[m].x, hi = rng_s[m].y, mid = min(hi, lo + kBand);
+      // the band's first kBand weights from LDS, the rest (wider bands) from
+      // global memory: two loops, so the LDS one reads through LDS
+      // instructions (one select between the two spaces made every read a
+      // generic load that waited for memory); the sum runs over the bins in
+      // order either way; four bins' reads are issued before their sums
+      const float* const wl = &fbw[m][0];
+      const float* const pl = pwv + lo;
+      const int nl = mid - lo;
       float acc = 0.f;
-      for (int kk = lo; kk < hi; ++kk)
-        acc += (kk - lo < kBand ? fbw[m][kk - lo] : p.fb[(int64_t)m * kBins + kk]) * pwv[kk];
+      int j = 0;
+      for (; j + 4 <= nl; j += 4) {
+        float w[4], q[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          w[e] = wl[j + e];
+          q[e] = pl[j + e];
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc += w[e] * q[e];
+      }
+      for (; j < nl; ++j) acc += wl[j] * pl[j];
+      for (int kk = mid; kk < hi; ++kk) acc += p.fb[(int64_t)m * kBins + kk] * pwv[kk];
       mrow[m] = logf(acc + p.guard);
     }
     wave_lds_sync();  // this frame's reads of bw and pwv before the next frame's writes
