@@ -433,8 +433,9 @@ __global__ void __launch_bounds__(256) select_kernel(const DecK p) {
 }
 
 // ---------------------------------------------------------------------------
-// SPW streams per workgroup (16 or 32; the host takes 32 when that keeps every
-// workgroup on a CU of its own), 8 waves: 4 gates x {input part, recurrent part}.
+// SPW streams per workgroup (16 or 32; the host takes 32 when every stream may
+// update and that keeps every workgroup on a CU of its own), 8 waves: 4 gates x
+// {input part, recurrent part}.
 template <typename ST, int SPW>
 struct LstmCfg {
   static constexpr int WAVES = 8;
