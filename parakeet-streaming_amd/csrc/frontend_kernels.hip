@@ -293,16 +293,23 @@ __global__ void __launch_bounds__(64 * kFeWaves) fe_kernel(const FeK p) {
         for (int r = 0; r < 4; ++r) v[r] = bw[lane + 64 * r];
       }
     }
-    // real-input bins: X[k] = E[k] + W^k O[k], E/O from Z[k] and conj(Z[256-k])
+    // real-input bins: X[k] = E[k] + W^k O[k], E/O from Z[k] and conj(Z[256-k]);
+    // bins lane + 64 r in one unrolled pass, the Nyquist bin 256 by lane 0.
+    // The products are fused as written (one rounding order whatever the
+    // surrounding code)
     float* pwv = pw[wave];
-    for (int kk = lane; kk < kBins; kk += 64) {
+    auto bin = [&](int kk) {
+#pragma clang fp contract(off)
       const float2 zk = bw[kk & (kCplx - 1)], zm = bw[(kCplx - kk) & (kCplx - 1)];
       const float er = 0.5f * (zk.x + zm.x), ei = 0.5f * (zk.y - zm.y);
       const float orr = 0.5f * (zk.y + zm.y), oi = -0.5f * (zk.x - zm.x);
       const float2 w = tw2[kk];
-      const float xr = er + (w.x * orr - w.y * oi), xi = ei + (w.x * oi + w.y * orr);
-      pwv[kk] = xr * xr + xi * xi;
-    }
+      const float xr = er + fmaf(w.x, orr, -(w.y * oi)), xi = ei + fmaf(w.x, oi, w.y * orr);
+      pwv[kk] = fmaf(xr, xr, xi * xi);
+    };
+#pragma unroll
+    for (int r = 0; r < kCplx / 64; ++r) bin(lane + 64 * r);
+    if (lane == 0) bin(kCplx);
     wave_lds_sync();
     float* mrow = p.mel + ((int64_t)s.slot * p.mel_rows + (f & (p.mel_rows - 1))) * p.n_mels;
     for (int m = lane; m < p.n_mels; m += 64) {
