@@ -338,26 +338,30 @@ __global__ void __launch_bounds__(kJointWaves * 64) joint_kernel(const DecK p) {
 // ---------------------------------------------------------------------------
 // Stream b's decision at (t, s): the first maximum over the vocabulary tiles'
 // partial maxima; -1 when the stream is not deciding or decides blank.  Taken
-// by the 16 lanes c = 0 .. 15 of an aligned lane group, every lane with the
-// same b (every lane gets the result): lane c reads tiles c, c + 16, ... and
+// by the N lanes c = 0 .. N - 1 of an aligned lane group, every lane with the
+// same b (every lane gets the result): lane c reads tiles c, c + N, ... and
 // the lanes combine.  The (value, index) pairs are ordered by value, then by
 // the lower index, a total order over the pairs the joint writes (never NaN),
 // so any combining order gives the sequential scan's first maximum.  The
 // stream words and the first 64 tiles are loaded in one round.
 // Workspace words: 0 = blank seen in the current frame, 1 = token that updates
 // the predictor this iteration (-1: none), 2 = tokens emitted this step.
-// The loads of a decision: the stream words and the lane's first 4 tiles (the
-// first 64 tiles of the group), issued together.
+// The loads of a decision taken by N lanes (N = 4 or 16): the stream words and
+// the lane's first 64 / N tiles (the first 64 tiles of the group), issued
+// together.
+template <int N>
 struct DecideLoads {
   StreamWords sw;
-  int2 m[4];
+  int2 m[64 / N];
 };
-__device__ static inline DecideLoads decide_load(const DecK& p, int b, int c) {
+template <int N>
+__device__ static inline DecideLoads<N> decide_load(const DecK& p, int b, int c) {
   const int32_t* ws = ws_of(p, b);
-  DecideLoads d;
+  DecideLoads<N> d;
   d.sw = stream_words(p, b);
 #pragma unroll
-  for (int u = 0; u < 4; ++u) d.m[u] = *reinterpret_cast<const int2*>(ws + kWsHead + 2 * min(c + 16 * u, p.vtiles - 1));
+  for (int u = 0; u < 64 / N; ++u)
+    d.m[u] = *reinterpret_cast<const int2*>(ws + kWsHead + 2 * min(c + N * u, p.vtiles - 1));
   return d;
 }
 __device__ static inline void decide_take(float ov, int oi, float& v, int& ix) {
@@ -366,14 +370,15 @@ __device__ static inline void decide_take(float ov, int oi, float& v, int& ix) {
     ix = oi;
   }
 }
-__device__ static inline int decide_finish(const DecK& p, int b, int c, const DecideLoads& d, bool* act_out) {
+template <int N>
+__device__ static inline int decide_finish(const DecK& p, int b, int c, const DecideLoads<N>& d, bool* act_out) {
   float v = -INFINITY;
   int ix = 0x7fffffff;
 #pragma unroll
-  for (int u = 0; u < 4; ++u)
-    if (c + 16 * u < p.vtiles) decide_take(__int_as_float(d.m[u].x), d.m[u].y, v, ix);
+  for (int u = 0; u < 64 / N; ++u)
+    if (c + N * u < p.vtiles) decide_take(__int_as_float(d.m[u].x), d.m[u].y, v, ix);
   const int32_t* ws = ws_of(p, b);
-  for (int k0 = 64; k0 < p.vtiles; k0 += 16) {  // tiles past the first 64 (vocabularies past 4,096 rows)
+  for (int k0 = 64; k0 < p.vtiles; k0 += N) {  // tiles past the first 64 (vocabularies past 4,096 rows)
     const int t = k0 + c;
     if (t < p.vtiles) {
       const int2 m = *reinterpret_cast<const int2*>(ws + kWsHead + 2 * t);
@@ -381,14 +386,11 @@ __device__ static inline int decide_finish(const DecK& p, int b, int c, const De
     }
   }
 #pragma unroll
-  for (int m = 1; m < 16; m <<= 1) decide_take(__shfl_xor(v, m), __shfl_xor(ix, m), v, ix);
+  for (int m = 1; m < N; m <<= 1) decide_take(__shfl_xor(v, m), __shfl_xor(ix, m), v, ix);
   const bool act = active_from(p, d.sw);
   *act_out = act;
   if (!act) return -1;
   return (ix == p.blank || ix < 0 || ix >= p.V1) ? -1 : ix;
-}
-__device__ static inline int decide16(const DecK& p, int b, int c, bool* act_out) {
-  return decide_finish(p, b, c, decide_load(p, b, c), act_out);
 }
 
 // The record of stream b's decision (one writer per stream).  Other
@@ -419,10 +421,10 @@ __device__ static inline void record(const DecK& p, int b, bool act, int tok) {
 // the order of the atomic appends; every later launch treats each stream on
 // its own, so the order does not change any result).
 __global__ void __launch_bounds__(256) select_kernel(const DecK p) {
-  const int c = threadIdx.x & 15, b = blockIdx.x * 16 + (threadIdx.x >> 4);  // 16 lanes a stream
+  const int c = threadIdx.x & 3, b = blockIdx.x * 64 + (threadIdx.x >> 2);  // 4 lanes a stream
   if (b >= p.batch) return;  // uniform per lane group
   bool act;
-  const int tk = decide16(p, b, c, &act);
+  const int tk = decide_finish<4>(p, b, c, decide_load<4>(p, b, c), &act);
   if (c != 0) return;
   record(p, b, act, tk);
   if (tk >= 0) {
@@ -478,12 +480,12 @@ __global__ void __launch_bounds__(512) lstm_kernel(const DecK p) {  // LstmCfg::
   const bool deciding = layer == 0 && !p.compact && !p.prime;
   int tk[NE];
   bool act[NE];
-  DecideLoads dl[NE];
+  DecideLoads<16> dl[NE];
 #pragma unroll
   for (int e = 0; e < NE; ++e) {
     tk[e] = -1;
     act[e] = false;
-    if (deciding && part == 0) dl[e] = decide_load(p, min(b0 + k + 16 * e, p.batch - 1), c);
+    if (deciding && part == 0) dl[e] = decide_load<16>(p, min(b0 + k + 16 * e, p.batch - 1), c);
   }
   // lane c of every 16-lane group reads whether entries c + 16 e may update
   // (deciding: they are active), so each wave holds all entries: a tile with
@@ -520,7 +522,7 @@ __global__ void __launch_bounds__(512) lstm_kernel(const DecK p) {  // LstmCfg::
   if (deciding && part == 0) {
 #pragma unroll
     for (int e = 0; e < NE; ++e)
-      if (b[e] >= 0) tk[e] = decide_finish(p, b[e], c, dl[e], &act[e]);
+      if (b[e] >= 0) tk[e] = decide_finish<16>(p, b[e], c, dl[e], &act[e]);
   }
   const bool rec = deciding && part == 0 && blockIdx.x == 0 && c == 0;
   if (__ballot(may) == 0) {
@@ -805,7 +807,7 @@ static int run_step(const pk_rnnt_args* a, hipStream_t st) {
         k.s = s;
         k.it = t * a->max_symbols + s;
         hipLaunchKernelGGL(joint_kernel<ST>, gj, dim3(kJointWaves * 64), 0, st, k);
-        if (k.compact) hipLaunchKernelGGL(select_kernel, dim3((a->batch + 15) / 16), dim3(256), 0, st, k);
+        if (k.compact) hipLaunchKernelGGL(select_kernel, dim3((a->batch + 63) / 64), dim3(256), 0, st, k);
         lstm();
         pred();
       }
