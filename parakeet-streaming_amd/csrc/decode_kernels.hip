@@ -435,9 +435,9 @@ __global__ void __launch_bounds__(256) select_kernel(const DecK p) {
 }
 
 // ---------------------------------------------------------------------------
-// SPW streams per workgroup (16 or 32; the host takes 32 when every stream may
-// update and that keeps every workgroup on a CU of its own), 8 waves: 4 gates x
-// {input part, recurrent part}.
+// SPW streams per workgroup (16 or 32; the host takes 32 in compact mode, and
+// when every stream may update and that keeps every workgroup on a CU of its
+// own), 8 waves: 4 gates x {input part, recurrent part}.
 template <typename ST, int SPW>
 struct LstmCfg {
   static constexpr int WAVES = 8;
@@ -776,10 +776,12 @@ static int run_step(const pk_rnnt_args* a, hipStream_t st) {
   k.h = a->h;
   k.prime = a->prime;
   const dim3 gj(k.vtiles, (a->batch + 15) / 16);
-  // 32 streams a LSTM workgroup when every stream may update (a frame's first
-  // symbol, or priming) and that leaves no CU with two workgroups, else 16: at
-  // later symbols the smaller tiles more often have no update and return early
-  // (16-bit types only: the fp32 rows of 32 streams do not fit in LDS)
+  // 32 streams a LSTM workgroup (16-bit types only: the fp32 rows of 32 streams
+  // do not fit in LDS) in compact mode, where the tiles hold only streams that
+  // update and 32 of them read the weights half as often, and otherwise when
+  // every stream may update (a frame's first symbol, or priming) and that
+  // leaves no CU with two workgroups; else 16: at later symbols the smaller
+  // tiles more often have no update and return early
   const int cus = cu_count();
   const bool wide_fits = sizeof(ST) == 2 && !k.compact &&
                          (int64_t)(a->hidden / 16) * ((a->batch + 15) / 16) > cus &&
@@ -790,7 +792,7 @@ static int run_step(const pk_rnnt_args* a, hipStream_t st) {
     for (int l = 0; l < a->layers; ++l) {
       k.layer = l;
       if constexpr (sizeof(ST) == 2) {
-        if (wide_fits && (k.prime || k.s == 0)) {
+        if (k.compact || (wide_fits && (k.prime || k.s == 0))) {
           hipLaunchKernelGGL((lstm_kernel<ST, 32>), gl32, dim3(LstmCfg<ST, 32>::WAVES * 64), 0, st, k);
           continue;
         }
