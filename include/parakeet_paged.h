@@ -196,8 +196,10 @@ typedef struct pk_attn_args {
   void* out;
   int64_t out_stride_b;
   int64_t out_stride_t;
-  int32_t rows_per_lane; /* kernel choice: 0 = automatic; 4, 9, 12, 18 = the vector-ALU
-                            kernel with that many key rows per lane; fp16/bf16 only:
+  int32_t rows_per_lane; /* kernel choice: 0 = automatic; 4, 5, 9, 12, 18 = the vector-ALU
+                            kernel, one wave a workgroup, with that many key rows per
+                            lane (automatic fp32 splits a window over 4 waves when the
+                            grid is at most two workgroups a CU); fp16/bf16 only:
                             -1 = the two-query matrix-core kernel, -2 = the whole-chunk
                             matrix-core kernel (chunk <= 14, window <= 96; automatic for
                             chunks of 3..14 frames); fp32 ignores negative values */

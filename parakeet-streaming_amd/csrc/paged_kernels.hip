@@ -131,9 +131,10 @@ struct StreamMask {
   }
 };
 
-// One single-wave workgroup per (stream b, head h, query group of TQ queries).
-// Lane group rl (G lanes, VEC columns each) owns window rows jb + n*RLW + rl,
-// n < NR, of every tile of BLK = RLW*NR rows.  Per tile:
+// One workgroup of WAVES waves per (stream b, head h, query group of TQ
+// queries); wave w takes the tiles w, w + WAVES, ... of BLK = RLW*NR window
+// rows, and its lane group rl (G lanes, VEC columns each) the rows jb + n*RLW
+// + rl, n < NR, of each.  Per tile:
 //   1. the position rows of the tile (L2-resident, shared by all streams) are
 //      loaded in the same round trip as the stream's page header, the queries
 //      and the biases, and reduced to the (q+v).pos terms in a wave-private LDS
@@ -142,10 +143,12 @@ struct StreamMask {
 //   2. page ids come from the ring held one entry per lane (ds_bpermute), and
 //      all NR K rows and NR V rows of the lane are issued back to back;
 //   3. scores, an online softmax over the lane group's rows and the value sum.
-// The lane groups are combined with cross-lane shuffles at the end: no
-// workgroup barrier, and one wave holds the whole window of its head in flight.
-template <typename ST, int DK, int TQ, int NR>
-__global__ void __launch_bounds__(64) relpos_attn_kernel(const AttnK<ST> p) {
+// The lane groups are combined with cross-lane shuffles at the end, then
+// (WAVES > 1) the waves' states through LDS in wave order, one barrier: one
+// wave holds a whole window in flight, or WAVES waves a quarter of it each
+// (small batches, where a single wave's latency is the launch's).
+template <typename ST, int DK, int TQ, int NR, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES) relpos_attn_kernel(const AttnK<ST> p) {
   constexpr int VEC = Tr<ST>::VEC;
   constexpr int G = DK / VEC;
   static_assert(G >= 1 && 64 % G == 0, "head_dim / VEC must divide 64");
@@ -156,15 +159,18 @@ __global__ void __launch_bounds__(64) relpos_attn_kernel(const AttnK<ST> p) {
   constexpr float NEG = -1e30f;
   constexpr float MASKED = -1e5f * 1.4426950408889634f;  // -1e5 in log2 units
 
-  __shared__ float cbuf[TQ][NP * RLW];  // (q+v).pos terms of the tile
-  __shared__ uint8_t mbuf[TQ][BLK];     // mask bytes of the tile (pointer mask)
+  __shared__ float cbuf[WAVES][TQ][NP * RLW];  // (q+v).pos terms of the wave's tile
+  __shared__ uint8_t mbuf[WAVES][TQ][BLK];     // mask bytes of the wave's tile (pointer mask)
 
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wave = WAVES == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  float(*const cb)[NP * RLW] = cbuf[wave];
+  uint8_t(*const mb)[BLK] = mbuf[wave];
   const int g = lane % G;
   const int rl = lane / G;
   const int b = blockIdx.x / p.H;
   const int h = blockIdx.x - b * p.H;
-  if (p.nact && b >= *p.nact) return;  // the wave's stream is not live this step
+  if (p.nact && b >= *p.nact) return;  // the workgroup's stream is not live this step
   const int i0 = blockIdx.y * TQ;
   const int nq = min(TQ, p.T - i0);
   const int col = h * DK + g * VEC;
@@ -214,7 +220,7 @@ __global__ void __launch_bounds__(64) relpos_attn_kernel(const AttnK<ST> p) {
   const ST* kn_b = p.kn + b * p.k_sb;
   const ST* vn_b = p.vn + b * p.v_sb;
 
-  for (int tile = 0; tile < p.tiles; ++tile) {
+  for (int tile = wave; tile < p.tiles; tile += WAVES) {
     const int jb = tile * BLK;
 
     // (1) position rows rb .. rb + CROWS - 1 and mask bytes of the tile
@@ -231,7 +237,7 @@ __global__ void __launch_bounds__(64) relpos_attn_kernel(const AttnK<ST> p) {
         const int jj = x - ii * BLK;
         const int ic = min(i0 + ii, p.T - 1);
         const int jcl = min(jb + jj, p.Lk - 1);
-        mbuf[ii][jj] = p.mask[b * p.m_sb + h * p.m_sh + (int64_t)ic * p.m_st + jcl];
+        mb[ii][jj] = p.mask[b * p.m_sb + h * p.m_sh + (int64_t)ic * p.m_st + jcl];
       }
     }
     float qu[TQ][VEC];
@@ -252,7 +258,7 @@ __global__ void __launch_bounds__(64) relpos_attn_kernel(const AttnK<ST> p) {
           qv[ii][e] = x + bv[e];
         }
       }
-      // bd terms cbuf[ii][mm] = (q_ii + v) . pos[rb + mm]
+      // bd terms cb[ii][mm] = (q_ii + v) . pos[rb + mm]
 #pragma unroll
       for (int k = 0; k < NP; ++k) {
         float pf[VEC];
@@ -266,7 +272,7 @@ __global__ void __launch_bounds__(64) relpos_attn_kernel(const AttnK<ST> p) {
 #pragma unroll
           for (int e = 0; e < VEC; ++e) d = fmaf(qv[ii][e], pf[e], d);
           d = group_sum<G>(d);
-          if (g == 0) cbuf[ii][mm] = live ? d : 0.f;
+          if (g == 0) cb[ii][mm] = live ? d : 0.f;
         }
       }
     }
@@ -315,13 +321,13 @@ __global__ void __launch_bounds__(64) relpos_attn_kernel(const AttnK<ST> p) {
         ac = group_sum<G>(ac);
         if (!ok[n]) ac = 0.f;  // a key outside the stream's history reads as zeros
         bool msk = false;
-        if (mask_mode == 1) msk = mbuf[ii][n * RLW + rl] != 0;
+        if (mask_mode == 1) msk = mb[ii][n * RLW + rl] != 0;
         if (mask_mode == 2) msk = sm.masked(i0 + ii, qchunk[ii], jc);
         float sc;
         if (msk)
           sc = fmaf(ac, p.scale, MASKED);
         else
-          sc = (ac + cbuf[ii][n * RLW + rl + TQ - 1 - ii]) * p.scale;
+          sc = (ac + cb[ii][n * RLW + rl + TQ - 1 - ii]) * p.scale;
         s[ii][n] = (j < p.Lk && ii < nq) ? sc : NEG;
       }
     }
@@ -370,7 +376,7 @@ __global__ void __launch_bounds__(64) relpos_attn_kernel(const AttnK<ST> p) {
         }
       }
     }
-    wave_lds_sync();  // the next tile rewrites cbuf / mbuf
+    wave_lds_sync();  // the wave's next tile rewrites its cbuf / mbuf
   }
 
   // combine the RLW lane groups and write [b, i, h*DK + ...]
@@ -390,6 +396,39 @@ __global__ void __launch_bounds__(64) relpos_attn_kernel(const AttnK<ST> p) {
         acc[ii][e] = acc[ii][e] * c1 + a2 * c2;
       }
       m[ii] = mx;
+    }
+  }
+  if constexpr (WAVES > 1) {
+    // every lane holds its wave's state; lane group 0 of each wave stores it
+    // and wave 0 folds in waves 1 .. WAVES-1 in order (an empty wave: m = NEG,
+    // l = 0, adds nothing)
+    __shared__ float part[WAVES][TQ][2 + VEC][G];
+    if (rl == 0) {
+#pragma unroll
+      for (int ii = 0; ii < TQ; ++ii) {
+        part[wave][ii][0][g] = m[ii];
+        part[wave][ii][1][g] = l[ii];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) part[wave][ii][2 + e][g] = acc[ii][e];
+      }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    if (rl == 0) {
+#pragma unroll
+      for (int ii = 0; ii < TQ; ++ii) {
+        for (int w = 1; w < WAVES; ++w) {
+          const float m2 = part[w][ii][0][g];
+          const float l2 = part[w][ii][1][g];
+          const float mx = fmaxf(m[ii], m2);
+          const float c1 = __builtin_amdgcn_exp2f(m[ii] - mx);
+          const float c2 = __builtin_amdgcn_exp2f(m2 - mx);
+          l[ii] = l[ii] * c1 + l2 * c2;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) acc[ii][e] = acc[ii][e] * c1 + part[w][ii][2 + e][g] * c2;
+          m[ii] = mx;
+        }
+      }
     }
   }
   if (rl == 0) {
@@ -1772,38 +1811,50 @@ unsigned grid_for(int64_t total, int block) {
 
 // ---- attention dispatch
 
-template <typename ST, int DK, int TQ, int NR>
+template <typename ST, int DK, int TQ, int NR, int WAVES>
 int launch_attn_t(const pk_attn_args* a, const AttnK<ST>& k, hipStream_t s) {
   dim3 grid((unsigned)(a->batch * a->num_heads), (unsigned)((a->chunk + TQ - 1) / TQ));
-  dim3 block(64u);
+  dim3 block(64u * WAVES);
   if (a->start_event || a->stop_event) {
-    hipExtLaunchKernelGGL(relpos_attn_kernel<ST, DK, TQ, NR>, grid, block, 0u, s,
+    hipExtLaunchKernelGGL(relpos_attn_kernel<ST, DK, TQ, NR, WAVES>, grid, block, 0u, s,
                           (hipEvent_t)a->start_event, (hipEvent_t)a->stop_event, 0u, k);
   } else {
-    hipLaunchKernelGGL((relpos_attn_kernel<ST, DK, TQ, NR>), grid, block, 0, s, k);
+    hipLaunchKernelGGL((relpos_attn_kernel<ST, DK, TQ, NR, WAVES>), grid, block, 0, s, k);
   }
   return check_launch("pk_paged_relpos_attn");
 }
 
 // Rows per lane a kernel is built for.
-constexpr int kRowsPerLane[4] = {4, 9, 12, 18};
+constexpr int kRowsPerLane[5] = {4, 5, 9, 12, 18};
+// Waves a workgroup of the fp32 kernel when the window is split (small grids)
+constexpr int kSplitWaves = 4;
+
+template <typename ST, int DK, int TQ, int NR>
+int launch_attn_w(const pk_attn_args* a, const AttnK<ST>& k, int waves, hipStream_t s) {
+  if constexpr (std::is_same<ST, float>::value) {
+    if (waves == kSplitWaves) return launch_attn_t<ST, DK, TQ, NR, kSplitWaves>(a, k, s);
+  }
+  if (waves != 1) return fail(PK_ERR_UNSUPPORTED, "pk_paged_relpos_attn: %d waves a workgroup not built", waves);
+  return launch_attn_t<ST, DK, TQ, NR, 1>(a, k, s);
+}
 
 template <typename ST, int DK, int TQ>
-int launch_attn_nr(const pk_attn_args* a, const AttnK<ST>& k, int NR, hipStream_t s) {
+int launch_attn_nr(const pk_attn_args* a, const AttnK<ST>& k, int NR, int waves, hipStream_t s) {
   switch (NR) {
-    case 4: return launch_attn_t<ST, DK, TQ, 4>(a, k, s);
-    case 9: return launch_attn_t<ST, DK, TQ, 9>(a, k, s);
-    case 12: return launch_attn_t<ST, DK, TQ, 12>(a, k, s);
-    case 18: return launch_attn_t<ST, DK, TQ, 18>(a, k, s);
+    case 4: return launch_attn_w<ST, DK, TQ, 4>(a, k, waves, s);
+    case 5: return launch_attn_w<ST, DK, TQ, 5>(a, k, waves, s);
+    case 9: return launch_attn_w<ST, DK, TQ, 9>(a, k, waves, s);
+    case 12: return launch_attn_w<ST, DK, TQ, 12>(a, k, waves, s);
+    case 18: return launch_attn_w<ST, DK, TQ, 18>(a, k, waves, s);
     default: return fail(PK_ERR_UNSUPPORTED, "pk_paged_relpos_attn: rows_per_lane %d not built", NR);
   }
 }
 
 template <typename ST, int DK>
-int launch_attn_tq(const pk_attn_args* a, const AttnK<ST>& k, int TQ, int NR, hipStream_t s) {
+int launch_attn_tq(const pk_attn_args* a, const AttnK<ST>& k, int TQ, int NR, int waves, hipStream_t s) {
   switch (TQ) {
-    case 1: return launch_attn_nr<ST, DK, 1>(a, k, NR, s);
-    case 2: return launch_attn_nr<ST, DK, 2>(a, k, NR, s);
+    case 1: return launch_attn_nr<ST, DK, 1>(a, k, NR, waves, s);
+    case 2: return launch_attn_nr<ST, DK, 2>(a, k, NR, waves, s);
     default: return fail(PK_ERR_UNSUPPORTED, "pk_paged_relpos_attn: query group %d not built", TQ);
   }
 }
@@ -1811,9 +1862,11 @@ int launch_attn_tq(const pk_attn_args* a, const AttnK<ST>& k, int TQ, int NR, hi
 // Queries per workgroup: one chunk frame alone, otherwise groups of two.
 int pick_tq(int T) { return T <= 1 ? 1 : 2; }
 
-// Rows per lane NR for a window of Lk keys with rlw rows per wave load: the
-// fewest tiles, then the least padding (hint > 0 forces NR).
-void pick_tiling(int Lk, int rlw, int hint, int* NR, int* tiles) {
+// Rows per lane NR for a window of Lk keys with rlw rows per wave load and
+// `waves` waves sharing the tiles: the fewest tiles a wave, then the fewest
+// rows a lane, then the least padding (one wave: the fewest tiles, then the
+// least padding; hint > 0 forces NR).
+void pick_tiling(int Lk, int rlw, int hint, int waves, int* NR, int* tiles) {
   int best_nr = 0, best_t = 0;
   long best_score = -1;
   for (int c : kRowsPerLane) {
@@ -1821,7 +1874,8 @@ void pick_tiling(int Lk, int rlw, int hint, int* NR, int* tiles) {
     const int per_tile = rlw * c;
     const int t = (Lk + per_tile - 1) / per_tile;
     const int waste = t * per_tile - Lk;
-    const long score = (long)t * 1000000L + waste;
+    const long rounds = (t + waves - 1) / waves;
+    const long score = waves == 1 ? (long)t * 1000000L + waste : (rounds * 1000L + c) * 1000000L + waste;
     if (best_score < 0 || score < best_score) {
       best_score = score;
       best_nr = c;
@@ -2061,14 +2115,19 @@ int attn_typed(const pk_attn_args* a, hipStream_t s) {
   const int G = DK / VEC;
   const int rlw = 64 / G;
   const int TQ = pick_tq(a->chunk);
+  // fp32, automatic choice: a grid of at most two workgroups a CU splits each
+  // window over kSplitWaves waves (one wave's latency would be the launch's)
+  const int64_t wgs = (int64_t)a->batch * a->num_heads * ((a->chunk + TQ - 1) / TQ);
+  const int waves =
+      std::is_same<ST, float>::value && a->rows_per_lane == 0 && wgs <= 2 * (int64_t)cu_count() ? kSplitWaves : 1;
   int NR = 0, tiles = 0;
-  pick_tiling(Lk, rlw, a->rows_per_lane, &NR, &tiles);
+  pick_tiling(Lk, rlw, a->rows_per_lane, waves, &NR, &tiles);
   if (NR == 0)
-    return fail(PK_ERR_UNSUPPORTED, "%s: rows_per_lane %d not built (4, 9, 12, 18)", what,
+    return fail(PK_ERR_UNSUPPORTED, "%s: rows_per_lane %d not built (4, 5, 9, 12, 18)", what,
                 a->rows_per_lane);
   k.tiles = tiles;
-  if (DK == 64) return launch_attn_tq<ST, 64>(a, k, TQ, NR, s);
-  return launch_attn_tq<ST, 128>(a, k, TQ, NR, s);
+  if (DK == 64) return launch_attn_tq<ST, 64>(a, k, TQ, NR, waves, s);
+  return launch_attn_tq<ST, 128>(a, k, TQ, NR, waves, s);
 }
 
 template <typename ST>

@@ -244,8 +244,9 @@ def paged_relpos_attn(
     bias_u/bias_v: [H, dk]; mask: [B, T, L] / [B, 1|H, T, L] bool, True = masked.
     With ``mask`` None and ``mask_state`` given, the kernel evaluates the
     streaming mask from the stream state instead.
-    rows_per_lane: 0 lets the library pick the kernel; 4, 9, 12 or 18 force the
-    vector-ALU kernel with that many key rows per lane; for fp16/bf16, -1 forces
+    rows_per_lane: 0 lets the library pick the kernel; 4, 5, 9, 12 or 18 force
+    the one-wave vector-ALU kernel with that many key rows per lane (automatic
+    fp32 splits each window over 4 waves on small grids); for fp16/bf16, -1 forces
     the two-query matrix-core kernel and -2 the whole-chunk one (chunks of up to
     14 frames over windows of up to 96).
     """

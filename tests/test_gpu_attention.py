@@ -205,9 +205,26 @@ def test_long_window_multi_tile(cuda):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("nr", [4, 9, 12, 18])
+@pytest.mark.parametrize("nr", [4, 5, 9, 12, 18])
 def test_every_row_tiling(cuda, nr):
     _run(cuda, torch.bfloat16, B=2, H=8, dk=128, left=70, right=1, P=16, steps=8, rows_per_lane=nr, layers=1)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("left,mask_kind", [(9, "engine"), (70, "state"), (600, "engine"), (70, "ragged")])
+def test_fp32_split_window(cuda, left, mask_kind):
+    """fp32 at a small batch splits each window over 4 waves of a workgroup:
+    fewer tiles than waves (left 9), one tile a wave (70: 4 tiles of 20 keys)
+    and several a wave (600), each wave's softmax state folded in by wave 0."""
+    _run(cuda, torch.float32, B=2, H=8, dk=64, left=left, right=1, P=16, steps=8, mask_kind=mask_kind, layers=1)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("nr", [5, 18])
+def test_fp32_one_wave_tilings(cuda, nr):
+    """A rows_per_lane hint keeps the one-wave kernel (the form large fp32
+    batches take)."""
+    _run(cuda, torch.float32, B=3, H=8, dk=64, left=70, right=1, P=16, steps=8, rows_per_lane=nr, layers=1)
 
 
 @pytest.mark.gpu
