@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define PK_ABI_VERSION 8
+#define PK_ABI_VERSION 9
 
 enum pk_dtype { PK_DTYPE_F32 = 0, PK_DTYPE_F16 = 1, PK_DTYPE_BF16 = 2 };
 
@@ -298,6 +298,45 @@ typedef struct pk_conv_args {
   int64_t out_stride_t;
 } pk_conv_args;
 int pk_conv_step(const pk_conv_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * pk_residual_norm -- a Conformer layer's residual update and the LayerNorm that
+ * reads it, for `rows` frames of d_model channels:
+ *   residual_out = residual + alpha * branch   (alpha * branch rounded to
+ *                  `dtype` first when alpha != 1, then the sum rounded: the two
+ *                  roundings of the reference's `residual += x * 0.5`; one
+ *                  rounding of `residual += x` when alpha == 1)
+ *   norm_out     = LayerNorm(residual_out) * ln_weight + ln_bias  (biased
+ *                  variance, fp32 two-pass statistics over the channels of the
+ *                  rounded residual_out, each output rounded once)
+ * Replaces, per layer, parakeet/modules/encoder.py:61,63,68,70,74,76,78,80: the
+ * four `residual += ...` updates, the two `x * 0.5` scalings, and the LayerNorms
+ * norm_self_att, norm_conv, norm_feed_forward2 and norm_out that read them.
+ * residual, branch, residual_out, norm_out: [rows][d_model] of `dtype` with row
+ * strides in elements (channels contiguous, 16-byte aligned rows);
+ * residual_out may be residual (updated in place), norm_out may be branch; no
+ * other overlap.  ln_weight, ln_bias: [d_model].  d_model a multiple of 8
+ * (fp16/bf16) or 4 (fp32), at most 4096 (fp16/bf16) or 2048 (fp32).
+ */
+typedef struct pk_resnorm_args {
+  int32_t dtype;
+  int32_t device;
+  int32_t rows;
+  int32_t d_model;
+  float alpha;
+  float ln_eps;
+  const void* residual;
+  int64_t residual_stride;
+  const void* branch;
+  int64_t branch_stride;
+  const void* ln_weight;
+  const void* ln_bias;
+  void* residual_out;
+  int64_t residual_out_stride;
+  void* norm_out;
+  int64_t norm_out_stride;
+} pk_resnorm_args;
+int pk_residual_norm(const pk_resnorm_args* args, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Pre-encode front end: pcm -> log-mel (pk_fe_step) -> 8x convolution

@@ -7,6 +7,8 @@
 //                     next cache is written back in place
 //   conv_chunk_kernel the same step with a chunk's frames in parallel (chunks of
 //                     3 or more frames at small batches); same bits
+//   resnorm_kernel    a Conformer layer's residual update and the LayerNorm
+//                     that reads it (parakeet/modules/encoder.py:58-81)
 //
 // conv_step_kernel: one workgroup per stream.  Lane l of the workgroup owns the channels
 // [l*VEC, (l+1)*VEC) -- one 16-byte chunk, 8 fp16/bf16 or 4 fp32 channels -- so
@@ -327,6 +329,91 @@ __global__ void __launch_bounds__(64 * kConvMaxWaves) conv_chunk_kernel(const Co
   }
 }
 
+// ---------------------------------------------------------------------------
+// Residual update + LayerNorm (parakeet/modules/encoder.py:58-81): per row,
+//   r = residual + alpha * branch  (alpha * branch rounded to the storage type
+//       first when alpha != 1, then the sum rounded: `residual += x * 0.5`)
+//   n = LayerNorm(r) * w + b       (fp32 two-pass statistics of the rounded r)
+// One wave per row; lane l owns the 16-byte chunks l, l + 64, ... (NV of them)
+// and reads each before writing it, so r may overwrite residual in place.
+template <typename ST>
+struct ResNormK {
+  const ST* res;
+  int64_t res_s;
+  const ST* br;
+  int64_t br_s;
+  const ST* lnw;
+  const ST* lnb;
+  ST* rout;
+  int64_t rout_s;
+  ST* nout;
+  int64_t nout_s;
+  float alpha, eps;
+  int32_t rows, D;
+};
+
+constexpr int kResNormRows = 4;  // rows (waves) a workgroup
+
+template <typename ST, int NV>
+__global__ void __launch_bounds__(64 * kResNormRows) resnorm_kernel(const ResNormK<ST> p) {
+#pragma clang fp contract(off)
+  constexpr int VEC = Tr<ST>::VEC;
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kResNormRows + (threadIdx.x >> 6);
+  if (row >= p.rows) return;  // the whole wave: the kernel has no barrier
+  const float inv_d = 1.f / (float)p.D;
+  const bool scaled = p.alpha != 1.f;
+  u32x4 rv[NV], bv[NV], wv[NV], cv[NV];
+  bool own[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int c = (lane + 64 * v) * VEC;
+    own[v] = c < p.D;
+    const int cc = own[v] ? c : 0;  // a valid address for every lane
+    rv[v] = ld16(p.res + row * p.res_s + cc);
+    bv[v] = ld16(p.br + row * p.br_s + cc);
+    wv[v] = ld16(p.lnw + cc);
+    cv[v] = ld16(p.lnb + cc);
+  }
+  float x[NV][VEC];
+  float s = 0.f;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    float r[VEC], b[VEC];
+    Tr<ST>::unpack(rv[v], r);
+    Tr<ST>::unpack(bv[v], b);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float t = scaled ? round_to<ST>(p.alpha * b[e]) : b[e];
+      x[v][e] = round_to<ST>(r[e] + t);
+      s += own[v] ? x[v][e] : 0.f;
+    }
+  }
+  const float mean = group_sum<64>(s) * inv_d;
+  float q = 0.f;
+#pragma unroll
+  for (int v = 0; v < NV; ++v)
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float d = x[v][e] - mean;
+      q += own[v] ? d * d : 0.f;
+    }
+  const float var = group_sum<64>(q) * inv_d;
+  const float rstd = rsqrtf(var + p.eps);
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    if (!own[v]) continue;
+    const int c = (lane + 64 * v) * VEC;
+    float w[VEC], bb[VEC], z[VEC];
+    Tr<ST>::unpack(wv[v], w);
+    Tr<ST>::unpack(cv[v], bb);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) z[e] = fmaf((x[v][e] - mean) * rstd, w[e], bb[e]);
+    st16(p.rout + row * p.rout_s + c, Tr<ST>::pack(x[v]));
+    st16(p.nout + row * p.nout_s + c, Tr<ST>::pack(z));
+  }
+}
+
 namespace {
 
 // a step's conv caches (every layer's rows of the batch) above this share of
@@ -435,8 +522,74 @@ int conv_typed(const pk_conv_args* a, hipStream_t s) {
   }
 }
 
+constexpr int kResNormMaxNV = 8;  // 16-byte chunks a lane: d_model up to 512 chunks
+
+template <typename ST, int NV>
+int launch_resnorm(const ResNormK<ST>& k, hipStream_t s) {
+  const dim3 grid((unsigned)((k.rows + kResNormRows - 1) / kResNormRows)), block(64u * kResNormRows);
+  hipLaunchKernelGGL((resnorm_kernel<ST, NV>), grid, block, 0, s, k);
+  return check_launch("pk_residual_norm");
+}
+
+template <typename ST>
+int resnorm_typed(const pk_resnorm_args* a, hipStream_t s) {
+  constexpr int VEC = Tr<ST>::VEC;
+  const char* what = "pk_residual_norm";
+  if (a->rows < 0) return fail(PK_ERR_INVALID, "%s: rows %d < 0", what, a->rows);
+  if (a->d_model <= 0 || a->d_model % VEC != 0 || a->d_model > 64 * kResNormMaxNV * VEC)
+    return fail(PK_ERR_INVALID, "%s: d_model %d must be a positive multiple of %d, at most %d", what,
+                a->d_model, VEC, 64 * kResNormMaxNV * VEC);
+  if (!(a->ln_eps >= 0.f)) return fail(PK_ERR_INVALID, "%s: ln_eps must be >= 0", what);
+  if (!(a->alpha == a->alpha) || a->alpha == INFINITY || a->alpha == -INFINITY)
+    return fail(PK_ERR_INVALID, "%s: alpha must be finite", what);
+  if (a->rows == 0) return PK_OK;
+  const void* ptrs[6] = {a->residual, a->branch, a->ln_weight, a->ln_bias, a->residual_out, a->norm_out};
+  for (const void* q : ptrs) {
+    if (!q) return fail(PK_ERR_INVALID, "%s: a tensor pointer is NULL", what);
+    if (!aligned16(q)) return fail(PK_ERR_INVALID, "%s: tensors must be 16-byte aligned", what);
+  }
+  const int64_t strides[4] = {a->residual_stride, a->branch_stride, a->residual_out_stride, a->norm_out_stride};
+  for (int64_t st : strides)
+    if (st % VEC != 0 || (a->rows > 1 && st < a->d_model))
+      return fail(PK_ERR_INVALID, "%s: row strides must be multiples of %d elements, at least d_model", what, VEC);
+  ResNormK<ST> k{};
+  k.res = static_cast<const ST*>(a->residual);
+  k.res_s = a->residual_stride;
+  k.br = static_cast<const ST*>(a->branch);
+  k.br_s = a->branch_stride;
+  k.lnw = static_cast<const ST*>(a->ln_weight);
+  k.lnb = static_cast<const ST*>(a->ln_bias);
+  k.rout = static_cast<ST*>(a->residual_out);
+  k.rout_s = a->residual_out_stride;
+  k.nout = static_cast<ST*>(a->norm_out);
+  k.nout_s = a->norm_out_stride;
+  k.alpha = a->alpha;
+  k.eps = a->ln_eps;
+  k.rows = a->rows;
+  k.D = a->d_model;
+  DeviceGuard dg(a->device);
+  if (!dg.ok) return fail(PK_ERR_HIP, "%s: cannot select device %d", what, a->device);
+  const int nv = (a->d_model / VEC + 63) / 64;
+  if (nv <= 1) return launch_resnorm<ST, 1>(k, s);
+  if (nv <= 2) return launch_resnorm<ST, 2>(k, s);
+  if (nv <= 4) return launch_resnorm<ST, 4>(k, s);
+  return launch_resnorm<ST, kResNormMaxNV>(k, s);
+}
+
 }  // namespace
 }  // namespace pk
+
+extern "C" int pk_residual_norm(const pk_resnorm_args* a, void* stream) {
+  pk::clear_error();
+  if (!a) return pk::fail(PK_ERR_INVALID, "pk_residual_norm: args is NULL");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (a->dtype) {
+    case PK_DTYPE_F32: return pk::resnorm_typed<float>(a, s);
+    case PK_DTYPE_F16: return pk::resnorm_typed<_Float16>(a, s);
+    case PK_DTYPE_BF16: return pk::resnorm_typed<pk::bf16_t>(a, s);
+    default: return pk::fail(PK_ERR_INVALID, "pk_residual_norm: unknown dtype %d", a->dtype);
+  }
+}
 
 extern "C" int pk_conv_step(const pk_conv_args* a, void* stream) {
   pk::clear_error();

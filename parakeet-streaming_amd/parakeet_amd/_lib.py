@@ -15,7 +15,7 @@ from pathlib import Path
 LIB_NAME = "libparakeet_paged.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -173,6 +173,27 @@ class ConvArgs(ctypes.Structure):
     ]
 
 
+class ResNormArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", c_int32),
+        ("device", c_int32),
+        ("rows", c_int32),
+        ("d_model", c_int32),
+        ("alpha", ctypes.c_float),
+        ("ln_eps", ctypes.c_float),
+        ("residual", c_void_p),
+        ("residual_stride", c_int64),
+        ("branch", c_void_p),
+        ("branch_stride", c_int64),
+        ("ln_weight", c_void_p),
+        ("ln_bias", c_void_p),
+        ("residual_out", c_void_p),
+        ("residual_out_stride", c_int64),
+        ("norm_out", c_void_p),
+        ("norm_out_stride", c_int64),
+    ]
+
+
 class FeStream(ctypes.Structure):
     _fields_ = [
         ("slot", c_int32),
@@ -300,6 +321,7 @@ SIGNATURES = {
     "pk_paged_relpos_attn": (c_int, [POINTER(AttnArgs), c_void_p]),
     "pk_streaming_mask": (c_int, [POINTER(MaskArgs), c_void_p]),
     "pk_conv_step": (c_int, [POINTER(ConvArgs), c_void_p]),
+    "pk_residual_norm": (c_int, [POINTER(ResNormArgs), c_void_p]),
     "pk_fe_step": (c_int, [POINTER(FeArgs), c_void_p]),
     "pk_subsample": (c_int, [POINTER(SubArgs), c_void_p]),
     "pk_rnnt_workspace_bytes": (c_int64, [c_int32, c_int32, c_int32, c_int32, c_int32]),

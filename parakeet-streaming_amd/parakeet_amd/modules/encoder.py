@@ -133,14 +133,23 @@ class ConformerLayer(nn.Module):
         self.norm_out = nn.LayerNorm(hidden_size)
 
     def forward(self, x: Tensor, pos_emb: Tensor, pad_mask: Tensor, attn_mask: Tensor, cache: ModelCache):
-        residual = x
-        residual = residual + 0.5 * self.feed_forward1(self.norm_feed_forward1(residual))
-        residual = residual + self.self_attn(self.norm_self_att(residual), pos_emb, attn_mask=attn_mask, cache=cache)
-        conv_out, conv_cache = self.conv(self.norm_conv(residual), pad_mask=pad_mask, cache=cache.conv_ref(self.layer_idx))
+        # each residual update and the LayerNorm that reads it are one step
+        # (``residual_norm``); the layer's input is not modified
+        residual, h = self.residual_norm(x, self.feed_forward1(self.norm_feed_forward1(x)), self.norm_self_att, 0.5)
+        attn = self.self_attn(h, pos_emb, attn_mask=attn_mask, cache=cache)
+        residual, h = self.residual_norm(residual, attn, self.norm_conv, 1.0, in_place=True)
+        conv_out, conv_cache = self.conv(h, pad_mask=pad_mask, cache=cache.conv_ref(self.layer_idx))
         cache.update_conv_cache(self.layer_idx, conv_cache)
-        residual = residual + conv_out
-        residual = residual + 0.5 * self.feed_forward2(self.norm_feed_forward2(residual))
-        return self.norm_out(residual)
+        residual, h = self.residual_norm(residual, conv_out, self.norm_feed_forward2, 1.0, in_place=True)
+        _, out = self.residual_norm(residual, self.feed_forward2(h), self.norm_out, 0.5, in_place=True)
+        return out
+
+    @staticmethod
+    def residual_norm(residual: Tensor, branch: Tensor, norm: nn.LayerNorm, alpha: float, in_place: bool = False):
+        """``residual += alpha * branch`` and ``norm(residual)`` (encoder.py:61-80),
+        one HIP launch: returns the updated residual (``residual`` itself when
+        ``in_place``) and its norm."""
+        return ops.residual_norm(residual, branch, norm.weight, norm.bias, alpha=alpha, eps=norm.eps, in_place=in_place)
 
 
 class ConformerEncoder(nn.Module):

@@ -14,7 +14,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from ._lib import AttnArgs, ConvArgs, FeArgs, KvAppendArgs, KvGatherArgs, MaskArgs, PagedLayout, SubArgs, check, lib
+from ._lib import AttnArgs, ConvArgs, FeArgs, KvAppendArgs, KvGatherArgs, MaskArgs, PagedLayout, ResNormArgs, SubArgs, check, lib
 
 _DTYPES = {
     torch.float32: _lib.DTYPE_F32,
@@ -464,6 +464,55 @@ def conv_step(
     a.out, a.out_stride_b, a.out_stride_t = out.data_ptr(), out.stride(0), out.stride(1)
     check(lib().pk_conv_step(ctypes.byref(a), _stream(dev)), "pk_conv_step")
     return out
+
+
+def residual_norm(
+    residual: torch.Tensor,
+    branch: torch.Tensor,
+    ln_weight: torch.Tensor,
+    ln_bias: torch.Tensor,
+    *,
+    alpha: float = 1.0,
+    eps: float = 1e-5,
+    in_place: bool = False,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """A Conformer layer's residual update and the LayerNorm that reads it, in
+    one launch (parakeet/modules/encoder.py:61-80): ``r = residual + alpha *
+    branch`` (``alpha * branch`` rounded to the dtype first when alpha != 1, as
+    ``residual += x * 0.5`` rounds it) and ``LayerNorm(r)`` with ``ln_weight``,
+    ``ln_bias`` and ``eps``.  Returns ``(r, norm)``; ``r`` is ``residual``
+    itself, updated, when ``in_place``.
+
+    residual, branch: [..., D] of one dtype and shape (``residual`` contiguous
+    when ``in_place``); ln_weight, ln_bias: [D] of the same dtype."""
+    if residual.shape != branch.shape or residual.dtype != branch.dtype:
+        raise ValueError(f"residual {tuple(residual.shape)} {residual.dtype} and branch "
+                         f"{tuple(branch.shape)} {branch.dtype} must match")
+    D = int(residual.shape[-1])
+    dt = residual.dtype
+    for name, v in (("ln_weight", ln_weight), ("ln_bias", ln_bias)):
+        if tuple(v.shape) != (D,) or v.dtype != dt or not v.is_contiguous():
+            raise ValueError(f"{name} must be contiguous [{D}] of {dt}")
+    if in_place and not residual.is_contiguous():
+        raise ValueError("residual must be contiguous to be updated in place")
+    dev = _require_device(residual, branch, ln_weight, ln_bias)
+    res = residual.contiguous()
+    br = branch.contiguous()
+    rout = res if in_place else torch.empty_like(res)
+    nout = torch.empty_like(res)
+    a = ResNormArgs()
+    a.dtype = dtype_code(dt)
+    a.device = dev.index if dev.index is not None else torch.cuda.current_device()
+    a.rows = res.numel() // D if D else 0
+    a.d_model = D
+    a.alpha, a.ln_eps = float(alpha), float(eps)
+    a.residual, a.residual_stride = res.data_ptr(), D
+    a.branch, a.branch_stride = br.data_ptr(), D
+    a.ln_weight, a.ln_bias = ln_weight.data_ptr(), ln_bias.data_ptr()
+    a.residual_out, a.residual_out_stride = rout.data_ptr(), D
+    a.norm_out, a.norm_out_stride = nout.data_ptr(), D
+    check(lib().pk_residual_norm(ctypes.byref(a), _stream(dev)), "pk_residual_norm")
+    return rout, nout
 
 
 # ---------------------------------------------------------------------------

@@ -81,6 +81,14 @@ def oracle_conv(conv):
     return forward
 
 
+def torch_residual_norm(residual, branch, norm, alpha, in_place=False):
+    """encoder.py:61-80 as torch ops: ``residual += x * 0.5`` (or ``+= x``), then
+    the LayerNorm that reads it; replaces the layer's one-launch form on the CPU
+    reference."""
+    residual = residual + (branch * alpha if alpha != 1.0 else branch)
+    return residual, norm(residual)
+
+
 def oracle_attention(att, left, H):
     """Replaces ConformerAttention.forward on the CPU reference."""
 
@@ -108,6 +116,7 @@ def module_reference(enc, H):
     for layer in ref.layers:
         layer.self_attn.forward = oracle_attention(layer.self_attn, left, H)
         layer.conv.forward = oracle_conv(layer.conv)
+        layer.residual_norm = torch_residual_norm
 
     def ref_masks(current_len, cache_lengths, processed_frames, device, lengths):
         pad, att = om.create_streaming_masks(

@@ -57,6 +57,7 @@ def test_every_declared_symbol_is_exported_and_bound():
         ("pk_attn_args", _lib.AttnArgs),
         ("pk_mask_args", _lib.MaskArgs),
         ("pk_conv_args", _lib.ConvArgs),
+        ("pk_resnorm_args", _lib.ResNormArgs),
         ("pk_fe_stream", _lib.FeStream),
         ("pk_fe_args", _lib.FeArgs),
         ("pk_sub_stream", _lib.SubStream),
@@ -116,6 +117,25 @@ def test_conv_args_validated_before_launch():
     assert L.pk_conv_step(ctypes.byref(a), None) == _lib.PK_ERR_INVALID
     a.batch, a.dtype = 0, 7
     assert L.pk_conv_step(ctypes.byref(a), None) == _lib.PK_ERR_INVALID  # unknown dtype
+
+
+def test_residual_norm_args_validated_before_launch():
+    L = _lib.lib()
+    a = _lib.ResNormArgs()
+    a.dtype, a.rows, a.d_model, a.alpha, a.ln_eps = _lib.DTYPE_F16, 4, 512, 0.5, 1e-5
+    a.residual_stride = a.branch_stride = a.residual_out_stride = a.norm_out_stride = 512
+    assert L.pk_residual_norm(ctypes.byref(a), None) == _lib.PK_ERR_INVALID  # NULL tensors
+    assert "NULL" in _lib.last_error()
+    a.d_model = 500  # not a multiple of 8 channels
+    assert L.pk_residual_norm(ctypes.byref(a), None) == _lib.PK_ERR_INVALID
+    a.d_model = 8192  # past 4096 fp16 channels
+    assert L.pk_residual_norm(ctypes.byref(a), None) == _lib.PK_ERR_INVALID
+    a.d_model, a.alpha = 512, float("nan")
+    assert L.pk_residual_norm(ctypes.byref(a), None) == _lib.PK_ERR_INVALID
+    a.alpha, a.rows = 1.0, 0  # nothing to do: no pointer is read
+    assert L.pk_residual_norm(ctypes.byref(a), None) == _lib.PK_OK
+    a.dtype = 7
+    assert L.pk_residual_norm(ctypes.byref(a), None) == _lib.PK_ERR_INVALID  # unknown dtype
 
 
 def test_struct_sizes_match_the_header_alignment():

@@ -34,6 +34,7 @@ from _dense_encoder import dense_shift as _dense_shift
 from _dense_encoder import init_attention as _init_attention
 from _dense_encoder import oracle_attention as _oracle_attention
 from _dense_encoder import oracle_conv as _oracle_conv
+from _dense_encoder import torch_residual_norm
 
 
 @pytest.mark.gpu
@@ -202,6 +203,7 @@ def test_encoder_streaming_matches_dense_reference(cuda):
     for layer in ref.layers:
         layer.self_attn.forward = _oracle_attention(layer.self_attn, left, H)
         layer.conv.forward = _oracle_conv(layer.conv)
+        layer.residual_norm = torch_residual_norm
     proc = np.zeros(B, dtype=np.int64)
     cl = np.zeros(B, dtype=np.int64)
 
@@ -309,6 +311,7 @@ def test_engine_loop_with_scheduler_matches_per_stream_reference(cuda, sync_each
     for layer in ref.layers:
         layer.self_attn.forward = _oracle_attention(layer.self_attn, left, H)
         layer.conv.forward = _oracle_conv(layer.conv)
+        layer.residual_norm = torch_residual_norm
 
     def ref_masks(current_len, cache_lengths, processed_frames, device, lengths):
         pad, att = om.create_streaming_masks(
