@@ -71,6 +71,49 @@ class ConformerAttention(nn.Module):
         self.qkv = nn.Linear(hidden_size, hidden_size * 3, bias=use_bias)
         self.pos_bias_u = nn.Parameter(torch.empty(self.num_heads, self.d_k))
         self.pos_bias_v = nn.Parameter(torch.empty(self.num_heads, self.d_k))
+        # linear_pos(pos_emb), kept between steps: a streaming step's table is the
+        # same slice of the same buffer every step (attention.py:102 recomputes it)
+        self._pos_val: Tensor | None = None
+        self._pos_key = None
+        self._pos_src: Tensor | None = None
+
+    def _pos_version(self, pos_emb: Tensor):
+        """What the kept projection depends on: the table (address, shape, dtype,
+        in-place version) and linear_pos's weight and bias; None when a version
+        is not tracked (inference tensors), which disables keeping it."""
+        try:
+            parts = [pos_emb.data_ptr(), tuple(pos_emb.shape), tuple(pos_emb.stride()), pos_emb.dtype, pos_emb._version]
+            for t in (self.linear_pos.weight, self.linear_pos.bias):
+                parts += [None, None] if t is None else [t.data_ptr(), t._version]
+        except RuntimeError:
+            return None
+        return tuple(parts)
+
+    def projected_pos(self, pos_emb: Tensor) -> Tensor:
+        """linear_pos(pos_emb), recomputed only when the table or the weights
+        changed (always with gradients enabled).  A recomputation of the same
+        shape is written into the kept buffer, which a recorded step reads."""
+        if torch.is_grad_enabled():
+            return self.linear_pos(pos_emb)
+        key = self._pos_version(pos_emb)
+        if key is None:
+            return self.linear_pos(pos_emb)
+        if key != self._pos_key:
+            new = self.linear_pos(pos_emb)
+            v = self._pos_val
+            if v is not None and v.shape == new.shape and v.dtype == new.dtype and v.device == new.device:
+                v.copy_(new)
+            else:
+                self._pos_val = new
+            self._pos_key, self._pos_src = key, pos_emb
+        return self._pos_val
+
+    def refresh_projected_pos(self) -> None:
+        """Recomputes the kept projection in place if the table or the weights
+        changed since it was taken (a recorded step replays with the kept buffer)."""
+        if self._pos_src is not None and self._pos_version(self._pos_src) != self._pos_key:
+            with torch.no_grad():
+                self.projected_pos(self._pos_src)
 
     def forward(self, x: Tensor, pos_emb: Tensor, attn_mask: Tensor, cache: ModelCache = None):
         B, T = x.shape[:2]
@@ -78,7 +121,7 @@ class ConformerAttention(nn.Module):
         query, key, value = qkv.chunk(3, dim=-1)
         # [1, P, D] is one table for every stream; [B, P, D] gives each stream
         # its own (the reference broadcasts both, attention.py:102-106)
-        pos = self.linear_pos(pos_emb)
+        pos = self.projected_pos(pos_emb)
         if pos.dim() == 3 and pos.shape[0] == 1:
             pos = pos[0]
         mask = attn_mask.bool() if attn_mask is not None else None

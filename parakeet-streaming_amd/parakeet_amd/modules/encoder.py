@@ -331,6 +331,8 @@ class EncoderStepGraph:
             self.graph = graph
             return out
         self.x.copy_(x)
+        for layer in self.encoder.layers:  # the recording reads the kept position projections
+            layer.self_attn.refresh_projected_pos()
         self.graph.replay()
         return self.out
 

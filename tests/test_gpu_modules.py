@@ -241,7 +241,9 @@ def test_encoder_step_graph_matches_eager_steps(cuda, dtype):
     """EncoderStepGraph (one recorded step replayed per call) against the eager
     forward on a second state with the same weights: outputs, state counters,
     conv state and the pages of every layer agree bit for bit, step after step
-    (eviction included), with the eager path's launches between the replays."""
+    (eviction included), with the eager path's launches between the replays.
+    Halfway, every layer's linear_pos weight changes in place before a replay:
+    the replay refreshes the kept position projections it reads."""
     print(f"\n[encoder graph] 2 layers {dtype} replay vs eager", flush=True)
     from parakeet_amd.modules.encoder import EncoderStepGraph
 
@@ -264,8 +266,11 @@ def test_encoder_step_graph_matches_eager_steps(cuda, dtype):
     with torch.no_grad():
         for step in range(12):  # the window fills after 5 steps; pages are evicted from then on
             x = torch.randn(B, T, D, generator=g).to(dtype).to(cuda)
-            ref, _ = enc(x, eager, length=length)
+            if step == 6:
+                for layer in enc.layers:
+                    layer.self_attn.linear_pos.weight.mul_(1.5)
             got = graph(x)
+            ref, _ = enc(x, eager, length=length)
             assert torch.equal(got, ref), f"step {step}: max diff {(got.float() - ref.float()).abs().max():.3e}"
             assert torch.equal(replay.processed_frames, eager.processed_frames)
             assert torch.equal(replay.cache_lengths, eager.cache_lengths)
@@ -277,6 +282,32 @@ def test_encoder_step_graph_matches_eager_steps(cuda, dtype):
     assert graph.graph is not None
     assert replay.processed_frames.tolist() == [12 * T] * B
     torch.cuda.synchronize()
+
+
+@pytest.mark.gpu
+def test_kept_position_projection_follows_its_inputs(cuda):
+    """projected_pos keeps linear_pos(pos_emb) in one buffer and recomputes it
+    after an in-place change of the weights or the table; with gradients
+    enabled it keeps nothing (linear_pos stays trainable)."""
+    from parakeet_amd.modules.attention import ConformerAttention
+
+    att = ConformerAttention(layer_idx=0, num_heads=2, hidden_size=64).to(cuda)
+    pe = torch.randn(1, 9, 64, device=cuda)
+    with torch.no_grad():
+        first = att.projected_pos(pe)
+        kept = first.data_ptr()
+        assert torch.equal(first, att.linear_pos(pe))
+        before = first.clone()
+        assert att.projected_pos(pe).data_ptr() == kept  # no recomputation
+        att.linear_pos.weight.mul_(2.0)
+        again = att.projected_pos(pe)
+        assert again.data_ptr() == kept and torch.equal(again, att.linear_pos(pe))
+        assert not torch.equal(again, before)
+        pe.add_(1.0)
+        assert torch.equal(att.projected_pos(pe), att.linear_pos(pe))
+    y = att.projected_pos(pe)
+    y.float().sum().backward()
+    assert att.linear_pos.weight.grad is not None
 
 
 @pytest.mark.gpu
