@@ -541,8 +541,9 @@ __device__ static inline __amdgpu_buffer_rsrc_t rows_rsrc(const void* base, int 
                                            (int)nrows, 0x00020000);
 }
 
-// Workgroup of 4 waves: 4 / SPLIT streams of one head h and one query pair,
-// each stream's head split over SPLIT = head_dim / 64 waves of 64 columns.
+// Workgroup of NW waves (4, or 2 when a 4-wave grid would leave CUs idle):
+// NW / SPLIT streams of one head h and one query pair, each stream's head
+// split over SPLIT = head_dim / 64 waves of 64 columns.
 // Score slots are window columns: per pass, NT tiles of 16 slots hold columns
 // jb .. jb + 16*NT - 1; column j is cached history (j < left, read from the
 // pages), one of this step's frames (left <= j < left + chunk, read from the
@@ -576,10 +577,10 @@ __device__ static inline __amdgpu_buffer_rsrc_t rows_rsrc(const void* base, int 
 // Pages hold 64-byte column blocks ([page][block][page_size][32 elements]),
 // so one k-step load of a 16-slot tile reads 16 rows x 64 bytes of one block:
 // 1 KB of contiguous memory when the 16 slots share a page.
-template <typename ST, int DK, int NT, int MODE, bool MULTI, bool STREAM>
-__global__ void __launch_bounds__(256) relpos_attn_mfma_kernel(const AttnK<ST> p) {
+template <typename ST, int DK, int NT, int MODE, bool MULTI, bool STREAM, int NW>
+__global__ void __launch_bounds__(64 * NW) relpos_attn_mfma_kernel(const AttnK<ST> p) {
   constexpr int SPLIT = DK / 64;
-  constexpr int NW = 4;
+  static_assert(NW == 4 || NW == 2, "waves a workgroup");
   constexpr int SPW = NW / SPLIT;  // streams per workgroup
   constexpr int NTH = 64 * NW;
   constexpr int TQ = 2;
@@ -1886,24 +1887,40 @@ void pick_tiling(int Lk, int rlw, int hint, int waves, int* NR, int* tiles) {
   *tiles = best_t;
 }
 
-// Matrix-core path (fp16 / bf16): workgroups of 4 streams x one head x one
-// pair of queries, key tiles of 16 * kMfmaTiles rows.
+// Matrix-core path (fp16 / bf16): workgroups of NW waves = NW / (head_dim /
+// 64) streams x one head x one pair of queries, key tiles of 16 * kMfmaTiles
+// rows.
 constexpr int kMfmaTiles = 5;
 
-template <typename ST, int DK, int MODE, bool MULTI, bool STREAM>
+template <typename ST, int DK, int MODE, bool MULTI, bool STREAM, int NW>
 int launch_attn_mfma_t(const pk_attn_args* a, const AttnK<ST>& k, hipStream_t s) {
-  constexpr int SPW = 4 / (DK / 64);  // streams per workgroup
+  constexpr int SPW = NW / (DK / 64);  // streams per workgroup
   dim3 grid((unsigned)((a->batch + SPW - 1) / SPW), (unsigned)a->num_heads,
             (unsigned)((a->chunk + 1) / 2));
-  dim3 block(256u);
+  dim3 block(64u * NW);
   if (a->start_event || a->stop_event) {
-    hipExtLaunchKernelGGL(relpos_attn_mfma_kernel<ST, DK, kMfmaTiles, MODE, MULTI, STREAM>, grid, block,
+    hipExtLaunchKernelGGL(relpos_attn_mfma_kernel<ST, DK, kMfmaTiles, MODE, MULTI, STREAM, NW>, grid, block,
                           0u, s, (hipEvent_t)a->start_event, (hipEvent_t)a->stop_event, 0u, k);
   } else {
-    hipLaunchKernelGGL((relpos_attn_mfma_kernel<ST, DK, kMfmaTiles, MODE, MULTI, STREAM>), grid, block, 0,
+    hipLaunchKernelGGL((relpos_attn_mfma_kernel<ST, DK, kMfmaTiles, MODE, MULTI, STREAM, NW>), grid, block, 0,
                        s, k);
   }
   return check_launch("pk_paged_relpos_attn");
+}
+
+// 2-wave workgroups (half the streams a workgroup, twice the workgroups) when
+// the 4-wave grid has fewer workgroups than the chip has CUs: at 64 streams of
+// the small model (128 workgroups of 4 waves) 6.3-6.5 -> 5.9-6.0 us a launch;
+// with a CU's worth or more they are slower (230 streams of the large model:
+// 13.6-14.1 -> 14.7-15.0 us), and small grids never take the streaming policy
+template <typename ST, int DK, int MODE, bool MULTI, bool STREAM>
+int launch_attn_mfma_nw(const pk_attn_args* a, const AttnK<ST>& k, hipStream_t s) {
+  if constexpr (!STREAM) {
+    const int64_t wgs4 = (int64_t)((a->batch + 4 / (DK / 64) - 1) / (4 / (DK / 64))) * a->num_heads *
+                         ((a->chunk + 1) / 2);
+    if (wgs4 < cu_count()) return launch_attn_mfma_t<ST, DK, MODE, MULTI, STREAM, 2>(a, k, s);
+  }
+  return launch_attn_mfma_t<ST, DK, MODE, MULTI, STREAM, 4>(a, k, s);
 }
 
 // Page rows are read with the streaming cache policy once a step's windows
@@ -1919,8 +1936,8 @@ template <typename ST, int DK, int MODE, bool STREAM>
 int launch_attn_mfma_ms(const pk_attn_args* a, const AttnK<ST>& k, hipStream_t s) {
   // the single-pass form holds at most 16 * kMfmaTiles - 1 keys (its staged
   // position rows stop at 16 * kMfmaTiles)
-  if (k.tiles > 1 || k.Lk > 16 * kMfmaTiles - 1) return launch_attn_mfma_t<ST, DK, MODE, true, STREAM>(a, k, s);
-  return launch_attn_mfma_t<ST, DK, MODE, false, STREAM>(a, k, s);
+  if (k.tiles > 1 || k.Lk > 16 * kMfmaTiles - 1) return launch_attn_mfma_nw<ST, DK, MODE, true, STREAM>(a, k, s);
+  return launch_attn_mfma_nw<ST, DK, MODE, false, STREAM>(a, k, s);
 }
 
 template <typename ST, int DK, int MODE>
