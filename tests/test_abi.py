@@ -213,3 +213,9 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     # host tensors are refused before the library is even looked up
     with pytest.raises(RuntimeError, match="no CPU implementation|missing"):
         ops.streaming_mask(torch.zeros(2, dtype=torch.int64), torch.zeros(2, dtype=torch.int64), 2, chunk=2, left=70, chunk_size=2)
+    x = torch.zeros(2, 8, dtype=torch.float16)
+    w = torch.ones(8, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="no CPU implementation"):
+        ops.residual_norm(x, x, w, w, alpha=0.5)
+    with pytest.raises(ValueError, match="must match"):
+        ops.residual_norm(x, x[:, :4], w, w)
